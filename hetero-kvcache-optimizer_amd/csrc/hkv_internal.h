@@ -1,0 +1,119 @@
+// Internal helpers shared by the libheterokv HIP sources (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "../../include/heterokv.h"
+
+namespace hkv {
+
+// ---------------------------------------------------------------- errors
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define HKV_REQUIRE(cond, code, ...)            \
+    do {                                        \
+        if (!(cond)) {                          \
+            ::hkv::set_error(__VA_ARGS__);      \
+            return (code);                      \
+        }                                       \
+    } while (0)
+
+#define HKV_HIP_CHECK(expr)                                                        \
+    do {                                                                           \
+        hipError_t _e = (expr);                                                    \
+        if (_e != hipSuccess) {                                                    \
+            ::hkv::set_error("%s failed: %s", #expr, hipGetErrorString(_e));       \
+            return HKV_ERR_HIP;                                                    \
+        }                                                                          \
+    } while (0)
+
+// Launch-error check after a kernel launch.
+#define HKV_LAUNCH_CHECK(name)                                                     \
+    do {                                                                           \
+        hipError_t _e = hipGetLastError();                                         \
+        if (_e != hipSuccess) {                                                    \
+            ::hkv::set_error("launch of %s failed: %s", name, hipGetErrorString(_e)); \
+            return HKV_ERR_HIP;                                                    \
+        }                                                                          \
+    } while (0)
+
+constexpr int kHeadDim = 128;
+constexpr int kBlockTokens = 16;
+constexpr int kCodeRowBytes = kHeadDim / 2;          // 64 B of packed codes per token row
+constexpr int kHeadCodeBytes = kBlockTokens * kCodeRowBytes;  // 1024 B per (block, head)
+
+// Block record offsets (bytes) for H kv heads; see heterokv.h.
+struct RecordLayout {
+    int64_t kc, vc, ks, vs, kz, vz, bytes;
+    __host__ __device__ explicit RecordLayout(int H)
+        : kc(0),
+          vc((int64_t)H * 1024),
+          ks((int64_t)H * 2048),
+          vs((int64_t)H * 2048 + (int64_t)H * 64),
+          kz((int64_t)H * 2048 + (int64_t)H * 128),
+          vz((int64_t)H * 2048 + (int64_t)H * 144),
+          bytes((int64_t)H * 2208) {}
+};
+
+// ---------------------------------------------------------------- numeric helpers
+__device__ __forceinline__ float h2f(uint16_t b) {
+    return __half2float(__ushort_as_half(b));
+}
+__device__ __forceinline__ uint16_t f2h_rn(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+__device__ __forceinline__ float bf2f(uint16_t b) {
+    return __uint_as_float(((uint32_t)b) << 16);
+}
+// float -> bfloat16, round to nearest even (NaN stays NaN), as c10::BFloat16.
+__device__ __forceinline__ uint16_t f2bf_rn(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    uint32_t bias = 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)((u + bias) >> 16);
+}
+
+__device__ __forceinline__ float load_as_float(const void* p, int dtype, int64_t i) {
+    if (dtype == HKV_DTYPE_F16) return h2f(((const uint16_t*)p)[i]);
+    if (dtype == HKV_DTYPE_BF16) return bf2f(((const uint16_t*)p)[i]);
+    return ((const float*)p)[i];
+}
+
+// Group quantization parameters, bit-exact with kv_compressor.py:76-84 (float32 math,
+// IEEE division, clamp(min=1e-8) that keeps NaN, round half to even).
+struct QParams {
+    float scale;
+    float zpf;
+    uint8_t zp;
+};
+
+__device__ __forceinline__ QParams qparams_from_minmax(float mn, float mx) {
+    QParams q;
+    float s = (mx - mn) / 15.0f;
+    s = (s < 1e-8f) ? 1e-8f : s;          // torch.clamp(min=1e-8): NaN propagates
+    float z = rintf(-mn / s);
+    z = fminf(fmaxf(z, 0.0f), 15.0f);
+    q.scale = s;
+    q.zpf = z;
+    q.zp = (uint8_t)z;
+    return q;
+}
+
+// kv_compressor.py:86-88: clamp(round(x / scale + zp), 0, 15)
+__device__ __forceinline__ uint32_t quant_code(float x, const QParams& q) {
+    float t = x / q.scale;
+    t = t + q.zpf;
+    t = rintf(t);
+    t = fminf(fmaxf(t, 0.0f), 15.0f);
+    return (uint32_t)t;
+}
+
+// Position of logical code k (0..7) inside a packed 32-bit word.
+__host__ __device__ constexpr int nib_shift(int k) { return (k & 1) * 16 + (k >> 1) * 4; }
+
+}  // namespace hkv

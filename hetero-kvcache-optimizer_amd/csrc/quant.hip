@@ -1,0 +1,436 @@
+// INT4 asymmetric group quantizer: the reference-layout compress/decompress
+// (kv_compressor.py:50-132) and the quantize+pack kernel that appends tokens to
+// the INT4 block pool.
+#include "hkv_internal.h"
+
+#include <math.h>
+
+namespace hkv {
+namespace {
+
+// --------------------------------------------------------------------------
+// Reference layout: one wavefront per group of `G` flattened elements; the last
+// group is zero-padded (kv_compressor.py:70-74), so padding takes part in min/max.
+__global__ __launch_bounds__(256) void quantize_groups_kernel(
+    const void* __restrict__ x, int dtype, int64_t n, int G, int64_t ngroups,
+    uint8_t* __restrict__ codes, float* __restrict__ scales, uint8_t* __restrict__ zps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+    for (int64_t g = wave; g < ngroups; g += nwaves) {
+        const int64_t base = g * (int64_t)G;
+        float mn = INFINITY, mx = -INFINITY;
+        for (int i = lane; i < G; i += 64) {
+            const int64_t idx = base + i;
+            const float v = idx < n ? load_as_float(x, dtype, idx) : 0.0f;
+            mn = fminf(mn, v);
+            mx = fmaxf(mx, v);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            mn = fminf(mn, __shfl_xor(mn, off));
+            mx = fmaxf(mx, __shfl_xor(mx, off));
+        }
+        const QParams q = qparams_from_minmax(mn, mx);
+        if (lane == 0) {
+            scales[g] = q.scale;
+            zps[g] = q.zp;
+        }
+        for (int i = lane; i < G; i += 64) {
+            const int64_t idx = base + i;
+            if (idx < n) codes[idx] = (uint8_t)quant_code(load_as_float(x, dtype, idx), q);
+        }
+    }
+}
+
+// kv_compressor.py:131-132: (q - zp) * scale in float32, then cast (round to nearest even).
+__global__ __launch_bounds__(256) void dequantize_groups_kernel(
+    const uint8_t* __restrict__ codes, const float* __restrict__ scales,
+    const uint8_t* __restrict__ zps, int64_t n, int G, void* __restrict__ out, int out_dtype) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int64_t g = i / G;
+        const float v = ((float)codes[i] - (float)zps[g]) * scales[g];
+        if (out_dtype == HKV_DTYPE_F16) ((uint16_t*)out)[i] = f2h_rn(v);
+        else if (out_dtype == HKV_DTYPE_BF16) ((uint16_t*)out)[i] = f2bf_rn(v);
+        else ((float*)out)[i] = v;
+    }
+}
+
+// --------------------------------------------------------------------------
+// Quantize + pack into block records.  One workgroup per (logical block, head,
+// sequence).  Phase 1: 8 lanes per token row (K rows 0..15, V rows 16..31)
+// compute min/max, scale, zp and the codes into LDS.  Phase 2: every lane
+// assembles one K word and one V word of the record.
+struct PackParams {
+    const void* k;
+    const void* v;
+    int dtype;
+    int64_t sb, sh, st;
+    int H, T;
+    const int32_t* start_pos;
+    const int32_t* bt;
+    int bt_stride;
+    uint8_t* pool;
+    int64_t pool_blocks;
+    int32_t* err;
+    int vec_ok;  // 16-byte aligned rows: use 128-bit loads
+};
+
+__device__ __forceinline__ void load16(const void* src, int dtype, int64_t off, int vec_ok,
+                                       float (&vals)[16]) {
+    const uint16_t* p = (const uint16_t*)src + off;
+    if (vec_ok) {
+        const uint4 a = *(const uint4*)p;
+        const uint4 b = *(const uint4*)(p + 8);
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint16_t lo = (uint16_t)(w[i] & 0xffffu), hi = (uint16_t)(w[i] >> 16);
+            vals[2 * i] = dtype == HKV_DTYPE_F16 ? h2f(lo) : bf2f(lo);
+            vals[2 * i + 1] = dtype == HKV_DTYPE_F16 ? h2f(hi) : bf2f(hi);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) vals[i] = dtype == HKV_DTYPE_F16 ? h2f(p[i]) : bf2f(p[i]);
+    }
+}
+
+// Phase 2 of both packers: every lane of the 256 assembles one K word and one V
+// word of head h's part of the record from codes staged in LDS; rows outside
+// [lo, hi) keep their previous contents.
+__device__ __forceinline__ void write_block_words(const uint8_t (&codes)[2][kBlockTokens][kHeadDim],
+                                                  int lo, int hi, uint8_t* rec, const RecordLayout& L,
+                                                  int h) {
+    const int t = threadIdx.x;
+    // K word t: token r, dims 8j..8j+7.
+    {
+        const int r = t >> 4, j = t & 15;
+        if (r >= lo && r < hi) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) w |= (uint32_t)codes[0][r][8 * j + k] << nib_shift(k);
+            *(uint32_t*)(rec + L.kc + h * kHeadCodeBytes + r * kCodeRowBytes + j * 4) = w;
+        }
+    }
+    // V word t = (g*16 + c)*4 + m: tokens 4g..4g+3, dims c+32m (x0..x3) and c+32m+16 (x4..x7).
+    {
+        const int g = t >> 6, c = (t >> 2) & 15, m = t & 3;
+        uint32_t w = 0, mask = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int tok = 4 * g + (k & 3);
+            const int dim = c + 32 * m + (k >> 2) * 16;
+            if (tok >= lo && tok < hi) {
+                w |= (uint32_t)codes[1][tok][dim] << nib_shift(k);
+                mask |= 0xFu << nib_shift(k);
+            }
+        }
+        if (mask) {
+            uint32_t* dst = (uint32_t*)(rec + L.vc + h * kHeadCodeBytes) + t;
+            if (mask != 0xFFFFFFFFu) w |= (*dst & ~mask);
+            *dst = w;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void pack_tokens_kernel(PackParams p) {
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int start = p.start_pos[b];
+    const int lb = start / kBlockTokens + (int)blockIdx.x;
+    const int lo = max(start, lb * kBlockTokens) - lb * kBlockTokens;
+    const int hi = min(start + p.T, lb * kBlockTokens + kBlockTokens) - lb * kBlockTokens;
+    if (lo >= hi) return;
+    if (lb < 0 || lb >= p.bt_stride) {
+        if (threadIdx.x == 0 && p.err) atomicOr(p.err, 2);
+        return;
+    }
+    const int phys = p.bt[(int64_t)b * p.bt_stride + lb];
+    if (phys < 0 || (int64_t)phys >= p.pool_blocks) {
+        if (threadIdx.x == 0 && p.err) atomicOr(p.err, 1);
+        return;
+    }
+    const RecordLayout L(p.H);
+    uint8_t* rec = p.pool + (int64_t)phys * L.bytes;
+
+    __shared__ uint8_t codes[2][kBlockTokens][kHeadDim];
+
+    const int t = threadIdx.x;
+    const int row = t >> 3;
+    const int kv = row >> 4, slot = row & 15, part = t & 7;
+    const bool active = slot >= lo && slot < hi;
+    float vals[16];
+    float mn = INFINITY, mx = -INFINITY;
+    if (active) {
+        const int tok = lb * kBlockTokens + slot - start;
+        const int64_t off = (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)tok * p.st + part * 16;
+        load16(kv ? p.v : p.k, p.dtype, off, p.vec_ok, vals);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            mn = fminf(mn, vals[i]);
+            mx = fmaxf(mx, vals[i]);
+        }
+    }
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        mn = fminf(mn, __shfl_xor(mn, off));
+        mx = fmaxf(mx, __shfl_xor(mx, off));
+    }
+    if (active) {
+        const QParams q = qparams_from_minmax(mn, mx);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) codes[kv][slot][part * 16 + i] = (uint8_t)quant_code(vals[i], q);
+        if (part == 0) {
+            float* sc = (float*)(rec + (kv ? L.vs : L.ks)) + h * kBlockTokens + slot;
+            uint8_t* zp = rec + (kv ? L.vz : L.kz) + h * kBlockTokens + slot;
+            *sc = q.scale;
+            *zp = q.zp;
+        }
+    }
+    __syncthreads();
+    write_block_words(codes, lo, hi, rec, L, h);
+}
+
+// Already-quantized tokens in the reference layout (codes uint8 [.., T, 128] and
+// per-token scale/zp) -> block records.  Same placement rules as pack_tokens_kernel.
+struct RepackParams {
+    const uint8_t* kc;
+    const uint8_t* vc;
+    int64_t cb, ch, ct;            // code strides (bytes)
+    const float* ks;
+    const float* vs;
+    const void* kz;
+    const void* vz;
+    int zp_is_float;
+    int64_t mb, mh, mt;            // scale / zp strides (elements)
+    int H, T;
+    const int32_t* start_pos;
+    const int32_t* bt;
+    int bt_stride;
+    uint8_t* pool;
+    int64_t pool_blocks;
+    int32_t* err;
+};
+
+__global__ __launch_bounds__(256) void repack_codes_kernel(RepackParams p) {
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int start = p.start_pos[b];
+    const int lb = start / kBlockTokens + (int)blockIdx.x;
+    const int lo = max(start, lb * kBlockTokens) - lb * kBlockTokens;
+    const int hi = min(start + p.T, lb * kBlockTokens + kBlockTokens) - lb * kBlockTokens;
+    if (lo >= hi) return;
+    if (lb < 0 || lb >= p.bt_stride) {
+        if (threadIdx.x == 0 && p.err) atomicOr(p.err, 2);
+        return;
+    }
+    const int phys = p.bt[(int64_t)b * p.bt_stride + lb];
+    if (phys < 0 || (int64_t)phys >= p.pool_blocks) {
+        if (threadIdx.x == 0 && p.err) atomicOr(p.err, 1);
+        return;
+    }
+    const RecordLayout L(p.H);
+    uint8_t* rec = p.pool + (int64_t)phys * L.bytes;
+    __shared__ uint8_t codes[2][kBlockTokens][kHeadDim];
+    const int t = threadIdx.x;
+    const int row = t >> 3;
+    const int kv = row >> 4, slot = row & 15, part = t & 7;
+    if (slot >= lo && slot < hi) {
+        const int tok = lb * kBlockTokens + slot - start;
+        const uint8_t* src = (kv ? p.vc : p.kc) + (int64_t)b * p.cb + (int64_t)h * p.ch + (int64_t)tok * p.ct + part * 16;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) codes[kv][slot][part * 16 + i] = src[i] & 0xF;
+        if (part == 0) {
+            const int64_t mi = (int64_t)b * p.mb + (int64_t)h * p.mh + (int64_t)tok * p.mt;
+            const float sc = (kv ? p.vs : p.ks)[mi];
+            const void* zsrc = kv ? p.vz : p.kz;
+            const uint8_t zp = p.zp_is_float ? (uint8_t)((const float*)zsrc)[mi] : ((const uint8_t*)zsrc)[mi];
+            ((float*)(rec + (kv ? L.vs : L.ks)))[h * kBlockTokens + slot] = sc;
+            (rec + (kv ? L.vz : L.kz))[h * kBlockTokens + slot] = zp;
+        }
+    }
+    __syncthreads();
+    write_block_words(codes, lo, hi, rec, L, h);
+}
+
+// Pool -> reference layout, one thread per (head, token, dim).
+__global__ __launch_bounds__(256) void unpack_tokens_kernel(
+    const uint8_t* __restrict__ pool, int64_t pool_blocks, const int32_t* __restrict__ bt, int H,
+    int T, int which, uint8_t* __restrict__ codes, float* __restrict__ scales,
+    uint8_t* __restrict__ zps) {
+    const int64_t total = (int64_t)H * T * kHeadDim;
+    const RecordLayout L(H);
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int d = (int)(i % kHeadDim);
+        const int tok = (int)((i / kHeadDim) % T);
+        const int h = (int)(i / ((int64_t)kHeadDim * T));
+        const int phys = bt[tok / kBlockTokens];
+        if (phys < 0 || (int64_t)phys >= pool_blocks) continue;
+        const uint8_t* rec = pool + (int64_t)phys * L.bytes;
+        const int s = tok % kBlockTokens;
+        uint32_t code;
+        if (which == 0) {
+            const uint32_t w = *(const uint32_t*)(rec + L.kc + h * kHeadCodeBytes + s * kCodeRowBytes + (d >> 3) * 4);
+            code = (w >> nib_shift(d & 7)) & 0xFu;
+        } else {
+            const int g = s >> 2, ii = s & 3, c = d & 15, n = d >> 4;
+            const int m = n >> 1, k = ii + (n & 1) * 4;
+            const uint32_t w = ((const uint32_t*)(rec + L.vc + h * kHeadCodeBytes))[(g * 16 + c) * 4 + m];
+            code = (w >> nib_shift(k)) & 0xFu;
+        }
+        if (codes) codes[i] = (uint8_t)code;
+        if (d == 0) {
+            const int64_t gi = (int64_t)h * T + tok;
+            if (scales) scales[gi] = ((const float*)(rec + (which ? L.vs : L.ks)))[h * kBlockTokens + s];
+            if (zps) zps[gi] = (rec + (which ? L.vz : L.kz))[h * kBlockTokens + s];
+        }
+    }
+}
+
+int grid_for(int64_t work, int per_block) {
+    int64_t g = (work + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > 65536) g = 65536;
+    return (int)g;
+}
+
+}  // namespace
+}  // namespace hkv
+
+using namespace hkv;
+
+extern "C" int hkv_quantize_groups(const void* x, int32_t dtype, int64_t n, int32_t group_size,
+                                   uint8_t* codes, float* scales, uint8_t* zps, void* stream) {
+    clear_error();
+    HKV_REQUIRE(n >= 0, HKV_ERR_ARG, "hkv_quantize_groups: n < 0");
+    HKV_REQUIRE(group_size > 0, HKV_ERR_ARG, "hkv_quantize_groups: group_size must be > 0");
+    HKV_REQUIRE(dtype == HKV_DTYPE_F16 || dtype == HKV_DTYPE_BF16 || dtype == HKV_DTYPE_F32,
+                HKV_ERR_ARG, "hkv_quantize_groups: unsupported dtype %d", dtype);
+    if (n == 0) return HKV_OK;
+    HKV_REQUIRE(x && codes && scales && zps, HKV_ERR_ARG, "hkv_quantize_groups: null pointer");
+    const int64_t ngroups = (n + group_size - 1) / group_size;
+    const int blocks = grid_for(ngroups, 4);
+    hipLaunchKernelGGL(quantize_groups_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, x,
+                       dtype, n, group_size, ngroups, codes, scales, zps);
+    HKV_LAUNCH_CHECK("quantize_groups_kernel");
+    return HKV_OK;
+}
+
+extern "C" int hkv_dequantize_groups(const uint8_t* codes, const float* scales, const uint8_t* zps,
+                                     int64_t n, int32_t group_size, void* out, int32_t out_dtype,
+                                     void* stream) {
+    clear_error();
+    HKV_REQUIRE(n >= 0, HKV_ERR_ARG, "hkv_dequantize_groups: n < 0");
+    HKV_REQUIRE(group_size > 0, HKV_ERR_ARG, "hkv_dequantize_groups: group_size must be > 0");
+    HKV_REQUIRE(out_dtype == HKV_DTYPE_F16 || out_dtype == HKV_DTYPE_BF16 || out_dtype == HKV_DTYPE_F32,
+                HKV_ERR_ARG, "hkv_dequantize_groups: unsupported dtype %d", out_dtype);
+    if (n == 0) return HKV_OK;
+    HKV_REQUIRE(codes && scales && zps && out, HKV_ERR_ARG, "hkv_dequantize_groups: null pointer");
+    const int blocks = grid_for(n, 256 * 4);
+    hipLaunchKernelGGL(dequantize_groups_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                       codes, scales, zps, n, group_size, out, out_dtype);
+    HKV_LAUNCH_CHECK("dequantize_groups_kernel");
+    return HKV_OK;
+}
+
+extern "C" int hkv_pack_tokens(const HkvPackArgs* a, void* stream) {
+    clear_error();
+    HKV_REQUIRE(a != nullptr, HKV_ERR_ARG, "hkv_pack_tokens: null args");
+    HKV_REQUIRE(a->head_dim == kHeadDim, HKV_ERR_UNSUPPORTED, "hkv_pack_tokens: head_dim %d != 128",
+                a->head_dim);
+    HKV_REQUIRE(a->dtype == HKV_DTYPE_F16 || a->dtype == HKV_DTYPE_BF16, HKV_ERR_ARG,
+                "hkv_pack_tokens: dtype must be F16 or BF16");
+    HKV_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->num_tokens >= 0, HKV_ERR_ARG,
+                "hkv_pack_tokens: bad batch/heads/tokens");
+    if (a->batch == 0 || a->num_tokens == 0) return HKV_OK;
+    HKV_REQUIRE(a->k && a->v && a->start_pos && a->block_table && a->pool, HKV_ERR_ARG,
+                "hkv_pack_tokens: null pointer");
+    HKV_REQUIRE(a->pool_blocks > 0 && a->bt_stride > 0, HKV_ERR_ARG, "hkv_pack_tokens: empty pool/table");
+    HKV_REQUIRE(a->batch <= 65535 && a->num_kv_heads <= 65535, HKV_ERR_ARG, "hkv_pack_tokens: grid too large");
+    PackParams p;
+    p.k = a->k;
+    p.v = a->v;
+    p.dtype = a->dtype;
+    p.sb = a->src_stride_b;
+    p.sh = a->src_stride_h;
+    p.st = a->src_stride_t;
+    p.H = a->num_kv_heads;
+    p.T = a->num_tokens;
+    p.start_pos = a->start_pos;
+    p.bt = a->block_table;
+    p.bt_stride = a->bt_stride;
+    p.pool = a->pool;
+    p.pool_blocks = a->pool_blocks;
+    p.err = a->err_flag;
+    const bool aligned = (((uintptr_t)a->k | (uintptr_t)a->v) & 15) == 0 &&
+                         ((a->src_stride_b | a->src_stride_h | a->src_stride_t) & 7) == 0;
+    p.vec_ok = aligned ? 1 : 0;
+    // A run of T tokens starting anywhere touches at most ceil(T/16)+1 blocks.
+    const int nblk = (a->num_tokens + kBlockTokens - 1) / kBlockTokens + 1;
+    hipLaunchKernelGGL(pack_tokens_kernel, dim3(nblk, a->num_kv_heads, a->batch), dim3(256), 0,
+                       (hipStream_t)stream, p);
+    HKV_LAUNCH_CHECK("pack_tokens_kernel");
+    return HKV_OK;
+}
+
+extern "C" int hkv_unpack_tokens(const uint8_t* pool, int64_t pool_blocks, const int32_t* block_table,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t num_tokens,
+                                 int32_t which, uint8_t* codes, float* scales, uint8_t* zps,
+                                 void* stream) {
+    clear_error();
+    HKV_REQUIRE(head_dim == kHeadDim, HKV_ERR_UNSUPPORTED, "hkv_unpack_tokens: head_dim %d != 128", head_dim);
+    HKV_REQUIRE(which == 0 || which == 1, HKV_ERR_ARG, "hkv_unpack_tokens: which must be 0 (K) or 1 (V)");
+    HKV_REQUIRE(num_kv_heads > 0 && num_tokens >= 0, HKV_ERR_ARG, "hkv_unpack_tokens: bad sizes");
+    if (num_tokens == 0) return HKV_OK;
+    HKV_REQUIRE(pool && block_table && pool_blocks > 0, HKV_ERR_ARG, "hkv_unpack_tokens: null pool/table");
+    const int64_t total = (int64_t)num_kv_heads * num_tokens * kHeadDim;
+    hipLaunchKernelGGL(unpack_tokens_kernel, dim3(grid_for(total, 256 * 4)), dim3(256), 0,
+                       (hipStream_t)stream, pool, pool_blocks, block_table, num_kv_heads, num_tokens,
+                       which, codes, scales, zps);
+    HKV_LAUNCH_CHECK("unpack_tokens_kernel");
+    return HKV_OK;
+}
+
+extern "C" int hkv_repack_codes(const HkvRepackArgs* a, void* stream) {
+    clear_error();
+    HKV_REQUIRE(a != nullptr, HKV_ERR_ARG, "hkv_repack_codes: null args");
+    HKV_REQUIRE(a->head_dim == kHeadDim, HKV_ERR_UNSUPPORTED, "hkv_repack_codes: head_dim %d != 128",
+                a->head_dim);
+    HKV_REQUIRE(a->zp_dtype == HKV_DTYPE_U8 || a->zp_dtype == HKV_DTYPE_F32, HKV_ERR_ARG,
+                "hkv_repack_codes: zp dtype must be U8 or F32");
+    HKV_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->num_tokens >= 0, HKV_ERR_ARG,
+                "hkv_repack_codes: bad batch/heads/tokens");
+    if (a->batch == 0 || a->num_tokens == 0) return HKV_OK;
+    HKV_REQUIRE(a->k_codes && a->v_codes && a->k_scales && a->v_scales && a->k_zps && a->v_zps &&
+                    a->start_pos && a->block_table && a->pool,
+                HKV_ERR_ARG, "hkv_repack_codes: null pointer");
+    HKV_REQUIRE(a->pool_blocks > 0 && a->bt_stride > 0, HKV_ERR_ARG, "hkv_repack_codes: empty pool/table");
+    HKV_REQUIRE(a->batch <= 65535 && a->num_kv_heads <= 65535, HKV_ERR_ARG, "hkv_repack_codes: grid too large");
+    RepackParams p;
+    p.kc = a->k_codes;
+    p.vc = a->v_codes;
+    p.cb = a->code_stride_b;
+    p.ch = a->code_stride_h;
+    p.ct = a->code_stride_t;
+    p.ks = a->k_scales;
+    p.vs = a->v_scales;
+    p.kz = a->k_zps;
+    p.vz = a->v_zps;
+    p.zp_is_float = a->zp_dtype == HKV_DTYPE_F32 ? 1 : 0;
+    p.mb = a->meta_stride_b;
+    p.mh = a->meta_stride_h;
+    p.mt = a->meta_stride_t;
+    p.H = a->num_kv_heads;
+    p.T = a->num_tokens;
+    p.start_pos = a->start_pos;
+    p.bt = a->block_table;
+    p.bt_stride = a->bt_stride;
+    p.pool = a->pool;
+    p.pool_blocks = a->pool_blocks;
+    p.err = a->err_flag;
+    const int nblk = (a->num_tokens + kBlockTokens - 1) / kBlockTokens + 1;
+    hipLaunchKernelGGL(repack_codes_kernel, dim3(nblk, a->num_kv_heads, a->batch), dim3(256), 0,
+                       (hipStream_t)stream, p);
+    HKV_LAUNCH_CHECK("repack_codes_kernel");
+    return HKV_OK;
+}

@@ -1,0 +1,132 @@
+// fp16 zone storage (sink, recent window, heavy hitters) and the library's common
+// entry points (version, last error, record size).
+#include "hkv_internal.h"
+
+#include <string.h>
+
+namespace hkv {
+
+static thread_local char g_last_error[512] = "";
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+}
+
+void clear_error() { g_last_error[0] = '\0'; }
+
+namespace {
+
+// Halves offset of V[token s][dim d] inside a 16-token transposed tile:
+// [g = s/4][c = d%16][n = d/16][i = s%4].
+__device__ __forceinline__ int vtile_off(int s, int d) {
+    return (((s >> 2) * 16 + (d & 15)) * 8 + (d >> 4)) * 4 + (s & 3);
+}
+
+struct ZoneWriteParams {
+    const uint16_t* k;
+    const uint16_t* v;
+    int64_t sb, sh, st;
+    int H, T;
+    const int32_t* slot_start;
+    int cap, ring;
+    uint16_t* zk;
+    uint16_t* zv;
+};
+
+// One workgroup of 128 lanes per (token, head, sequence); lane = dim.
+__global__ __launch_bounds__(128) void zone_write_kernel(ZoneWriteParams p) {
+    const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int d = threadIdx.x;
+    int slot = p.slot_start[b] + t;
+    if (p.ring) {
+        slot %= p.cap;
+        if (slot < 0) slot += p.cap;
+    }
+    if (slot < 0 || slot >= p.cap) return;
+    const int64_t src = (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)t * p.st + d;
+    const int64_t bh = (int64_t)b * p.H + h;
+    p.zk[(bh * p.cap + slot) * kHeadDim + d] = p.k[src];
+    const int64_t tile = bh * (p.cap / kBlockTokens) + slot / kBlockTokens;
+    p.zv[tile * (kBlockTokens * kHeadDim) + vtile_off(slot & 15, d)] = p.v[src];
+}
+
+__global__ __launch_bounds__(128) void zone_read_kernel(const uint16_t* __restrict__ zk,
+                                                        const uint16_t* __restrict__ zv, int H,
+                                                        int cap, int n, uint16_t* __restrict__ ok,
+                                                        uint16_t* __restrict__ ov) {
+    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int d = threadIdx.x;
+    const int64_t bh = (int64_t)b * H + h;
+    const int64_t dst = (bh * n + s) * kHeadDim + d;
+    if (ok) ok[dst] = zk[(bh * cap + s) * kHeadDim + d];
+    if (ov) {
+        const int64_t tile = bh * (cap / kBlockTokens) + s / kBlockTokens;
+        ov[dst] = zv[tile * (kBlockTokens * kHeadDim) + vtile_off(s & 15, d)];
+    }
+}
+
+}  // namespace
+}  // namespace hkv
+
+using namespace hkv;
+
+extern "C" int hkv_abi_version(void) { return HKV_ABI_VERSION; }
+
+extern "C" const char* hkv_last_error(void) { return g_last_error; }
+
+extern "C" int64_t hkv_block_bytes(int32_t num_kv_heads, int32_t head_dim) {
+    if (num_kv_heads <= 0 || head_dim != kHeadDim) return -1;
+    return RecordLayout(num_kv_heads).bytes;
+}
+
+extern "C" int hkv_zone_write(const HkvZoneWriteArgs* a, void* stream) {
+    clear_error();
+    HKV_REQUIRE(a != nullptr, HKV_ERR_ARG, "hkv_zone_write: null args");
+    HKV_REQUIRE(a->head_dim == kHeadDim, HKV_ERR_UNSUPPORTED, "hkv_zone_write: head_dim %d != 128", a->head_dim);
+    HKV_REQUIRE(a->capacity > 0 && a->capacity % kBlockTokens == 0, HKV_ERR_ARG,
+                "hkv_zone_write: capacity %d must be a positive multiple of 16", a->capacity);
+    HKV_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->num_tokens >= 0, HKV_ERR_ARG,
+                "hkv_zone_write: bad sizes");
+    if (a->batch == 0 || a->num_tokens == 0) return HKV_OK;
+    HKV_REQUIRE(a->k && a->v && a->slot_start && a->zone_k && a->zone_v, HKV_ERR_ARG,
+                "hkv_zone_write: null pointer");
+    HKV_REQUIRE(a->num_tokens <= 2147483647 && a->num_kv_heads <= 65535 && a->batch <= 65535,
+                HKV_ERR_ARG, "hkv_zone_write: grid too large");
+    ZoneWriteParams p;
+    p.k = a->k;
+    p.v = a->v;
+    p.sb = a->src_stride_b;
+    p.sh = a->src_stride_h;
+    p.st = a->src_stride_t;
+    p.H = a->num_kv_heads;
+    p.T = a->num_tokens;
+    p.slot_start = a->slot_start;
+    p.cap = a->capacity;
+    p.ring = a->ring;
+    p.zk = a->zone_k;
+    p.zv = a->zone_v;
+    hipLaunchKernelGGL(zone_write_kernel, dim3(a->num_tokens, a->num_kv_heads, a->batch), dim3(128), 0,
+                       (hipStream_t)stream, p);
+    HKV_LAUNCH_CHECK("zone_write_kernel");
+    return HKV_OK;
+}
+
+extern "C" int hkv_zone_read(const uint16_t* zone_k, const uint16_t* zone_v, int32_t batch,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t capacity, int32_t n,
+                             uint16_t* out_k, uint16_t* out_v, void* stream) {
+    clear_error();
+    HKV_REQUIRE(head_dim == kHeadDim, HKV_ERR_UNSUPPORTED, "hkv_zone_read: head_dim %d != 128", head_dim);
+    HKV_REQUIRE(capacity > 0 && capacity % kBlockTokens == 0, HKV_ERR_ARG,
+                "hkv_zone_read: capacity must be a positive multiple of 16");
+    HKV_REQUIRE(n >= 0 && n <= capacity && batch >= 0 && num_kv_heads > 0, HKV_ERR_ARG,
+                "hkv_zone_read: bad sizes");
+    if (n == 0 || batch == 0) return HKV_OK;
+    HKV_REQUIRE(zone_k && zone_v && (out_k || out_v), HKV_ERR_ARG, "hkv_zone_read: null pointer");
+    hipLaunchKernelGGL(zone_read_kernel, dim3(n, num_kv_heads, batch), dim3(128), 0, (hipStream_t)stream,
+                       zone_k, zone_v, num_kv_heads, capacity, n, out_k, out_v);
+    HKV_LAUNCH_CHECK("zone_read_kernel");
+    return HKV_OK;
+}

@@ -1,0 +1,13 @@
+"""heterokv: MI355X-native INT4-KV hot path (HIP kernels for gfx950 behind a C ABI).
+
+Drop-in names of the reference's quantized-KV path:
+  KVCompressor                 (src/quantization/kv_compressor.py)
+  fused_dequant_attn_decode    (src/quantization/kernels/fused_dequant_attn.py)
+plus the block-pool / fp16-zone primitives in ``heterokv.ops``.
+"""
+from ._lib import HeteroKVError, load  # noqa: F401
+from .kv_compressor import KVCompressor  # noqa: F401
+from .fused_dequant_attn import fused_dequant_attn_decode  # noqa: F401
+from . import ops  # noqa: F401
+
+__all__ = ["HeteroKVError", "KVCompressor", "fused_dequant_attn_decode", "ops", "load"]

@@ -1,0 +1,131 @@
+"""ctypes binding of libheterokv.so (declared in include/heterokv.h).
+
+The library is loaded after torch so that it resolves torch's HIP runtime
+(same soname) instead of loading a second one.  There is no fallback: if the
+library is missing or a call fails, a HeteroKVError is raised.
+"""
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must be loaded before the HIP library, see above)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libheterokv.so")
+
+ABI_VERSION = 1
+DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_U8 = 0, 1, 2, 3
+MAX_F16_ZONES = 3
+BLOCK_TOKENS = 16
+HEAD_DIM = 128
+
+HKV_OK = 0
+ERR_NAMES = {-1: "HKV_ERR_ARG", -2: "HKV_ERR_HIP", -3: "HKV_ERR_CAPACITY", -4: "HKV_ERR_UNSUPPORTED"}
+
+
+class HeteroKVError(RuntimeError):
+    """A libheterokv call failed (carries the C return code)."""
+
+    def __init__(self, code, msg):
+        super().__init__("%s (%d): %s" % (ERR_NAMES.get(code, "HKV_ERR"), code, msg))
+        self.code = code
+
+
+vp = ctypes.c_void_p
+i32 = ctypes.c_int32
+i64 = ctypes.c_int64
+
+
+class PackArgs(ctypes.Structure):
+    _fields_ = [("k", vp), ("v", vp), ("dtype", i32),
+                ("src_stride_b", i64), ("src_stride_h", i64), ("src_stride_t", i64),
+                ("batch", i32), ("num_kv_heads", i32), ("head_dim", i32), ("num_tokens", i32),
+                ("start_pos", vp), ("block_table", vp), ("bt_stride", i32),
+                ("pool", vp), ("pool_blocks", i64), ("err_flag", vp)]
+
+
+class RepackArgs(ctypes.Structure):
+    _fields_ = [("k_codes", vp), ("v_codes", vp),
+                ("code_stride_b", i64), ("code_stride_h", i64), ("code_stride_t", i64),
+                ("k_scales", vp), ("v_scales", vp), ("k_zps", vp), ("v_zps", vp), ("zp_dtype", i32),
+                ("meta_stride_b", i64), ("meta_stride_h", i64), ("meta_stride_t", i64),
+                ("batch", i32), ("num_kv_heads", i32), ("head_dim", i32), ("num_tokens", i32),
+                ("start_pos", vp), ("block_table", vp), ("bt_stride", i32),
+                ("pool", vp), ("pool_blocks", i64), ("err_flag", vp)]
+
+
+class ZoneWriteArgs(ctypes.Structure):
+    _fields_ = [("k", vp), ("v", vp),
+                ("src_stride_b", i64), ("src_stride_h", i64), ("src_stride_t", i64),
+                ("batch", i32), ("num_kv_heads", i32), ("head_dim", i32), ("num_tokens", i32),
+                ("slot_start", vp), ("capacity", i32), ("ring", i32),
+                ("zone_k", vp), ("zone_v", vp)]
+
+
+class F16Zone(ctypes.Structure):
+    _fields_ = [("k", vp), ("v", vp), ("capacity", i32), ("max_len", i32), ("lens", vp)]
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [("batch", i32), ("num_q_heads", i32), ("num_kv_heads", i32), ("head_dim", i32),
+                ("sm_scale", ctypes.c_float),
+                ("q", vp), ("q_stride_b", i64), ("q_stride_h", i64),
+                ("num_f16_zones", i32), ("f16", F16Zone * MAX_F16_ZONES),
+                ("pool", vp), ("pool_blocks", i64), ("block_table", vp), ("bt_stride", i32),
+                ("int4_lens", vp), ("int4_max_len", i32),
+                ("out", vp), ("out_stride_b", i64), ("out_stride_h", i64),
+                ("workspace", vp), ("workspace_bytes", ctypes.c_size_t), ("splits_hint", i32)]
+
+
+# (name, restype, argtypes) of every symbol include/heterokv.h declares.
+SYMBOLS = [
+    ("hkv_abi_version", ctypes.c_int, []),
+    ("hkv_last_error", ctypes.c_char_p, []),
+    ("hkv_block_bytes", i64, [i32, i32]),
+    ("hkv_quantize_groups", ctypes.c_int, [vp, i32, i64, i32, vp, vp, vp, vp]),
+    ("hkv_dequantize_groups", ctypes.c_int, [vp, vp, vp, i64, i32, vp, i32, vp]),
+    ("hkv_pack_tokens", ctypes.c_int, [ctypes.POINTER(PackArgs), vp]),
+    ("hkv_repack_codes", ctypes.c_int, [ctypes.POINTER(RepackArgs), vp]),
+    ("hkv_unpack_tokens", ctypes.c_int, [vp, i64, vp, i32, i32, i32, i32, vp, vp, vp, vp]),
+    ("hkv_zone_write", ctypes.c_int, [ctypes.POINTER(ZoneWriteArgs), vp]),
+    ("hkv_zone_read", ctypes.c_int, [vp, vp, i32, i32, i32, i32, i32, vp, vp, vp]),
+    ("hkv_decode_workspace_bytes", ctypes.c_size_t, [i32, i32, i32, i32, i32, vp, i32]),
+    ("hkv_decode_attn", ctypes.c_int, [ctypes.POINTER(DecodeArgs), vp]),
+]
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load():
+    """Load libheterokv.so once; raises if it is missing or has the wrong ABI."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise HeteroKVError(-2, "libheterokv.so not built at %s (run __graft_entry__.build() or "
+                                    "hetero-kvcache-optimizer_amd/build.py)" % LIB_PATH)
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, res, args in SYMBOLS:
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.hkv_abi_version()
+        if ver != ABI_VERSION:
+            raise HeteroKVError(-1, "libheterokv ABI %d, expected %d" % (ver, ABI_VERSION))
+        _lib = lib
+    return _lib
+
+
+def check(rc, what=""):
+    if rc != HKV_OK:
+        msg = load().hkv_last_error().decode("utf-8", "replace")
+        raise HeteroKVError(rc, (what + ": " if what else "") + msg)
+
+
+def stream_ptr(device=None):
+    """Raw hipStream_t of torch's current stream on `device`."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

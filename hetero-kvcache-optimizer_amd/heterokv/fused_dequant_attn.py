@@ -1,0 +1,57 @@
+"""Fused dequant-attention entry points on the GPU.
+
+Drop-ins for the reference's src/quantization/kernels/fused_dequant_attn.py:301-368
+(``fused_dequant_attn_decode``) with the numerics of its torch path
+(src/quantization/fused_dequant_attn.py:326-331,388-390):
+    K = (Kq - zp) * s, V = (Vq - zp) * s, out = softmax(q K^T * sm_scale) V,
+sm_scale defaulting to 1/sqrt(head_dim).  Unlike the reference's Triton kernel
+(which drops sm_scale and mis-addresses K, see its :69-78,353-365) this computes
+exactly that formula, and it also accepts GQA (q heads a multiple of kv heads).
+
+The reference passes unpacked codes (one uint8 per value) with per-token
+scales/zps [B, H, S]; they are repacked into INT4 block records on the device
+(hkv_repack_codes) and attended by the split-K kernel (hkv_decode_attn).
+"""
+import math
+from typing import Optional
+
+import torch
+
+from . import ops
+from ._lib import BLOCK_TOKENS, HeteroKVError
+
+
+def _as_4d(t):
+    if t.dim() == 2:
+        return t.unsqueeze(0).unsqueeze(0)
+    if t.dim() == 3:
+        return t.unsqueeze(0)
+    return t
+
+
+def fused_dequant_attn_decode(q: torch.Tensor, k_data: torch.Tensor, k_scales: torch.Tensor,
+                              k_zps: torch.Tensor, v_data: torch.Tensor, v_scales: torch.Tensor,
+                              v_zps: torch.Tensor, sm_scale: Optional[float] = None) -> torch.Tensor:
+    """q [B, Hq, 1, D] fp16; k/v_data uint8 [B, Hkv, S, D]; scales/zps [B, Hkv, S] -> [B, Hq, 1, D] in q.dtype."""
+    if q.dim() != 4 or q.shape[2] != 1:
+        raise HeteroKVError(-1, "Decode expects [B,H,1,D], got %s" % (tuple(q.shape),))
+    B, Hq, _, D = q.shape
+    kd, vd = _as_4d(k_data), _as_4d(v_data)
+    if kd.dim() == 4 and kd.shape[0] != B:
+        raise HeteroKVError(-1, "batch mismatch between q and k_data")
+    Hkv, S = kd.shape[1], kd.shape[2]
+    ks = k_scales.reshape(B, Hkv, S)
+    vs = v_scales.reshape(B, Hkv, S)
+    kz = k_zps.reshape(B, Hkv, S)
+    vz = v_zps.reshape(B, Hkv, S)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    nblk = (S + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+    pool = ops.Int4Pool(B * nblk, Hkv, q.device)
+    bt = torch.arange(B * nblk, dtype=torch.int32, device=q.device).reshape(B, nblk)
+    start = torch.zeros(B, dtype=torch.int32, device=q.device)
+    ops.repack_codes(pool, kd, vd, ks, vs, kz, vz, start, bt)
+    q16 = q if q.dtype == torch.float16 else q.to(torch.float16)
+    out = ops.decode_attention(q16, zones=(), pool=pool, block_table=bt, int4_lens=None, int4_max_len=S,
+                               sm_scale=sm_scale)
+    return out.to(q.dtype)

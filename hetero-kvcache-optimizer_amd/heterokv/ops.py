@@ -1,0 +1,331 @@
+"""Tensor-level wrappers over the libheterokv C ABI.
+
+Every function here takes torch tensors that live on a ROCm GPU, passes raw
+pointers and torch's current stream to the library, and raises HeteroKVError on
+any failure.  Nothing falls back to the CPU.
+"""
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import BLOCK_TOKENS, HEAD_DIM, HeteroKVError, check, load, stream_ptr
+
+_DTYPES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
+
+
+def _require_gpu(*ts):
+    for t in ts:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+            raise HeteroKVError(-1, "heterokv kernels need tensors on a ROCm GPU (got %s)" %
+                                (t.device if isinstance(t, torch.Tensor) else type(t)))
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def record_bytes(num_kv_heads, head_dim=HEAD_DIM):
+    n = load().hkv_block_bytes(num_kv_heads, head_dim)
+    if n < 0:
+        raise HeteroKVError(-4, "unsupported block geometry (heads=%d, head_dim=%d)" % (num_kv_heads, head_dim))
+    return int(n)
+
+
+# ----------------------------------------------------------------------- reference layout
+def quantize_groups(x, group_size=128):
+    """KVCompressor.compress on the GPU: (codes uint8 like x, scales f32 [G], zps u8 [G])."""
+    _require_gpu(x)
+    if x.dtype not in _DTYPES:
+        raise HeteroKVError(-1, "quantize_groups: unsupported dtype %s" % x.dtype)
+    xc = x.contiguous()
+    n = xc.numel()
+    ng = (n + group_size - 1) // group_size
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scales = torch.empty(ng, dtype=torch.float32, device=x.device)
+    zps = torch.empty(ng, dtype=torch.uint8, device=x.device)
+    check(load().hkv_quantize_groups(_p(xc), _DTYPES[x.dtype], n, group_size, _p(codes), _p(scales),
+                                     _p(zps), stream_ptr(x.device)), "hkv_quantize_groups")
+    return codes, scales, zps
+
+
+def dequantize_groups(codes, scales, zps, group_size=128, dtype=torch.float16):
+    """KVCompressor.decompress on the GPU."""
+    _require_gpu(codes, scales, zps)
+    if dtype not in _DTYPES:
+        raise HeteroKVError(-1, "dequantize_groups: unsupported dtype %s" % dtype)
+    c = codes.contiguous()
+    s = scales.contiguous().to(torch.float32)
+    z = zps.contiguous()
+    if z.dtype != torch.uint8:
+        z = z.to(torch.uint8)
+    n = c.numel()
+    ng = (n + group_size - 1) // group_size
+    if s.numel() < ng or z.numel() < ng:
+        raise HeteroKVError(-3, "dequantize_groups: %d groups need %d scales/zps, got %d/%d" %
+                            (ng, ng, s.numel(), z.numel()))
+    out = torch.empty(codes.shape, dtype=dtype, device=codes.device)
+    check(load().hkv_dequantize_groups(_p(c), _p(s), _p(z), n, group_size, _p(out), _DTYPES[dtype],
+                                       stream_ptr(codes.device)), "hkv_dequantize_groups")
+    return out
+
+
+# ----------------------------------------------------------------------- INT4 block pool
+class Int4Pool:
+    """Device array of INT4 block records: uint8 [num_blocks, record_bytes]."""
+
+    def __init__(self, num_blocks, num_kv_heads, device, head_dim=HEAD_DIM):
+        if head_dim != HEAD_DIM:
+            raise HeteroKVError(-4, "Int4Pool: head_dim must be 128")
+        self.num_kv_heads = num_kv_heads
+        self.record_bytes = record_bytes(num_kv_heads)
+        self.num_blocks = num_blocks
+        self.data = torch.zeros((max(num_blocks, 1), self.record_bytes), dtype=torch.uint8, device=device)
+        self.err = torch.zeros(1, dtype=torch.int32, device=device)
+
+    @property
+    def device(self):
+        return self.data.device
+
+    def check_errors(self):
+        """Raise if a pack kernel met a bad block id or slot (synchronizes)."""
+        e = int(self.err.item())
+        if e:
+            self.err.zero_()
+            why = []
+            if e & 1:
+                why.append("a block table held an id outside [0, %d)" % self.num_blocks)
+            if e & 2:
+                why.append("a token slot lay beyond its block table row")
+            raise HeteroKVError(-1, "; ".join(why))
+
+
+def _i32(t, device):
+    if not isinstance(t, torch.Tensor):
+        t = torch.tensor(t, dtype=torch.int32)
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+def _check_table(bt, sp, B, T, what):
+    if bt.shape[0] < B or sp.numel() < B:
+        raise HeteroKVError(-1, "%s: block table / start positions cover %d / %d sequences, need %d" %
+                            (what, bt.shape[0], sp.numel(), B))
+
+
+def pack_tokens(pool, k, v, start_pos, block_table):
+    """Quantize + pack k, v [B, H, T, 128] (fp16/bf16) into `pool` at INT4 slots start_pos[b] + t."""
+    _require_gpu(k, v)
+    if k.shape != v.shape or k.dim() != 4 or k.shape[-1] != HEAD_DIM:
+        raise HeteroKVError(-1, "pack_tokens: k/v must both be [B, H, T, 128], got %s / %s" %
+                            (tuple(k.shape), tuple(v.shape)))
+    if k.dtype != v.dtype or k.dtype not in (torch.float16, torch.bfloat16):
+        raise HeteroKVError(-1, "pack_tokens: k/v must be fp16 or bf16")
+    if k.stride() != v.stride() or k.stride(-1) != 1:
+        k, v = k.contiguous(), v.contiguous()
+    B, H, T, _ = k.shape
+    if H != pool.num_kv_heads:
+        raise HeteroKVError(-1, "pack_tokens: %d heads, pool has %d" % (H, pool.num_kv_heads))
+    sp = _i32(start_pos, k.device)
+    bt = _i32(block_table, k.device)
+    if bt.dim() == 1:
+        bt = bt.unsqueeze(0)
+    _check_table(bt, sp, B, T, "pack_tokens")
+    a = _lib.PackArgs(k=k.data_ptr(), v=v.data_ptr(), dtype=_DTYPES[k.dtype],
+                      src_stride_b=k.stride(0), src_stride_h=k.stride(1), src_stride_t=k.stride(2),
+                      batch=B, num_kv_heads=H, head_dim=HEAD_DIM, num_tokens=T,
+                      start_pos=sp.data_ptr(), block_table=bt.data_ptr(), bt_stride=bt.shape[1],
+                      pool=pool.data.data_ptr(), pool_blocks=pool.num_blocks, err_flag=pool.err.data_ptr())
+    check(load().hkv_pack_tokens(ctypes.byref(a), stream_ptr(k.device)), "hkv_pack_tokens")
+
+
+def repack_codes(pool, k_codes, v_codes, k_scales, v_scales, k_zps, v_zps, start_pos, block_table):
+    """Reference-layout INT4 (codes uint8 [B,H,T,128], scales/zps [B,H,T]) -> pool records."""
+    _require_gpu(k_codes, v_codes, k_scales, v_scales, k_zps, v_zps)
+    B, H, T, D = k_codes.shape
+    if D != HEAD_DIM or v_codes.shape != k_codes.shape:
+        raise HeteroKVError(-1, "repack_codes: codes must be [B, H, T, 128]")
+    kc, vc = k_codes.contiguous(), v_codes.contiguous()
+    ks = k_scales.reshape(B, H, T).to(torch.float32).contiguous()
+    vs = v_scales.reshape(B, H, T).to(torch.float32).contiguous()
+    zdt = torch.uint8 if k_zps.dtype == torch.uint8 else torch.float32
+    kz = k_zps.reshape(B, H, T).to(zdt).contiguous()
+    vz = v_zps.reshape(B, H, T).to(zdt).contiguous()
+    sp = _i32(start_pos, kc.device)
+    bt = _i32(block_table, kc.device)
+    if bt.dim() == 1:
+        bt = bt.unsqueeze(0)
+    _check_table(bt, sp, B, T, "repack_codes")
+    a = _lib.RepackArgs(k_codes=kc.data_ptr(), v_codes=vc.data_ptr(),
+                        code_stride_b=kc.stride(0), code_stride_h=kc.stride(1), code_stride_t=kc.stride(2),
+                        k_scales=ks.data_ptr(), v_scales=vs.data_ptr(), k_zps=kz.data_ptr(), v_zps=vz.data_ptr(),
+                        zp_dtype=_lib.DTYPE_U8 if zdt == torch.uint8 else _lib.DTYPE_F32,
+                        meta_stride_b=ks.stride(0), meta_stride_h=ks.stride(1), meta_stride_t=ks.stride(2),
+                        batch=B, num_kv_heads=H, head_dim=HEAD_DIM, num_tokens=T,
+                        start_pos=sp.data_ptr(), block_table=bt.data_ptr(), bt_stride=bt.shape[1],
+                        pool=pool.data.data_ptr(), pool_blocks=pool.num_blocks, err_flag=pool.err.data_ptr())
+    check(load().hkv_repack_codes(ctypes.byref(a), stream_ptr(kc.device)), "hkv_repack_codes")
+
+
+def unpack_tokens(pool, block_table_row, num_tokens, which):
+    """Pool -> reference layout for one sequence: (codes [H,T,128], scales [H*T], zps [H*T])."""
+    dev = pool.device
+    bt = _i32(block_table_row, dev).reshape(-1)
+    if bt.numel() * BLOCK_TOKENS < num_tokens:
+        raise HeteroKVError(-3, "unpack_tokens: block table row covers %d slots, need %d" %
+                            (bt.numel() * BLOCK_TOKENS, num_tokens))
+    H = pool.num_kv_heads
+    codes = torch.empty((H, num_tokens, HEAD_DIM), dtype=torch.uint8, device=dev)
+    scales = torch.empty(H * num_tokens, dtype=torch.float32, device=dev)
+    zps = torch.empty(H * num_tokens, dtype=torch.uint8, device=dev)
+    check(load().hkv_unpack_tokens(_p(pool.data), pool.num_blocks, _p(bt), H, HEAD_DIM, num_tokens,
+                                   0 if which in (0, "k", "K") else 1, _p(codes), _p(scales), _p(zps),
+                                   stream_ptr(dev)), "hkv_unpack_tokens")
+    return codes, scales, zps
+
+
+# ----------------------------------------------------------------------- fp16 zones
+class F16Zone:
+    """fp16 zone storage: K [B, H, cap, 128] row-major, V in 16-token transposed tiles."""
+
+    def __init__(self, batch, num_kv_heads, capacity, device):
+        cap = int(math.ceil(max(capacity, 1) / BLOCK_TOKENS) * BLOCK_TOKENS)
+        self.batch, self.num_kv_heads, self.capacity = batch, num_kv_heads, cap
+        self.k = torch.zeros((batch, num_kv_heads, cap, HEAD_DIM), dtype=torch.float16, device=device)
+        self.v = torch.zeros((batch, num_kv_heads, cap // BLOCK_TOKENS, BLOCK_TOKENS * HEAD_DIM),
+                             dtype=torch.float16, device=device)
+
+    @property
+    def device(self):
+        return self.k.device
+
+    def write(self, k, v, slot_start, ring=False):
+        """Write k, v [B, H, T, 128] fp16 at slots slot_start[b] + t (mod capacity if ring)."""
+        _require_gpu(k, v)
+        if k.dtype != torch.float16 or v.dtype != torch.float16:
+            raise HeteroKVError(-1, "F16Zone.write: k/v must be fp16")
+        if k.shape != v.shape or k.dim() != 4 or k.shape[-1] != HEAD_DIM:
+            raise HeteroKVError(-1, "F16Zone.write: k/v must be [B, H, T, 128]")
+        if k.stride() != v.stride() or k.stride(-1) != 1:
+            k, v = k.contiguous(), v.contiguous()
+        B, H, T, _ = k.shape
+        if B != self.batch or H != self.num_kv_heads:
+            raise HeteroKVError(-1, "F16Zone.write: shape %s does not match zone [%d, %d]" %
+                                (tuple(k.shape), self.batch, self.num_kv_heads))
+        ss = _i32(slot_start, k.device)
+        a = _lib.ZoneWriteArgs(k=k.data_ptr(), v=v.data_ptr(), src_stride_b=k.stride(0),
+                               src_stride_h=k.stride(1), src_stride_t=k.stride(2), batch=B, num_kv_heads=H,
+                               head_dim=HEAD_DIM, num_tokens=T, slot_start=ss.data_ptr(),
+                               capacity=self.capacity, ring=1 if ring else 0,
+                               zone_k=self.k.data_ptr(), zone_v=self.v.data_ptr())
+        check(load().hkv_zone_write(ctypes.byref(a), stream_ptr(k.device)), "hkv_zone_write")
+
+    def read(self, n):
+        """Slots [0, n) as row-major (K, V) [B, H, n, 128]."""
+        ok = torch.empty((self.batch, self.num_kv_heads, n, HEAD_DIM), dtype=torch.float16, device=self.device)
+        ov = torch.empty_like(ok)
+        check(load().hkv_zone_read(_p(self.k), _p(self.v), self.batch, self.num_kv_heads, HEAD_DIM,
+                                   self.capacity, n, _p(ok), _p(ov), stream_ptr(self.device)), "hkv_zone_read")
+        return ok, ov
+
+
+# ----------------------------------------------------------------------- decode attention
+def decode_workspace_bytes(batch, num_q_heads, num_kv_heads, int4_max_len, f16_max_lens):
+    arr = (ctypes.c_int32 * max(len(f16_max_lens), 1))(*f16_max_lens)
+    n = load().hkv_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, HEAD_DIM, int4_max_len,
+                                          ctypes.cast(arr, ctypes.c_void_p), len(f16_max_lens))
+    if n == 0:
+        raise HeteroKVError(-1, "decode_workspace_bytes: unsupported geometry")
+    return int(n)
+
+
+class DecodeWorkspace:
+    """Zero-initialised scratch for hkv_decode_attn; grows on demand (re-zeroed when it grows)."""
+
+    def __init__(self, device):
+        self.device = torch.device(device)
+        self.buf = None
+
+    def get(self, nbytes):
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=self.device)
+        return self.buf
+
+    def error_flag(self):
+        """Non-zero if a decode kernel met an out-of-range block id since the last call (syncs)."""
+        if self.buf is None:
+            return 0
+        v = int(self.buf[:4].view(torch.int32).item())
+        if v:
+            self.buf[:4].zero_()
+        return v
+
+
+def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
+                     sm_scale=None, workspace=None, out=None):
+    """Split-K decode attention over fp16 zones and the INT4 pool.
+
+    q: [B, Hq, 128] or [B, Hq, 1, 128] fp16.
+    zones: sequence of (F16Zone, lens int32 [B] or None, max_len).
+    pool / block_table [B, nblk] / int4_lens [B] / int4_max_len: the INT4 zone.
+    Returns fp16 [B, Hq, 128] (or [B, Hq, 1, 128] if q was 4-D).
+    """
+    _require_gpu(q)
+    squeeze = q.dim() == 4
+    q3 = q.reshape(q.shape[0], q.shape[1], q.shape[-1]) if squeeze else q
+    if q3.dtype != torch.float16 or q3.shape[-1] != HEAD_DIM:
+        raise HeteroKVError(-1, "decode_attention: q must be fp16 [B, Hq, 128]")
+    if q3.stride(-1) != 1 or q3.data_ptr() % 16 or q3.stride(0) % 8 or q3.stride(1) % 8:
+        q3 = q3.contiguous()
+    B, Hq, _ = q3.shape
+    if len(zones) > _lib.MAX_F16_ZONES:
+        raise HeteroKVError(-1, "decode_attention: at most %d fp16 zones" % _lib.MAX_F16_ZONES)
+    Hkv = pool.num_kv_heads if pool is not None else (zones[0][0].num_kv_heads if zones else None)
+    if Hkv is None:
+        raise HeteroKVError(-1, "decode_attention: no key/value zone given")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(HEAD_DIM)
+    dev = q3.device
+    if out is None:
+        out = torch.empty((B, Hq, HEAD_DIM), dtype=torch.float16, device=dev)
+    a = _lib.DecodeArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, HEAD_DIM
+    a.sm_scale = float(sm_scale)
+    a.q, a.q_stride_b, a.q_stride_h = q3.data_ptr(), q3.stride(0), q3.stride(1)
+    a.num_f16_zones = len(zones)
+    keep = []
+    zl = []
+    for i, (z, lens, max_len) in enumerate(zones):
+        if z.batch != B or z.num_kv_heads != Hkv:
+            raise HeteroKVError(-1, "decode_attention: zone %d geometry mismatch" % i)
+        lt = None
+        if lens is not None:
+            lt = _i32(lens, dev)
+            keep.append(lt)
+        a.f16[i] = _lib.F16Zone(k=z.k.data_ptr(), v=z.v.data_ptr(), capacity=z.capacity, max_len=int(max_len),
+                                lens=lt.data_ptr() if lt is not None else 0)
+        zl.append(int(max_len))
+    if int4_max_len > 0:
+        if pool is None or block_table is None:
+            raise HeteroKVError(-1, "decode_attention: INT4 zone needs a pool and a block table")
+        bt = _i32(block_table, dev)
+        if bt.dim() == 1:
+            bt = bt.unsqueeze(0)
+        keep.append(bt)
+        a.pool, a.pool_blocks = pool.data.data_ptr(), pool.num_blocks
+        a.block_table, a.bt_stride = bt.data_ptr(), bt.shape[1]
+        if int4_lens is not None:
+            il = _i32(int4_lens, dev)
+            keep.append(il)
+            a.int4_lens = il.data_ptr()
+    a.int4_max_len = int(int4_max_len)
+    a.out, a.out_stride_b, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    nbytes = decode_workspace_bytes(B, Hq, Hkv, int(int4_max_len), zl)
+    if workspace is None:
+        workspace = DecodeWorkspace(dev)
+    ws = workspace.get(nbytes)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    check(load().hkv_decode_attn(ctypes.byref(a), stream_ptr(dev)), "hkv_decode_attn")
+    return out.unsqueeze(2) if squeeze else out

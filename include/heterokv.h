@@ -1,0 +1,237 @@
+/*
+ * heterokv.h -- C ABI of libheterokv.so, the MI355X (gfx950) INT4-KV hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t passed
+ * as `void*` (NULL = the default stream).  Nothing here allocates device memory:
+ * the caller owns every buffer, including the decode workspace.  Every entry
+ * point returns HKV_OK (0) or a negative HKV_ERR_* code; hkv_last_error() then
+ * holds a message for the calling thread.  There is no fallback path: a call
+ * that cannot run on the GPU fails.
+ *
+ * Reference interfaces replaced (paths are inside kldxg123/Hetero-KVCache-Optimizer):
+ *   KVCompressor.compress          src/quantization/kv_compressor.py:50-98
+ *   KVCompressor.decompress        src/quantization/kv_compressor.py:100-132
+ *   fused_dequant_attn_decode      src/quantization/kernels/fused_dequant_attn.py:301-368
+ *                                  (numerics: src/quantization/fused_dequant_attn.py:326-331,388-390)
+ *   HeteroKVManager zone storage   src/memory/manager.py:416-674 (sink / tail / heavy-hitter)
+ *   _evict_to_dram + DRAM chunks   src/memory/manager.py:1231-1299, src/memory/dram_storage.py:106-138
+ *   decompress_dram_chunks (Path C gather order)   src/memory/manager.py:779-821
+ *
+ * INT4 block pool.  Tokens of the quantized middle zone live in 16-token
+ * blocks.  One block record holds every kv head of those 16 tokens:
+ *
+ *   offset                     contents
+ *   0                          K codes  [H][16 tokens][64 B]    (packed, see below)
+ *   H*1024                     V codes  [H][1024 B]             (packed, transposed tiles)
+ *   H*2048                     K scales [H][16] float32
+ *   H*2048 + H*64              V scales [H][16] float32
+ *   H*2048 + H*128             K zero points [H][16] uint8
+ *   H*2048 + H*144             V zero points [H][16] uint8
+ *   record size = H * 2208 bytes                                 (head_dim 128)
+ *
+ * A token's 128 values form one quantization group, exactly as the reference
+ * compressor's default group_size=128 over a [B,H,S,128] tensor: scale =
+ * max((max-min)/15, 1e-8) in float32, zp = clamp(rint(-min/scale),0,15),
+ * code = clamp(rint(x/scale + zp),0,15) (round half to even).
+ *
+ * Nibble packing.  A 32-bit little-endian word holds 8 codes x0..x7 with
+ * x_k at bit (k%2)*16 + (k/2)*4, so (w >> 4i) & 0x000F000F yields the pair
+ * (x_2i, x_2i+1) as two 16-bit lanes.
+ *   K: word j of a token row (j=0..15) holds dims 8j..8j+7 as x0..x7.
+ *   V: word (g*16+c)*4+m of a head's 1024 B holds, for tokens 4g..4g+3,
+ *      x0..x3 = dim c+32m and x4..x7 = dim c+32m+16   (g<4, c<16, m<4).
+ *
+ * fp16 zones (sink, recent window, heavy hitters).  K is row-major
+ * [B][H][cap][128]; V is stored in 16-token transposed tiles
+ * [B][H][cap/16][4 g][16 c][8 n][4 i] fp16 holding V[token 4g+i][dim c+16n].
+ * Slots [0, len) of a zone are attended; their order does not matter.
+ */
+#ifndef HETEROKV_H
+#define HETEROKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HKV_ABI_VERSION 1
+
+/* dtype codes */
+#define HKV_DTYPE_F16  0
+#define HKV_DTYPE_BF16 1
+#define HKV_DTYPE_F32  2
+#define HKV_DTYPE_U8   3
+
+/* return codes */
+#define HKV_OK               0
+#define HKV_ERR_ARG         -1   /* bad argument (shape, null pointer, size) */
+#define HKV_ERR_HIP         -2   /* a HIP runtime call failed */
+#define HKV_ERR_CAPACITY    -3   /* a caller buffer or pool is too small */
+#define HKV_ERR_UNSUPPORTED -4   /* shape the kernels do not handle (e.g. head_dim != 128) */
+
+#define HKV_BLOCK_TOKENS 16
+#define HKV_MAX_F16_ZONES 3
+
+/* Version of this ABI (HKV_ABI_VERSION). */
+int hkv_abi_version(void);
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* hkv_last_error(void);
+
+/* Bytes of one INT4 block record for `num_kv_heads` heads (head_dim must be 128). */
+int64_t hkv_block_bytes(int32_t num_kv_heads, int32_t head_dim);
+
+/*
+ * KVCompressor.compress over a flat tensor (kv_compressor.py:66-98).
+ * x: n elements of `dtype` (F16/BF16/F32), contiguous.  The tail is
+ * zero-padded to a multiple of group_size exactly as the reference does.
+ * codes: n uint8 (one code per byte, the reference's unpacked layout);
+ * scales/zps: ceil(n/group_size) entries.
+ */
+int hkv_quantize_groups(const void* x, int32_t dtype, int64_t n, int32_t group_size,
+                        uint8_t* codes, float* scales, uint8_t* zps, void* stream);
+
+/*
+ * KVCompressor.decompress (kv_compressor.py:119-132):
+ * out[i] = dtype((float(codes[i]) - float(zps[g])) * scales[g]), g = i / group_size.
+ */
+int hkv_dequantize_groups(const uint8_t* codes, const float* scales, const uint8_t* zps,
+                          int64_t n, int32_t group_size, void* out, int32_t out_dtype,
+                          void* stream);
+
+/*
+ * Quantize `num_tokens` consecutive tokens of every sequence and pack them into
+ * INT4 block records (the quantize+pack append kernel).  Token t of sequence b
+ * (source K/V at k + b*src_stride_b + h*src_stride_h + t*src_stride_t) goes to
+ * INT4 slot p = start_pos[b] + t: record block_table[b*bt_stride + p/16], row p%16.
+ * Rows of a block outside the written range keep their contents.
+ */
+typedef struct HkvPackArgs {
+    const void* k;
+    const void* v;
+    int32_t dtype;                 /* F16 or BF16 */
+    int64_t src_stride_b, src_stride_h, src_stride_t;   /* elements */
+    int32_t batch, num_kv_heads, head_dim, num_tokens;
+    const int32_t* start_pos;      /* [batch], device */
+    const int32_t* block_table;    /* [batch][bt_stride], device */
+    int32_t bt_stride;
+    uint8_t* pool;                 /* block records */
+    int64_t pool_blocks;
+    int32_t* err_flag;             /* optional device int: bit 0 = a block id outside the pool,
+                                      bit 1 = a slot beyond the block table row (nothing written) */
+} HkvPackArgs;
+
+int hkv_pack_tokens(const HkvPackArgs* args, void* stream);
+
+/*
+ * Pack tokens that are already quantized in the reference layout (one code per
+ * byte, per-token scale and zero point, as fused_dequant_attn_decode's
+ * k_data/k_scales/k_zps, kernels/fused_dequant_attn.py:301-310) into block
+ * records, with the same placement rules as hkv_pack_tokens.  Zero points may
+ * be uint8 (HKV_DTYPE_U8) or float32 holding integers (HKV_DTYPE_F32).
+ */
+typedef struct HkvRepackArgs {
+    const uint8_t* k_codes;
+    const uint8_t* v_codes;
+    int64_t code_stride_b, code_stride_h, code_stride_t;     /* bytes; dims contiguous */
+    const float* k_scales;
+    const float* v_scales;
+    const void* k_zps;
+    const void* v_zps;
+    int32_t zp_dtype;
+    int64_t meta_stride_b, meta_stride_h, meta_stride_t;     /* elements */
+    int32_t batch, num_kv_heads, head_dim, num_tokens;
+    const int32_t* start_pos;
+    const int32_t* block_table;
+    int32_t bt_stride;
+    uint8_t* pool;
+    int64_t pool_blocks;
+    int32_t* err_flag;
+} HkvRepackArgs;
+
+int hkv_repack_codes(const HkvRepackArgs* args, void* stream);
+
+/*
+ * Unpack INT4 slots [0, num_tokens) of one sequence into the reference's
+ * layout: codes [H][num_tokens][128] uint8, scales/zps [H*num_tokens]
+ * (flattened (head, token) order, as compress() of a [1,H,T,128] chunk).
+ * Any of codes/scales/zps may be NULL.
+ */
+int hkv_unpack_tokens(const uint8_t* pool, int64_t pool_blocks, const int32_t* block_table,
+                      int32_t num_kv_heads, int32_t head_dim, int32_t num_tokens,
+                      int32_t which /* 0 = K, 1 = V */,
+                      uint8_t* codes, float* scales, uint8_t* zps, void* stream);
+
+/*
+ * Write `num_tokens` fp16/bf16 tokens into an fp16 zone (sink / recent window /
+ * heavy hitters).  Token t of sequence b goes to slot slot_start[b] + t (mod
+ * capacity when `ring` != 0).  K rows are copied; V goes to transposed tiles.
+ * Source dtype must match the zone dtype (fp16).
+ */
+typedef struct HkvZoneWriteArgs {
+    const uint16_t* k;
+    const uint16_t* v;
+    int64_t src_stride_b, src_stride_h, src_stride_t;
+    int32_t batch, num_kv_heads, head_dim, num_tokens;
+    const int32_t* slot_start;     /* [batch], device */
+    int32_t capacity;              /* slots per (b,h); multiple of 16 */
+    int32_t ring;
+    uint16_t* zone_k;              /* [batch][H][capacity][128] */
+    uint16_t* zone_v;              /* [batch][H][capacity/16][4096 B tiles] */
+} HkvZoneWriteArgs;
+
+int hkv_zone_write(const HkvZoneWriteArgs* args, void* stream);
+
+/* Read slots [0,n) of an fp16 zone back as row-major K and V [batch][H][n][128]. */
+int hkv_zone_read(const uint16_t* zone_k, const uint16_t* zone_v, int32_t batch,
+                  int32_t num_kv_heads, int32_t head_dim, int32_t capacity, int32_t n,
+                  uint16_t* out_k, uint16_t* out_v, void* stream);
+
+/*
+ * Split-K decode attention over [fp16 zones || INT4 pool] for one query token per
+ * sequence (fused_dequant_attn_decode with GQA: q head i uses kv head i / n_rep,
+ * n_rep = num_q_heads / num_kv_heads).  One launch: partial results of the splits
+ * are combined in-kernel by the last workgroup of each (sequence, kv head).
+ * out = softmax(q K^T * sm_scale) V  over every valid token, fp16, fp32 accumulation.
+ */
+typedef struct HkvF16Zone {
+    const uint16_t* k;             /* [batch][H][capacity][128] */
+    const uint16_t* v;             /* transposed tiles */
+    int32_t capacity;              /* multiple of 16 */
+    int32_t max_len;               /* upper bound of lens[] (sizes the grid) */
+    const int32_t* lens;           /* [batch] device; NULL -> every sequence has max_len */
+} HkvF16Zone;
+
+typedef struct HkvDecodeArgs {
+    int32_t batch, num_q_heads, num_kv_heads, head_dim;
+    float sm_scale;
+    const uint16_t* q;             /* fp16 [batch][num_q_heads][128] with strides below */
+    int64_t q_stride_b, q_stride_h;
+    int32_t num_f16_zones;
+    HkvF16Zone f16[HKV_MAX_F16_ZONES];
+    const uint8_t* pool;           /* INT4 block records (may be NULL if int4_max_len == 0) */
+    int64_t pool_blocks;
+    const int32_t* block_table;    /* [batch][bt_stride] */
+    int32_t bt_stride;
+    const int32_t* int4_lens;      /* [batch] device; NULL -> int4_max_len */
+    int32_t int4_max_len;
+    uint16_t* out;                 /* fp16 [batch][num_q_heads][128] */
+    int64_t out_stride_b, out_stride_h;
+    void* workspace;               /* hkv_decode_workspace_bytes(); zero-filled once before first use */
+    size_t workspace_bytes;
+    int32_t splits_hint;           /* 0 = auto */
+} HkvDecodeArgs;
+
+size_t hkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t int4_max_len,
+                                  const int32_t* f16_max_lens, int32_t num_f16_zones);
+
+int hkv_decode_attn(const HkvDecodeArgs* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HETEROKV_H */

@@ -1,0 +1,109 @@
+"""The C-ABI library loads and exports every symbol include/heterokv.h declares;
+argument errors come back as return codes with a message.  No GPU needed."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "heterokv.h")
+
+
+def _declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(hkv_[a-z0-9_]+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from heterokv import _lib
+    return _lib.load()
+
+
+def test_header_symbols_exported(lib):
+    names = _declared_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+    from heterokv import _lib
+    assert sorted(n for n, _, _ in _lib.SYMBOLS) == names
+
+
+def test_version_and_record_size(lib):
+    assert lib.hkv_abi_version() == 1
+    assert lib.hkv_block_bytes(8, 128) == 17664
+    assert lib.hkv_block_bytes(4, 128) == 8832
+    assert lib.hkv_block_bytes(8, 64) == -1
+
+
+def test_struct_layouts_match_c_compiler(tmp_path):
+    """Every ctypes mirror has the size and field offsets gcc gives the C structs."""
+    import shutil
+    import subprocess
+    from heterokv import _lib
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    structs = {"HkvPackArgs": _lib.PackArgs, "HkvRepackArgs": _lib.RepackArgs,
+               "HkvZoneWriteArgs": _lib.ZoneWriteArgs, "HkvF16Zone": _lib.F16Zone,
+               "HkvDecodeArgs": _lib.DecodeArgs}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "%s"' % HEADER, "int main(void){"]
+    for cname, py in structs.items():
+        lines.append('printf("%s size %%zu\\n", sizeof(%s));' % (cname, cname))
+        for fname, _ in py._fields_:
+            lines.append('printf("%s %s %%zu\\n", offsetof(%s, %s));' % (cname, fname, cname, fname))
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], check=True, stdout=subprocess.PIPE, text=True).stdout.split("\n")
+    got = {}
+    for ln in out:
+        if ln.strip():
+            a, b, c = ln.split()
+            got[(a, b)] = int(c)
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for fname, _ in py._fields_:
+            assert got[(cname, fname)] == getattr(py, fname).offset, (cname, fname)
+
+
+def test_argument_errors_are_reported(lib):
+    rc = lib.hkv_quantize_groups(None, 0, 10, 0, None, None, None, None)
+    assert rc == -1
+    assert b"group_size" in lib.hkv_last_error()
+    rc = lib.hkv_quantize_groups(None, 7, 10, 128, None, None, None, None)
+    assert rc == -1 and b"dtype" in lib.hkv_last_error()
+    assert lib.hkv_quantize_groups(None, 0, 0, 128, None, None, None, None) == 0
+    assert lib.hkv_last_error() == b""
+
+
+def test_decode_argument_errors(lib):
+    from heterokv import _lib
+    a = _lib.DecodeArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = 1, 32, 8, 64
+    assert lib.hkv_decode_attn(ctypes.byref(a), None) == -4
+    a.head_dim = 128
+    a.num_q_heads = 30
+    assert lib.hkv_decode_attn(ctypes.byref(a), None) == -1
+    a.num_q_heads = 32 * 8 * 4
+    assert lib.hkv_decode_attn(ctypes.byref(a), None) == -4  # n_rep > 16
+    # workspace too small -> capacity error, before any launch
+    a.num_q_heads = 32
+    a.q = a.out = a.workspace = 4096
+    a.workspace_bytes = 16
+    a.num_f16_zones = 1
+    a.f16[0] = _lib.F16Zone(k=4096, v=4096, capacity=64, max_len=64, lens=None)
+    assert lib.hkv_decode_attn(ctypes.byref(a), None) == -3
+    assert b"workspace" in lib.hkv_last_error()
+    a.f16[0] = _lib.F16Zone(k=4096, v=4096, capacity=64, max_len=80, lens=None)
+    assert lib.hkv_decode_attn(ctypes.byref(a), None) == -1
+
+
+def test_workspace_size(lib):
+    from heterokv import ops
+    n = ops.decode_workspace_bytes(1, 32, 8, 28608, [64, 4096])
+    # 224 INT4 units + 2 + 128 fp16 units = 354 units -> 89 splits of 4 waves
+    assert n == 256 + 256 + 8 * 89 * 4 * 130 * 4

@@ -1,0 +1,160 @@
+"""GPU parity: the quantize+pack append kernel (hkv_pack_tokens), the reference-layout
+repacker and unpacker, and the fp16 zone writer, byte for byte against the oracle's
+compressor and its restatement of the documented record layout."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import compressor as oc
+from oracle import pool_format as pf
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _expected_pool(k, v, start, bt_row, num_blocks):
+    """Records the pool must hold after packing k, v [H, T, 128] (fp16 numpy) at INT4
+    slot `start` of a sequence whose block table row is bt_row (all else zero)."""
+    H, T, _ = k.shape
+    kc, ks, kz = oc.compress(k, 128)
+    vc, vs, vz = oc.compress(v, 128)
+    ks, kz, vs, vz = ks.reshape(H, T), kz.reshape(H, T), vs.reshape(H, T), vz.reshape(H, T)
+    rb = pf.record_bytes(H)
+    pool = np.zeros((num_blocks, rb), dtype=np.uint8)
+    nlb = (start + T + 15) // 16
+    for lb in range(start // 16, nlb):
+        lo = max(start, lb * 16) - lb * 16
+        hi = min(start + T, lb * 16 + 16) - lb * 16
+        KC = np.zeros((H, 16, 128), np.uint8)
+        VC = np.zeros((H, 16, 128), np.uint8)
+        KS = np.zeros((H, 16), np.float32)
+        VS = np.zeros((H, 16), np.float32)
+        KZ = np.zeros((H, 16), np.uint8)
+        VZ = np.zeros((H, 16), np.uint8)
+        t0 = lb * 16 + lo - start
+        t1 = lb * 16 + hi - start
+        KC[:, lo:hi] = kc[:, t0:t1]
+        VC[:, lo:hi] = vc[:, t0:t1]
+        KS[:, lo:hi] = ks[:, t0:t1]
+        VS[:, lo:hi] = vs[:, t0:t1]
+        KZ[:, lo:hi] = kz[:, t0:t1]
+        VZ[:, lo:hi] = vz[:, t0:t1]
+        pool[bt_row[lb]] = pf.build_record(KC, VC, KS, VS, KZ, VZ)
+    return pool, (kc, ks.reshape(-1), kz.reshape(-1)), (vc, vs.reshape(-1), vz.reshape(-1))
+
+
+def _rand_kv(seed, H, T):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn((1, H, T, 128), generator=g)
+    k[..., [7, 31, 64, 100]] *= 8
+    v = torch.randn((1, H, T, 128), generator=g)
+    return k.half(), v.half()
+
+
+@pytest.mark.parametrize("H,T,start", [(8, 100, 5), (8, 4096, 0), (4, 33, 16), (2, 1, 31), (8, 16, 0)])
+def test_pack_tokens_bytes(H, T, start):
+    print("case: pack_tokens H=%d T=%d start=%d" % (H, T, start), flush=True)
+    from heterokv import ops
+    k, v = _rand_kv(H * 1000 + T, H, T)
+    nlb = (start + T + 15) // 16
+    nblocks = nlb + 3
+    perm = torch.randperm(nblocks, generator=torch.Generator().manual_seed(T))[:nlb].to(torch.int32)
+    pool = ops.Int4Pool(nblocks, H, DEV)
+    ops.pack_tokens(pool, k.to(DEV), v.to(DEV), torch.tensor([start], dtype=torch.int32), perm[None])
+    exp, kref, vref = _expected_pool(k[0].numpy(), v[0].numpy(), start, perm.numpy(), nblocks)
+    got = pool.data.cpu().numpy()
+    assert np.array_equal(got, exp)
+    pool.check_errors()
+    # unpack the sequence's INT4 slots [start, start+T) back to the reference layout
+    for which, ref in ((0, kref), (1, vref)):
+        codes, scales, zps = ops.unpack_tokens(pool, perm, start + T, which)
+        assert np.array_equal(codes[:, start:].cpu().numpy(), ref[0])
+        assert np.array_equal(scales.reshape(H, -1)[:, start:].cpu().numpy().reshape(-1), ref[1])
+        assert np.array_equal(zps.reshape(H, -1)[:, start:].cpu().numpy().reshape(-1), ref[2])
+
+
+def test_incremental_append_equals_one_shot():
+    print("case: pack in pieces 37 + 1 + 1 + 90 vs one shot", flush=True)
+    from heterokv import ops
+    H, T = 8, 129
+    k, v = _rand_kv(7, H, T)
+    nb = (T + 15) // 16
+    bt = torch.arange(nb, dtype=torch.int32)[None]
+    one = ops.Int4Pool(nb, H, DEV)
+    ops.pack_tokens(one, k.to(DEV), v.to(DEV), [0], bt)
+    inc = ops.Int4Pool(nb, H, DEV)
+    pos = 0
+    for n in (37, 1, 1, 90):
+        ops.pack_tokens(inc, k[:, :, pos:pos + n].to(DEV), v[:, :, pos:pos + n].to(DEV), [pos], bt)
+        pos += n
+    assert torch.equal(one.data, inc.data)
+
+
+def test_repack_reference_layout_equals_pack():
+    print("case: repack_codes(oracle codes) == pack_tokens", flush=True)
+    from heterokv import ops
+    H, T = 8, 200
+    k, v = _rand_kv(11, H, T)
+    nb = (T + 15) // 16
+    bt = torch.arange(nb, dtype=torch.int32)[None]
+    a = ops.Int4Pool(nb, H, DEV)
+    ops.pack_tokens(a, k.to(DEV), v.to(DEV), [0], bt)
+    kc, ks, kz = oc.compress(k[0].numpy(), 128)
+    vc, vs, vz = oc.compress(v[0].numpy(), 128)
+    b = ops.Int4Pool(nb, H, DEV)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    ops.repack_codes(b, t(kc)[None], t(vc)[None], t(ks).reshape(1, H, T), t(vs).reshape(1, H, T),
+                     t(kz).reshape(1, H, T).float(), t(vz).reshape(1, H, T).float(), [0], bt)
+    assert torch.equal(a.data, b.data)
+
+
+def test_batched_pack_two_sequences():
+    print("case: batch of 2 with different starts", flush=True)
+    from heterokv import ops
+    H, T = 4, 40
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn((2, H, T, 128), generator=g).half()
+    v = torch.randn((2, H, T, 128), generator=g).half()
+    starts = [3, 20]
+    bt = torch.tensor([[0, 1, 2, 3, 4], [9, 8, 7, 6, 5]], dtype=torch.int32)
+    pool = ops.Int4Pool(10, H, DEV)
+    ops.pack_tokens(pool, k.to(DEV), v.to(DEV), torch.tensor(starts, dtype=torch.int32), bt)
+    got = pool.data.cpu().numpy()
+    for b in range(2):
+        exp, _, _ = _expected_pool(k[b].numpy(), v[b].numpy(), starts[b], bt[b].numpy(), 10)
+        used = sorted(set(bt[b, starts[b] // 16:(starts[b] + T + 15) // 16].tolist()))
+        assert np.array_equal(got[used], exp[used])
+
+
+def test_out_of_range_block_id_is_flagged_not_written():
+    print("case: bad block id", flush=True)
+    from heterokv import HeteroKVError, ops
+    k, v = _rand_kv(5, 2, 16)
+    pool = ops.Int4Pool(2, 2, DEV)
+    ops.pack_tokens(pool, k.to(DEV), v.to(DEV), [0], torch.tensor([[7]], dtype=torch.int32))
+    assert int(pool.data.abs().sum().item()) == 0
+    with pytest.raises(HeteroKVError):
+        pool.check_errors()
+
+
+def test_f16_zone_write_read_and_ring():
+    print("case: fp16 zone write/read", flush=True)
+    from heterokv import ops
+    H, cap = 4, 48
+    g = torch.Generator().manual_seed(9)
+    k = torch.randn((1, H, 40, 128), generator=g).half()
+    v = torch.randn((1, H, 40, 128), generator=g).half()
+    z = ops.F16Zone(1, H, cap, DEV)
+    z.write(k.to(DEV), v.to(DEV), [0])
+    rk, rv = z.read(40)
+    assert torch.equal(rk.cpu(), k) and torch.equal(rv.cpu(), v)
+    # V tiles follow the documented [g][c][n][i] layout
+    tile = z.v[0, 1, 0].cpu().reshape(4, 16, 8, 4).numpy()
+    assert np.array_equal(tile, pf.v_tile(v[0, 1, :16].numpy()))
+    # ring: 20 more tokens at logical slot 40 wrap to slots 40..47, 0..11
+    k2 = torch.randn((1, H, 20, 128), generator=g).half()
+    v2 = torch.randn((1, H, 20, 128), generator=g).half()
+    z.write(k2.to(DEV), v2.to(DEV), [40], ring=True)
+    rk, rv = z.read(48)
+    assert torch.equal(rk[0, :, 40:48].cpu(), k2[0, :, :8]) and torch.equal(rk[0, :, :12].cpu(), k2[0, :, 8:])
+    assert torch.equal(rv[0, :, 12:40].cpu(), v[0, :, 12:40])
