@@ -120,6 +120,9 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", type=float, default=0.0,
+                    help="run only torch's device copy of this many MB (20 launches) so that rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the decode path shards by kv head or "
@@ -127,6 +130,19 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration > 0:
+        dev = torch.device("cuda:0")
+        n = int(args.copy_calibration * 1e6) // 4
+        src = torch.ones(n, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read_per_launch": n * 4,
+                          "copy_calibration_bytes_written_per_launch": n * 4, "launches": 20}), flush=True)
+        return
+
     from heterokv import ops
 
     dev = torch.device("cuda:0")

@@ -18,11 +18,15 @@
 // pair (1024 + zp) leaves the exact integer code - zp.  The K scale multiplies
 // the score, the V scale multiplies the probability, both in fp32.
 //
-// Work split: a "unit" (8 INT4 blocks or 2 fp16 tiles, ~17 KB) per wave, 4 waves
-// per workgroup; a workgroup's waves merge through LDS, workgroups of one
-// (sequence, kv head) merge through a workspace, and the last workgroup to
-// finish (atomic ticket) writes the output.  Workgroup ids interleave the
-// (sequence, kv head) pairs so that all splits of a pair land on one XCD.
+// Work split.  Every (sequence, kv head) pair is cut into S byte-balanced
+// ranges (S chosen so that S x pairs is about one workgroup per CU); a range is
+// a run of items in the order [INT4 blocks | fp16 zone tiles], and each of the
+// 8 waves of the workgroup takes a contiguous piece of it.  Waves merge through
+// LDS, workgroups through a workspace: the last workgroup of a pair to finish
+// (atomic ticket after a release fence) merges the S partial states with
+// independent loads and writes the output, so the whole op is one launch.
+// Workgroup ids interleave the pairs so that all ranges of a pair land on one
+// XCD (dispatch is round-robin over XCDs by workgroup id).
 #include "hkv_internal.h"
 
 #include <math.h>
@@ -37,21 +41,15 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 4;
-constexpr int kUnitInt4Blocks = 8;
-constexpr int kUnitF16Tiles = 2;
-constexpr int kPartStride = kHeadDim + 2;  // o[128], m, l
-constexpr int kPrefetch = 3;
+constexpr int kWaves = 8;                 // waves per workgroup
+constexpr int kThreads = kWaves * 64;
+constexpr int kPartStride = kHeadDim + 4;  // o[128], m, l, 2 pad (16-byte rows)
+constexpr int kPrefetch = 2;               // INT4 block pairs in flight per wave
+constexpr int kMaxSplits = 64;
 constexpr float kLog2e = 1.4426950408889634f;
-
-__host__ __device__ inline int units_int4(int len) {
-    const int nb = (len + kBlockTokens - 1) / kBlockTokens;
-    return (nb + kUnitInt4Blocks - 1) / kUnitInt4Blocks;
-}
-__host__ __device__ inline int units_f16(int len) {
-    const int nt = (len + kBlockTokens - 1) / kBlockTokens;
-    return (nt + kUnitF16Tiles - 1) / kUnitF16Tiles;
-}
+// Bytes one kv head reads per item (the weights that balance the ranges).
+constexpr int64_t kInt4ItemBytes = kBlockTokens * (kHeadDim / 2 + 5) * 2;   // 2208
+constexpr int64_t kF16ItemBytes = kBlockTokens * kHeadDim * 2 * 2;           // 8192
 
 struct ZoneP {
     const uint16_t* k;
@@ -82,6 +80,18 @@ struct DecodeParams {
     int max_splits;
 };
 
+// Partial states cross workgroups (and XCDs) through agent-scope relaxed atomic
+// loads and stores: those are coherent at the device level by themselves, so the
+// hand-off needs no L2 writeback or invalidate.  Ordering comes from waiting for
+// the stores to complete (s_waitcnt) before the workgroup barrier and the ticket
+// increment, and from the ticket's return value before the loads.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 
 // (w >> 4i) & 0x000F000F | 0x6400_6400  ->  fp16 pair (1024 + x_2i, 1024 + x_2i+1)
@@ -103,13 +113,9 @@ struct F16Tile {
     u4 v[4];      // V^T tile: halves [n][i] for tokens 4g+i, dims c+16n
 };
 
-__device__ __forceinline__ void load_int4(const DecodeParams& p, int b, int h, int lb, int c, int g,
-                                          Int4Blk& d) {
-    int phys = p.bt[(int64_t)b * p.bt_stride + lb];
-    if (phys < 0 || (int64_t)phys >= p.pool_blocks) {
-        if (p.err) atomicOr(p.err, 1);
-        phys = 0;
-    }
+// `phys` is the (already validated) physical block id; every load of a block is
+// issued back to back so several blocks stay in flight.
+__device__ __forceinline__ void load_int4(const DecodeParams& p, int h, int phys, int c, int g, Int4Blk& d) {
     const int H = p.Hkv;
     const uint8_t* rec = p.pool + (int64_t)phys * ((int64_t)H * 2208);
     d.k = *(const u4*)(rec + h * kHeadCodeBytes + c * kCodeRowBytes + g * 16);
@@ -118,6 +124,17 @@ __device__ __forceinline__ void load_int4(const DecodeParams& p, int b, int h, i
     d.vs = *(const f4*)(rec + (int64_t)H * 2112 + h * 64 + g * 16);
     d.kz = rec[(int64_t)H * 2176 + h * 16 + c];
     d.vz = *(const uint32_t*)(rec + (int64_t)H * 2192 + h * 16 + g * 4);
+}
+
+// Block ids of logical blocks [lb0, lb0 + 64) of sequence b, one per lane, with
+// out-of-range ids replaced by 0 and reported once through p.err.
+__device__ __forceinline__ int load_block_ids(const DecodeParams& p, int b, int lb0, int lb1, int lane) {
+    int id = 0;
+    if (lb0 + lane < lb1) id = p.bt[(int64_t)b * p.bt_stride + lb0 + lane];
+    const bool bad = (lb0 + lane < lb1) && (id < 0 || (int64_t)id >= p.pool_blocks);
+    if (bad) id = 0;
+    if (__ballot(bad) && lane == 0 && p.err) atomicOr(p.err, 1);
+    return id;
 }
 
 __device__ __forceinline__ void load_f16(const ZoneP& z, int64_t bh, int tile, int c, int g, F16Tile& d) {
@@ -131,16 +148,23 @@ __device__ __forceinline__ void load_f16(const ZoneP& z, int64_t bh, int tile, i
     }
 }
 
-// Online-softmax update shared by both tile kinds.  s[] are log2-domain scores
-// (-inf for masked tokens); returns the probabilities for tokens 4g..4g+3.
-__device__ __forceinline__ void softmax_update(float (&s)[4], f4 (&acc)[8], float& m, float& l,
-                                               float (&pr)[4]) {
-    float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float m_new = fmaxf(m, mt);
-    if (__ballot(m_new > m)) {
-        const float alpha = (m_new > m) ? exp2f(m - m_new) : 1.0f;
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Online-softmax update for N log2-domain scores per lane (-inf = masked).  The
+// running max m is kept equal on the 4 lanes of a head; the cross-lane reduction
+// and the rescale of acc/l run only when some lane sees a score above it, so the
+// common step has no shuffle at all.  Returns exp2(s - m) in pr.
+template <int N>
+__device__ __forceinline__ void softmax_update(const float (&s)[N], f4 (&acc)[8], float& m, float& l,
+                                               float (&pr)[N]) {
+    float mt = s[0];
+#pragma unroll
+    for (int i = 1; i < N; ++i) mt = fmaxf(mt, s[i]);
+    if (__ballot(mt > m)) {
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float m_new = fmaxf(m, mt);
+        const float alpha = (m_new > m) ? fast_exp2(m - m_new) : 1.0f;
 #pragma unroll
         for (int n = 0; n < 8; ++n) acc[n] *= alpha;
         l *= alpha;
@@ -148,53 +172,85 @@ __device__ __forceinline__ void softmax_update(float (&s)[4], f4 (&acc)[8], floa
     }
     const float msafe = (m == -INFINITY) ? 0.0f : m;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        pr[v] = exp2f(s[v] - msafe);
+    for (int v = 0; v < N; ++v) {
+        pr[v] = fast_exp2(s[v] - msafe);
         l += pr[v];
     }
 }
 
-__device__ __forceinline__ void step_int4(const Int4Blk& d, int nvalid, int g, const h8 (&qf)[4],
-                                          float scale_log2, f4 (&acc)[8], float& m, float& l) {
-    // ---- scores
-    const _Float16 kzz = (_Float16)(1024.0f + (float)d.kz);
-    const h2 kz2 = {kzz, kzz};
-    const uint32_t kw[4] = {d.k.x, d.k.y, d.k.z, d.k.w};
-    f4 S = {0.f, 0.f, 0.f, 0.f};
+// K operand of one packed word (dims 8j..8j+7 of token lane%16): exact code - zp.
+__device__ __forceinline__ h8 k_operand(uint32_t w, h2 kz2) {
+    const h2 a0 = as_h2(nib_pair(w, 0)) - kz2;
+    const h2 a1 = as_h2(nib_pair(w, 1)) - kz2;
+    const h2 a2 = as_h2(nib_pair(w, 2)) - kz2;
+    const h2 a3 = as_h2(nib_pair(w, 3)) - kz2;
+    return h8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+}
+
+// Two INT4 blocks (32 tokens) per step: the two QK chains interleave, and one
+// 16x16x32 MFMA per 16 dims does PV for both blocks (k slots 0..3 = block A
+// tokens 4g..4g+3, slots 4..7 = block B tokens 4g..4g+3).
+__device__ __forceinline__ void step_int4_pair(const Int4Blk& A, const Int4Blk& B, int nA, int nB, int g,
+                                               const h8 (&qf)[4], float scale_log2, f4 (&acc)[8], float& m,
+                                               float& l) {
+    const _Float16 kzA = (_Float16)(1024.0f + (float)A.kz), kzB = (_Float16)(1024.0f + (float)B.kz);
+    const h2 kA2 = {kzA, kzA}, kB2 = {kzB, kzB};
+    const uint32_t kwA[4] = {A.k.x, A.k.y, A.k.z, A.k.w};
+    const uint32_t kwB[4] = {B.k.x, B.k.y, B.k.z, B.k.w};
+    f4 SA = {0.f, 0.f, 0.f, 0.f}, SB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const h2 a0 = as_h2(nib_pair(kw[j], 0)) - kz2;
-        const h2 a1 = as_h2(nib_pair(kw[j], 1)) - kz2;
-        const h2 a2 = as_h2(nib_pair(kw[j], 2)) - kz2;
-        const h2 a3 = as_h2(nib_pair(kw[j], 3)) - kz2;
-        const h8 a = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
-        S = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[j], S, 0, 0, 0);
+        SA = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand(kwA[j], kA2), qf[j], SA, 0, 0, 0);
+        SB = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand(kwB[j], kB2), qf[j], SB, 0, 0, 0);
     }
-    float s[4];
+    float s[8];
+    const bool full = nA >= kBlockTokens && nB >= kBlockTokens;
+    if (full) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) s[v] = (4 * g + v < nvalid) ? S[v] * (d.ks[v] * scale_log2) : -INFINITY;
-    float pr[4];
-    softmax_update(s, acc, m, l, pr);
-    // ---- P' = p * v_scale (exactly 0 for masked tokens)
-    h4 P;
+        for (int v = 0; v < 4; ++v) {
+            s[v] = SA[v] * (A.ks[v] * scale_log2);
+            s[4 + v] = SB[v] * (B.ks[v] * scale_log2);
+        }
+    } else {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) P[v] = (_Float16)((4 * g + v < nvalid) ? pr[v] * d.vs[v] : 0.0f);
-    const _Float16 z0 = (_Float16)(1024.0f + (float)(d.vz & 0xff));
-    const _Float16 z1 = (_Float16)(1024.0f + (float)((d.vz >> 8) & 0xff));
-    const _Float16 z2 = (_Float16)(1024.0f + (float)((d.vz >> 16) & 0xff));
-    const _Float16 z3 = (_Float16)(1024.0f + (float)(d.vz >> 24));
-    const h2 zz01 = {z0, z1}, zz23 = {z2, z3};
-    const uint32_t vw[4] = {d.v.x, d.v.y, d.v.z, d.v.w};
+        for (int v = 0; v < 4; ++v) {
+            s[v] = (4 * g + v < nA) ? SA[v] * (A.ks[v] * scale_log2) : -INFINITY;
+            s[4 + v] = (4 * g + v < nB) ? SB[v] * (B.ks[v] * scale_log2) : -INFINITY;
+        }
+    }
+    float pr[8];
+    softmax_update<8>(s, acc, m, l, pr);
+    h8 P;
+    if (full) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            P[v] = (_Float16)(pr[v] * A.vs[v]);
+            P[4 + v] = (_Float16)(pr[4 + v] * B.vs[v]);
+        }
+    } else {
+        // masked tokens get exactly 0 (their scale may be anything)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            P[v] = (_Float16)((4 * g + v < nA) ? pr[v] * A.vs[v] : 0.0f);
+            P[4 + v] = (_Float16)((4 * g + v < nB) ? pr[4 + v] * B.vs[v] : 0.0f);
+        }
+    }
+    const h2 zA01 = {(_Float16)(1024.0f + (float)(A.vz & 0xff)), (_Float16)(1024.0f + (float)((A.vz >> 8) & 0xff))};
+    const h2 zA23 = {(_Float16)(1024.0f + (float)((A.vz >> 16) & 0xff)), (_Float16)(1024.0f + (float)(A.vz >> 24))};
+    const h2 zB01 = {(_Float16)(1024.0f + (float)(B.vz & 0xff)), (_Float16)(1024.0f + (float)((B.vz >> 8) & 0xff))};
+    const h2 zB23 = {(_Float16)(1024.0f + (float)((B.vz >> 16) & 0xff)), (_Float16)(1024.0f + (float)(B.vz >> 24))};
+    const uint32_t vwA[4] = {A.v.x, A.v.y, A.v.z, A.v.w};
+    const uint32_t vwB[4] = {B.v.x, B.v.y, B.v.z, B.v.w};
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
-        const h2 e0 = as_h2(nib_pair(vw[mm], 0)) - zz01;
-        const h2 e1 = as_h2(nib_pair(vw[mm], 1)) - zz23;
-        const h2 o0 = as_h2(nib_pair(vw[mm], 2)) - zz01;
-        const h2 o1 = as_h2(nib_pair(vw[mm], 3)) - zz23;
-        const h4 A0 = {e0[0], e0[1], e1[0], e1[1]};
-        const h4 A1 = {o0[0], o0[1], o1[0], o1[1]};
-        acc[2 * mm] = __builtin_amdgcn_mfma_f32_16x16x16f16(A0, P, acc[2 * mm], 0, 0, 0);
-        acc[2 * mm + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A1, P, acc[2 * mm + 1], 0, 0, 0);
+        const h2 a0 = as_h2(nib_pair(vwA[mm], 0)) - zA01, a1 = as_h2(nib_pair(vwA[mm], 1)) - zA23;
+        const h2 a2 = as_h2(nib_pair(vwA[mm], 2)) - zA01, a3 = as_h2(nib_pair(vwA[mm], 3)) - zA23;
+        const h2 b0 = as_h2(nib_pair(vwB[mm], 0)) - zB01, b1 = as_h2(nib_pair(vwB[mm], 1)) - zB23;
+        const h2 b2 = as_h2(nib_pair(vwB[mm], 2)) - zB01, b3 = as_h2(nib_pair(vwB[mm], 3)) - zB23;
+        const h8 V0 = {a0[0], a0[1], a1[0], a1[1], b0[0], b0[1], b1[0], b1[1]};   // dims c + 32mm
+        const h8 V1 = {a2[0], a2[1], a3[0], a3[1], b2[0], b2[1], b3[0], b3[1]};   // dims c + 32mm + 16
+        acc[2 * mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(V0, P, acc[2 * mm], 0, 0, 0);
+        acc[2 * mm + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(V1, P, acc[2 * mm + 1], 0, 0, 0);
     }
 }
 
@@ -207,7 +263,7 @@ __device__ __forceinline__ void step_f16(F16Tile& d, int nvalid, int g, const h8
 #pragma unroll
     for (int v = 0; v < 4; ++v) s[v] = (4 * g + v < nvalid) ? S[v] * scale_log2 : -INFINITY;
     float pr[4];
-    softmax_update(s, acc, m, l, pr);
+    softmax_update<4>(s, acc, m, l, pr);
     h4 P;
 #pragma unroll
     for (int v = 0; v < 4; ++v) P[v] = (_Float16)((4 * g + v < nvalid) ? pr[v] : 0.0f);
@@ -232,31 +288,62 @@ __device__ __forceinline__ void step_f16(F16Tile& d, int nvalid, int g, const h8
     }
 }
 
-__global__ __launch_bounds__(256) void decode_attn_kernel(DecodeParams p) {
+// Item layout of one (sequence, kv head): INT4 blocks [0, nb4), then the tiles
+// of zone 0, 1, 2.  first_item(x) = index of the first item whose byte offset
+// is >= x, so [first_item(a), first_item(b)) partitions the items.
+struct ItemMap {
+    int nb4;
+    int nt[HKV_MAX_F16_ZONES];
+    int nz;
+    __device__ int64_t total_bytes() const {
+        int64_t t = (int64_t)nb4 * kInt4ItemBytes;
+#pragma unroll
+        for (int z = 0; z < HKV_MAX_F16_ZONES; ++z) t += (int64_t)nt[z] * kF16ItemBytes;
+        return t;
+    }
+    __device__ int first_item(int64_t x) const {
+        const int64_t e4 = (int64_t)nb4 * kInt4ItemBytes;
+        if (x <= e4) return (int)((x + kInt4ItemBytes - 1) / kInt4ItemBytes);
+        int base = nb4;
+        int64_t off = e4;
+        int r = -1;
+#pragma unroll
+        for (int z = 0; z < HKV_MAX_F16_ZONES; ++z) {
+            const int64_t ez = off + (int64_t)nt[z] * kF16ItemBytes;
+            if (r < 0 && x <= ez) r = base + (int)((x - off + kF16ItemBytes - 1) / kF16ItemBytes);
+            base += nt[z];
+            off = ez;
+        }
+        return r < 0 ? base : r;
+    }
+};
+
+__global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const int BH = p.B * p.Hkv;
     const int bh = blockIdx.x % BH;
     const int split = blockIdx.x / BH;
+    const int nsplit = p.max_splits;
     const int b = bh / p.Hkv, h = bh % p.Hkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
     const int nrep = p.nrep;
 
     const int len4 = p.int4_lens ? min(max(p.int4_lens[b], 0), p.int4_max_len) : p.int4_max_len;
-    const int n4 = units_int4(len4);
-    int lenz[HKV_MAX_F16_ZONES], nzu[HKV_MAX_F16_ZONES];
-    int total = n4;
+    int lenz[HKV_MAX_F16_ZONES];
+    ItemMap im;
+    im.nb4 = (len4 + kBlockTokens - 1) / kBlockTokens;
+    im.nz = p.nz;
 #pragma unroll
     for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
         lenz[zi] = 0;
-        nzu[zi] = 0;
-        if (zi < p.nz) {
+        if (zi < p.nz)
             lenz[zi] = p.z[zi].lens ? min(max(p.z[zi].lens[b], 0), p.z[zi].max_len) : p.z[zi].max_len;
-            nzu[zi] = units_f16(lenz[zi]);
-            total += nzu[zi];
-        }
+        im.nt[zi] = (lenz[zi] + kBlockTokens - 1) / kBlockTokens;
     }
-    const int nsplit = max((total + kWaves - 1) / kWaves, 1);
-    if (split >= nsplit) return;
+    const int64_t total = im.total_bytes();
+    const int64_t r0 = total * split / nsplit, r1 = total * (split + 1) / nsplit;
+    const int64_t w0 = r0 + (r1 - r0) * wave / kWaves, w1 = r0 + (r1 - r0) * (wave + 1) / kWaves;
+    const int i0 = im.first_item(w0), i1 = im.first_item(w1);
 
     // q fragments: lane (c, g) holds q[head c][32g + 8j .. +8] for step j.
     h8 qf[4];
@@ -275,156 +362,228 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeParams p) {
     for (int n = 0; n < 8; ++n) acc[n] = f4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.0f;
 
-    int u = split * kWaves + wave;
-    if (u < n4) {
-        const int nb = (len4 + kBlockTokens - 1) / kBlockTokens;
-        const int lb0 = u * kUnitInt4Blocks;
-        const int lb1 = min(lb0 + kUnitInt4Blocks, nb);
-        Int4Blk buf[kPrefetch];
-#pragma unroll
-        for (int k = 0; k < kPrefetch; ++k)
-            if (lb0 + k < lb1) load_int4(p, b, h, lb0 + k, c, g, buf[k]);
-        for (int base = lb0; base < lb1; base += kPrefetch) {
+    // ---- INT4 blocks of this wave's piece, two per step.  Block ids come 64 at
+    // a time; the loop body is branch-free so the next kPrefetch pairs stay in
+    // flight: past the end it re-reads the last block (an in-bounds address) and
+    // runs with no valid token, which contributes nothing.
+    {
+        const int lb0 = i0, lb1 = min(i1, im.nb4);
+        for (int cb = lb0; cb < lb1; cb += 64) {
+            const int cn = min(64, lb1 - cb);
+            const int ids = load_block_ids(p, b, cb, cb + cn, lane);
+            Int4Blk bufA[kPrefetch], bufB[kPrefetch];
 #pragma unroll
             for (int k = 0; k < kPrefetch; ++k) {
-                const int lb = base + k;
-                if (lb < lb1) {
-                    step_int4(buf[k], min(kBlockTokens, len4 - lb * kBlockTokens), g, qf, p.scale_log2, acc, m, l);
-                    if (lb + kPrefetch < lb1) load_int4(p, b, h, lb + kPrefetch, c, g, buf[k]);
+                load_int4(p, h, __builtin_amdgcn_readlane(ids, min(2 * k, cn - 1)), c, g, bufA[k]);
+                load_int4(p, h, __builtin_amdgcn_readlane(ids, min(2 * k + 1, cn - 1)), c, g, bufB[k]);
+            }
+            for (int base = 0; base < cn; base += 2 * kPrefetch) {
+#pragma unroll
+                for (int k = 0; k < kPrefetch; ++k) {
+                    const int i = base + 2 * k;
+                    const int nA = (i < cn ? min(kBlockTokens, len4 - (cb + i) * kBlockTokens) : 0);
+                    const int nB = (i + 1 < cn ? min(kBlockTokens, len4 - (cb + i + 1) * kBlockTokens) : 0);
+                    step_int4_pair(bufA[k], bufB[k], nA, nB, g, qf, p.scale_log2, acc, m, l);
+                    load_int4(p, h, __builtin_amdgcn_readlane(ids, min(i + 2 * kPrefetch, cn - 1)), c, g, bufA[k]);
+                    load_int4(p, h, __builtin_amdgcn_readlane(ids, min(i + 2 * kPrefetch + 1, cn - 1)), c, g, bufB[k]);
                 }
             }
         }
-    } else {
-        u -= n4;
-        for (int zi = 0; zi < p.nz; ++zi) {
-            if (u < nzu[zi]) {
+    }
+    // ---- fp16 zone tiles of this wave's piece (same pipelining, depth 2)
+    {
+        int zbase = im.nb4;
+#pragma unroll
+        for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
+            const int t0 = max(i0 - zbase, 0), t1 = min(i1 - zbase, im.nt[zi]);
+            if (zi < p.nz && t0 < t1) {
                 const ZoneP& z = p.z[zi];
-                const int nt = (lenz[zi] + kBlockTokens - 1) / kBlockTokens;
-                const int t0 = u * kUnitF16Tiles;
-                const int t1 = min(t0 + kUnitF16Tiles, nt);
+                const int len = lenz[zi];
                 F16Tile buf[2];
-                if (t0 < t1) load_f16(z, bh, t0, c, g, buf[0]);
-                if (t0 + 1 < t1) load_f16(z, bh, t0 + 1, c, g, buf[1]);
+                load_f16(z, bh, t0, c, g, buf[0]);
+                load_f16(z, bh, min(t0 + 1, t1 - 1), c, g, buf[1]);
                 for (int base = t0; base < t1; base += 2) {
 #pragma unroll
                     for (int k = 0; k < 2; ++k) {
                         const int t = base + k;
-                        if (t < t1) {
-                            step_f16(buf[k], min(kBlockTokens, lenz[zi] - t * kBlockTokens), g, qf, p.scale_log2, acc, m, l);
-                            if (t + 2 < t1) load_f16(z, bh, t + 2, c, g, buf[k]);
-                        }
+                        step_f16(buf[k], t < t1 ? min(kBlockTokens, len - t * kBlockTokens) : 0, g, qf,
+                                 p.scale_log2, acc, m, l);
+                        load_f16(z, bh, min(t + 2, t1 - 1), c, g, buf[k]);
                     }
                 }
-                break;
             }
-            u -= nzu[zi];
+            zbase += im.nt[zi];
         }
     }
 
-    // ---- merge the waves of this workgroup
+    // ---- merge the waves of this workgroup through LDS
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
-    __shared__ float sm_o[kWaves][16][kHeadDim];
-    __shared__ float sm_m[kWaves][16], sm_l[kWaves][16];
+    extern __shared__ float smem[];
+    float* sm_o = smem;                                   // [kWaves][nrep][128]
+    float* sm_m = sm_o + kWaves * nrep * kHeadDim;        // [kWaves][nrep]
+    float* sm_l = sm_m + kWaves * 16;                     // [kWaves][nrep]
     __shared__ int sm_ticket;
     if (c < nrep) {
+        float* o = sm_o + (wave * nrep + c) * kHeadDim;
 #pragma unroll
         for (int n = 0; n < 8; ++n)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) sm_o[wave][c][16 * n + 4 * g + v] = acc[n][v];
+            for (int v = 0; v < 4; ++v) o[16 * n + 4 * g + v] = acc[n][v];
         if (g == 0) {
-            sm_m[wave][c] = m;
-            sm_l[wave][c] = l;
+            sm_m[wave * 16 + c] = m;
+            sm_l[wave * 16 + c] = l;
         }
     }
     __syncthreads();
 
     const int nout = nrep * kHeadDim;
-    if (nsplit == 1) {
-        for (int idx = threadIdx.x; idx < nout; idx += blockDim.x) {
-            const int hd = idx >> 7, d = idx & (kHeadDim - 1);
-            float M = -INFINITY;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][hd]);
-            float O = 0.f, L = 0.f;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                const float e = (sm_m[w][hd] == -INFINITY) ? 0.f : exp2f(sm_m[w][hd] - M);
-                O += sm_o[w][hd][d] * e;
-                L += sm_l[w][hd] * e;
-            }
-            p.out[(int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d] = f2h_rn(L > 0.f ? O / L : 0.f);
-        }
-        return;
-    }
-
-    float* part = p.partials + ((int64_t)bh * p.max_splits + split) * (nrep * kPartStride);
-    for (int idx = threadIdx.x; idx < nout; idx += blockDim.x) {
+    float* part = p.partials + ((int64_t)bh * nsplit + split) * (nrep * kPartStride);
+    for (int idx = threadIdx.x; idx < nout; idx += kThreads) {
         const int hd = idx >> 7, d = idx & (kHeadDim - 1);
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][hd]);
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w * 16 + hd]);
         float O = 0.f, L = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            const float e = (sm_m[w][hd] == -INFINITY) ? 0.f : exp2f(sm_m[w][hd] - M);
-            O += sm_o[w][hd][d] * e;
-            L += sm_l[w][hd] * e;
+            const float mw = sm_m[w * 16 + hd];
+            const float e = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+            O += sm_o[(w * nrep + hd) * kHeadDim + d] * e;
+            L += sm_l[w * 16 + hd] * e;
         }
-        part[hd * kPartStride + d] = O;
-        if (d == 0) {
-            part[hd * kPartStride + kHeadDim] = M;
-            part[hd * kPartStride + kHeadDim + 1] = L;
+        if (nsplit == 1) {
+            p.out[(int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d] = f2h_rn(L > 0.f ? O / L : 0.f);
+        } else {
+            st_agent(part + hd * kPartStride + d, O);
+            if (d == 0) {
+                st_agent(part + hd * kPartStride + kHeadDim, M);
+                st_agent(part + hd * kPartStride + kHeadDim + 1, L);
+            }
         }
     }
-    __threadfence();
+    if (nsplit == 1) return;
+    // every lane waits until its agent-coherent stores have completed, then the
+    // barrier makes that true for the whole workgroup before the ticket is taken
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
-    if (threadIdx.x == 0) sm_ticket = atomicAdd(&p.counters[bh], 1);
+    if (threadIdx.x == 0)
+        sm_ticket = __hip_atomic_fetch_add(&p.counters[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (sm_ticket != nsplit - 1) return;
-    __threadfence();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
-    // ---- last workgroup of this (sequence, kv head): merge every split.
-    const float* parts = p.partials + (int64_t)bh * p.max_splits * (nrep * kPartStride);
-    for (int idx = threadIdx.x; idx < nout; idx += blockDim.x) {
-        const int hd = idx >> 7, d = idx & (kHeadDim - 1);
-        float M = -INFINITY, O = 0.f, L = 0.f;
-        for (int s = 0; s < nsplit; ++s) {
-            const float* ps = parts + (int64_t)s * (nrep * kPartStride) + hd * kPartStride;
-            const float ms = ps[kHeadDim];
-            if (ms == -INFINITY) continue;
-            const float os = ps[d];
-            const float ls = ps[kHeadDim + 1];
-            if (ms > M) {
-                const float a = (M == -INFINITY) ? 0.f : exp2f(M - ms);
-                O *= a;
-                L *= a;
-                M = ms;
+    // ---- last workgroup of this pair: merge the nsplit partial states in one
+    // memory round trip.  Thread t owns float4 `u` of one head and the splits
+    // s = k, k + K, k + 2K, ... (K = threads per unit); all its loads are
+    // independent.  The K per-thread states then merge through LDS.
+    const float* parts = p.partials + (int64_t)bh * nsplit * (nrep * kPartStride);
+    const int units = nrep * (kHeadDim / 4);
+    const int K = kThreads / units;                  // >= 1 because nrep <= 16
+    float* sm = smem;                                // [K][units][6] = (M, L, O[4])
+    if (threadIdx.x < K * units) {
+        const int u = threadIdx.x % units, k = threadIdx.x / units;
+        const int hd = u / (kHeadDim / 4), d4 = (u % (kHeadDim / 4)) * 4;
+        float M = -INFINITY, L = 0.f;
+        f4 O = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = k; s0 < nsplit; s0 += 8 * K) {
+            float ms[8], ls[8];
+            f4 os[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int sj = s0 + j * K;
+                const float* ps = parts + (int64_t)min(sj, nsplit - 1) * (nrep * kPartStride) + hd * kPartStride;
+                ms[j] = sj < nsplit ? ld_agent(ps + kHeadDim) : -INFINITY;
+                ls[j] = ld_agent(ps + kHeadDim + 1);
+                os[j] = f4{ld_agent(ps + d4), ld_agent(ps + d4 + 1), ld_agent(ps + d4 + 2), ld_agent(ps + d4 + 3)};
             }
-            const float e = exp2f(ms - M);
-            O += os * e;
-            L += ls * e;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (ms[j] == -INFINITY) continue;
+                const float Mn = fmaxf(M, ms[j]);
+                const float a = (M == -INFINITY) ? 0.f : exp2f(M - Mn);
+                const float e = exp2f(ms[j] - Mn);
+                O = O * a + os[j] * e;
+                L = L * a + ls[j] * e;
+                M = Mn;
+            }
         }
-        p.out[(int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d] = f2h_rn(L > 0.f ? O / L : 0.f);
+        float* w = sm + (k * units + u) * 6;
+        w[0] = M;
+        w[1] = L;
+        w[2] = O[0];
+        w[3] = O[1];
+        w[4] = O[2];
+        w[5] = O[3];
     }
-    if (threadIdx.x == 0) p.counters[bh] = 0;
+    __syncthreads();
+    if (threadIdx.x < units) {
+        const int u = threadIdx.x;
+        const int hd = u / (kHeadDim / 4), d4 = (u % (kHeadDim / 4)) * 4;
+        float M = -INFINITY;
+        for (int k = 0; k < K; ++k) M = fmaxf(M, sm[(k * units + u) * 6]);
+        float L = 0.f;
+        f4 O = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < K; ++k) {
+            const float* w = sm + (k * units + u) * 6;
+            if (w[0] == -INFINITY) continue;
+            const float e = exp2f(w[0] - M);
+            L += w[1] * e;
+            O += f4{w[2], w[3], w[4], w[5]} * e;
+        }
+        const float inv = L > 0.f ? 1.0f / L : 0.f;
+        uint16_t* op = p.out + (int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d4;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) op[v] = f2h_rn(O[v] * inv);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 constexpr size_t kWsHeader = 256;
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-int max_splits_for(int int4_max_len, const int32_t* f16_max_lens, int nz) {
-    int total = units_int4(int4_max_len);
-    for (int i = 0; i < nz; ++i) total += units_f16(f16_max_lens[i]);
-    const int s = (total + kWaves - 1) / kWaves;
-    return s > 1 ? s : 1;
+int num_cus() {
+    static int cached = 0;
+    if (cached > 0) return cached;
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+        cached = n;
+    else
+        n = 256;
+    return cached > 0 ? cached : n;
 }
 
-size_t workspace_bytes(int B, int Hq, int Hkv, int max_splits) {
+// Ranges per (sequence, kv head): about one 8-wave workgroup per CU for the
+// whole launch, each reading at least ~96 KB, at most kMaxSplits.
+int choose_splits(int BH, int int4_max_len, const int32_t* f16_max_lens, int nz, int hint) {
+    if (hint > 0) return hint < kMaxSplits ? hint : kMaxSplits;
+    int64_t bytes = (int64_t)((int4_max_len + kBlockTokens - 1) / kBlockTokens) * kInt4ItemBytes;
+    for (int i = 0; i < nz; ++i) bytes += (int64_t)((f16_max_lens[i] + kBlockTokens - 1) / kBlockTokens) * kF16ItemBytes;
+    const int cus = num_cus();
+    int64_t s = (cus + BH - 1) / BH;                       // fill the chip once
+    const int64_t by_size = (bytes + 96 * 1024 - 1) / (96 * 1024);
+    if (s > by_size) s = by_size;                           // small problems: fewer, fuller ranges
+    if (s < 1) s = 1;
+    if (s > kMaxSplits) s = kMaxSplits;
+    return (int)s;
+}
+
+size_t workspace_bytes(int B, int Hq, int Hkv, int nsplit) {
     const size_t BH = (size_t)B * Hkv;
     const int nrep = Hq / Hkv;
-    return kWsHeader + align256(BH * sizeof(int)) + BH * (size_t)max_splits * nrep * kPartStride * sizeof(float);
+    return kWsHeader + align256(BH * sizeof(int)) + BH * (size_t)nsplit * nrep * kPartStride * sizeof(float);
+}
+
+size_t lds_bytes(int nrep) {
+    const size_t merge = ((size_t)kWaves * nrep * kHeadDim + 2 * kWaves * 16) * sizeof(float);
+    const size_t units = (size_t)nrep * (kHeadDim / 4);
+    const size_t combine = (kThreads / units) * units * 6 * sizeof(float);
+    return merge > combine ? merge : combine;
 }
 
 }  // namespace
@@ -438,8 +597,7 @@ extern "C" size_t hkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads,
     if (batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || head_dim != kHeadDim ||
         num_f16_zones < 0 || num_f16_zones > HKV_MAX_F16_ZONES || (num_f16_zones > 0 && !f16_max_lens))
         return 0;
-    const int ms = max_splits_for(int4_max_len, f16_max_lens, num_f16_zones);
-    return workspace_bytes(batch, num_q_heads, num_kv_heads, ms);
+    return workspace_bytes(batch, num_q_heads, num_kv_heads, kMaxSplits);
 }
 
 extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
@@ -480,13 +638,13 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
         }
         zl[i] = z.max_len;
     }
-    const int ms = max_splits_for(a->int4_max_len, zl, a->num_f16_zones);
+    const int64_t BH = (int64_t)a->batch * a->num_kv_heads;
+    HKV_REQUIRE(BH < 65536, HKV_ERR_ARG, "hkv_decode_attn: batch x kv heads too large");
+    const int ms = choose_splits((int)BH, a->int4_max_len, zl, a->num_f16_zones, a->splits_hint);
     const size_t need = workspace_bytes(a->batch, a->num_q_heads, a->num_kv_heads, ms);
     HKV_REQUIRE(a->workspace_bytes >= need, HKV_ERR_CAPACITY,
                 "hkv_decode_attn: workspace %zu bytes, need %zu", a->workspace_bytes, need);
     HKV_REQUIRE((((uintptr_t)a->workspace) & 255) == 0, HKV_ERR_ARG, "hkv_decode_attn: workspace must be 256-byte aligned");
-    const int64_t BH = (int64_t)a->batch * a->num_kv_heads;
-    HKV_REQUIRE(BH * ms < 2147483647LL, HKV_ERR_ARG, "hkv_decode_attn: grid too large");
 
     DecodeParams p;
     p.B = a->batch;
@@ -519,7 +677,17 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     p.counters = (int*)(ws + kWsHeader);
     p.partials = (float*)(ws + kWsHeader + align256((size_t)BH * sizeof(int)));
     p.max_splits = ms;
-    hipLaunchKernelGGL(decode_attn_kernel, dim3((unsigned)(BH * ms)), dim3(256), 0, (hipStream_t)stream, p);
+    const size_t lds = lds_bytes(nrep);
+    if (lds > 64 * 1024) {
+        static bool raised = false;
+        if (!raised) {
+            HKV_HIP_CHECK(hipFuncSetAttribute((const void*)decode_attn_kernel,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
+            raised = true;
+        }
+    }
+    hipLaunchKernelGGL(decode_attn_kernel, dim3((unsigned)(BH * ms)), dim3(kThreads), lds,
+                       (hipStream_t)stream, p);
     HKV_LAUNCH_CHECK("decode_attn_kernel");
     return HKV_OK;
 }

@@ -264,12 +264,14 @@ class DecodeWorkspace:
 
 
 def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
-                     sm_scale=None, workspace=None, out=None):
+                     sm_scale=None, workspace=None, out=None, splits=0):
     """Split-K decode attention over fp16 zones and the INT4 pool.
 
     q: [B, Hq, 128] or [B, Hq, 1, 128] fp16.
     zones: sequence of (F16Zone, lens int32 [B] or None, max_len).
     pool / block_table [B, nblk] / int4_lens [B] / int4_max_len: the INT4 zone.
+    splits: ranges per (sequence, kv head); 0 lets the library choose (about one
+    workgroup per CU).
     Returns fp16 [B, Hq, 128] (or [B, Hq, 1, 128] if q was 4-D).
     """
     _require_gpu(q)
@@ -327,5 +329,6 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
         workspace = DecodeWorkspace(dev)
     ws = workspace.get(nbytes)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    a.splits_hint = int(splits)
     check(load().hkv_decode_attn(ctypes.byref(a), stream_ptr(dev)), "hkv_decode_attn")
     return out.unsqueeze(2) if squeeze else out

@@ -105,5 +105,6 @@ def test_decode_argument_errors(lib):
 def test_workspace_size(lib):
     from heterokv import ops
     n = ops.decode_workspace_bytes(1, 32, 8, 28608, [64, 4096])
-    # 224 INT4 units + 2 + 128 fp16 units = 354 units -> 89 splits of 4 waves
-    assert n == 256 + 256 + 8 * 89 * 4 * 130 * 4
+    # header + counters + partial states for up to 64 ranges per (sequence, kv head):
+    # 8 pairs x 64 ranges x 4 heads x 132 floats
+    assert n == 256 + 256 + 8 * 64 * 4 * 132 * 4
