@@ -41,9 +41,9 @@ __global__ __launch_bounds__(128) void zone_write_kernel(ZoneWriteParams p) {
     const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int d = threadIdx.x;
     int slot = p.slot_start[b] + t;
-    if (p.ring) {
-        slot %= p.cap;
-        if (slot < 0) slot += p.cap;
+    if (p.ring > 0) {
+        slot %= p.ring;
+        if (slot < 0) slot += p.ring;
     }
     if (slot < 0 || slot >= p.cap) return;
     const int64_t src = (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)t * p.st + d;
@@ -51,6 +51,19 @@ __global__ __launch_bounds__(128) void zone_write_kernel(ZoneWriteParams p) {
     p.zk[(bh * p.cap + slot) * kHeadDim + d] = p.k[src];
     const int64_t tile = bh * (p.cap / kBlockTokens) + slot / kBlockTokens;
     p.zv[tile * (kBlockTokens * kHeadDim) + vtile_off(slot & 15, d)] = p.v[src];
+}
+
+__global__ __launch_bounds__(128) void zone_copy_kernel(const uint16_t* __restrict__ sk,
+                                                        const uint16_t* __restrict__ sv, int scap, int s0,
+                                                        uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
+                                                        int dcap, int d0, int H) {
+    const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int d = threadIdx.x;
+    const int64_t bh = (int64_t)b * H + h;
+    const int ss = s0 + i, ds = d0 + i;
+    dk[(bh * dcap + ds) * kHeadDim + d] = sk[(bh * scap + ss) * kHeadDim + d];
+    dv[(bh * (dcap / kBlockTokens) + ds / kBlockTokens) * (kBlockTokens * kHeadDim) + vtile_off(ds & 15, d)] =
+        sv[(bh * (scap / kBlockTokens) + ss / kBlockTokens) * (kBlockTokens * kHeadDim) + vtile_off(ss & 15, d)];
 }
 
 __global__ __launch_bounds__(128) void zone_read_kernel(const uint16_t* __restrict__ zk,
@@ -93,8 +106,9 @@ extern "C" int hkv_zone_write(const HkvZoneWriteArgs* a, void* stream) {
     if (a->batch == 0 || a->num_tokens == 0) return HKV_OK;
     HKV_REQUIRE(a->k && a->v && a->slot_start && a->zone_k && a->zone_v, HKV_ERR_ARG,
                 "hkv_zone_write: null pointer");
-    HKV_REQUIRE(a->num_tokens <= 2147483647 && a->num_kv_heads <= 65535 && a->batch <= 65535,
-                HKV_ERR_ARG, "hkv_zone_write: grid too large");
+    HKV_REQUIRE(a->num_kv_heads <= 65535 && a->batch <= 65535, HKV_ERR_ARG, "hkv_zone_write: grid too large");
+    HKV_REQUIRE(a->ring >= 0 && a->ring <= a->capacity, HKV_ERR_ARG,
+                "hkv_zone_write: ring %d must be in [0, capacity %d]", a->ring, a->capacity);
     ZoneWriteParams p;
     p.k = a->k;
     p.v = a->v;
@@ -128,5 +142,27 @@ extern "C" int hkv_zone_read(const uint16_t* zone_k, const uint16_t* zone_v, int
     hipLaunchKernelGGL(zone_read_kernel, dim3(n, num_kv_heads, batch), dim3(128), 0, (hipStream_t)stream,
                        zone_k, zone_v, num_kv_heads, capacity, n, out_k, out_v);
     HKV_LAUNCH_CHECK("zone_read_kernel");
+    return HKV_OK;
+}
+
+extern "C" int hkv_zone_copy(const uint16_t* src_k, const uint16_t* src_v, int32_t src_capacity,
+                             int32_t src_slot, uint16_t* dst_k, uint16_t* dst_v, int32_t dst_capacity,
+                             int32_t dst_slot, int32_t batch, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t n, void* stream) {
+    clear_error();
+    HKV_REQUIRE(head_dim == kHeadDim, HKV_ERR_UNSUPPORTED, "hkv_zone_copy: head_dim %d != 128", head_dim);
+    HKV_REQUIRE(src_capacity > 0 && src_capacity % kBlockTokens == 0 && dst_capacity > 0 &&
+                    dst_capacity % kBlockTokens == 0,
+                HKV_ERR_ARG, "hkv_zone_copy: capacities must be positive multiples of 16");
+    HKV_REQUIRE(n >= 0 && batch >= 0 && num_kv_heads > 0 && num_kv_heads <= 65535 && batch <= 65535, HKV_ERR_ARG,
+                "hkv_zone_copy: bad sizes");
+    HKV_REQUIRE(src_slot >= 0 && dst_slot >= 0 && (int64_t)src_slot + n <= src_capacity &&
+                    (int64_t)dst_slot + n <= dst_capacity,
+                HKV_ERR_CAPACITY, "hkv_zone_copy: slot range outside a zone");
+    if (n == 0 || batch == 0) return HKV_OK;
+    HKV_REQUIRE(src_k && src_v && dst_k && dst_v, HKV_ERR_ARG, "hkv_zone_copy: null pointer");
+    hipLaunchKernelGGL(zone_copy_kernel, dim3(n, num_kv_heads, batch), dim3(128), 0, (hipStream_t)stream, src_k,
+                       src_v, src_capacity, src_slot, dst_k, dst_v, dst_capacity, dst_slot, num_kv_heads);
+    HKV_LAUNCH_CHECK("zone_copy_kernel");
     return HKV_OK;
 }

@@ -89,6 +89,7 @@ SYMBOLS = [
     ("hkv_unpack_tokens", ctypes.c_int, [vp, i64, vp, i32, i32, i32, i32, vp, vp, vp, vp]),
     ("hkv_zone_write", ctypes.c_int, [ctypes.POINTER(ZoneWriteArgs), vp]),
     ("hkv_zone_read", ctypes.c_int, [vp, vp, i32, i32, i32, i32, i32, vp, vp, vp]),
+    ("hkv_zone_copy", ctypes.c_int, [vp, vp, i32, i32, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
     ("hkv_decode_workspace_bytes", ctypes.c_size_t, [i32, i32, i32, i32, i32, vp, i32]),
     ("hkv_decode_attn", ctypes.c_int, [ctypes.POINTER(DecodeArgs), vp]),
 ]

@@ -1,0 +1,261 @@
+"""FusedHeteroCache: HuggingFace cache adapter over the GPU HeteroKVManager.
+
+Drop-in for src/core/engine_wrapper.py:32-539 of the reference: same constructor
+arguments, update / get_seq_length / get_mask_sizes / seen_tokens / dram_table /
+memory_summary, ChunkedPrefillEngine and build_fused_cache.
+
+Attention routes.
+  * Prefill (new_len > 1): the reference hands transformers the full chunk (first
+    chunk) or sink + old tail + chunk (later chunks) and lets SDPA attend
+    (manager.py:533-535,562-563); the same tensors are returned here.
+  * Decode, default (Path C, engine_wrapper.py:236-245): the reference prepends every
+    DRAM token, dequantized to fp16, to sink + tail + heavy hitters.  With
+    fused_decode=True (default) update() returns the new token's K/V tagged with a
+    route, and the attention function registered as "heterokv" computes the same
+    attention directly over the INT4 pool and the fp16 zones (one split-K launch);
+    nothing is dequantized or concatenated.  With fused_decode=False the reference's
+    concatenated tensors are materialized and returned.
+The Path C gate is the reference's: DRAM tokens join a layer's attention only
+while _swap_in_tokens > 0, which layer 0 refreshes after its own decode update.
+"""
+import gc
+import math
+from typing import Any, Dict, Optional, Tuple
+
+import torch
+from transformers.cache_utils import DynamicCache
+
+from ._lib import HeteroKVError
+from .manager import HeteroKVManager
+
+ATTN_IMPLEMENTATION = "heterokv"
+
+
+class FusedHeteroCache(DynamicCache):
+    """HF DynamicCache subclass backed by HeteroKVManager (engine_wrapper.py:32-110)."""
+
+    def __init__(self, num_layers: Optional[int] = None, sink_tokens: int = 64, keep_tail: int = 8192,
+                 chunk_size: int = 2048, device: str = "cuda:0", group_size: int = 128,
+                 enable_quant: bool = True, enable_prefetch: bool = True, enable_triton: bool = True,
+                 bandwidth_limiter=None, self_healing: bool = True, adaptive_self_healing: bool = False,
+                 enable_method_d: bool = False, method_d_alpha: float = 1.0, fused_decode: bool = True):
+        super().__init__()
+        if adaptive_self_healing:
+            raise HeteroKVError(-4, "windowed retrieval (adaptive_self_healing) is not part of this build; "
+                                    "the default full retrieval (Path C) is")
+        self.sink_tokens = sink_tokens
+        self.keep_tail = keep_tail
+        self.chunk_size = chunk_size
+        self.device = device
+        self.enable_quant = enable_quant
+        self.enable_triton = enable_triton
+        self.enable_prefetch = enable_prefetch
+        self.group_size = group_size
+        self._bandwidth_limiter = bandwidth_limiter
+        self.self_healing = self_healing
+        self.adaptive_self_healing = adaptive_self_healing
+        self.enable_method_d = enable_method_d
+        self.method_d_alpha = method_d_alpha
+        self.fused_decode = fused_decode
+        self._num_layers = num_layers
+        self._manager: Optional[HeteroKVManager] = None
+        self.real_seq_len: int = 0
+        self._swap_in_tokens: int = 0
+
+    def _ensure_manager(self, layer_idx: int) -> HeteroKVManager:
+        if self._manager is not None:
+            return self._manager
+        num_layers = self._num_layers if self._num_layers is not None else (layer_idx + 1)
+        self._manager = HeteroKVManager(num_layers=num_layers, sink_tokens=self.sink_tokens,
+                                        hbm_budget_tokens=self.keep_tail, device=self.device,
+                                        enable_quant=self.enable_quant, enable_prefetch=self.enable_prefetch,
+                                        group_size=self.group_size, bandwidth_limiter=self._bandwidth_limiter,
+                                        enable_method_d=self.enable_method_d, method_d_alpha=self.method_d_alpha)
+        return self._manager
+
+    # ------------------------------------------------------------------ DynamicCache interface
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int,
+               cache_kwargs: Optional[Dict[str, Any]] = None, *args, **kwargs) -> Tuple[torch.Tensor, torch.Tensor]:
+        """engine_wrapper.py:137-254."""
+        manager = self._ensure_manager(layer_idx)
+        new_len = key_states.shape[-2]
+        mode = "prefill" if new_len > 1 else "decode"
+        include_dram = mode == "decode" and self.self_healing and self._swap_in_tokens > 0
+        if mode == "decode" and self.fused_decode:
+            manager.update(layer_idx, key_states, value_states, mode="decode", seq_offset=self.real_seq_len,
+                           materialize=False)
+            out_k, out_v = key_states, value_states
+            route = (self, layer_idx, include_dram)
+            out_k._hkv_route = route
+            out_v._hkv_route = route
+        else:
+            out_k, out_v = manager.update(layer_idx, key_states, value_states, mode=mode,
+                                          seq_offset=self.real_seq_len)
+            if include_dram:
+                dram_k, dram_v, count = manager.decompress_dram_chunks(layer_idx)
+                if dram_k is not None and count > 0:
+                    out_k = torch.cat([dram_k.to(out_k.dtype), out_k], dim=-2)
+                    out_v = torch.cat([dram_v.to(out_v.dtype), out_v], dim=-2)
+        if layer_idx == 0:
+            self.real_seq_len += new_len
+            if mode == "decode" and self.self_healing:
+                self._refresh_swap_count()
+        return out_k, out_v
+
+    def get_seq_length(self, layer_idx: int = 0, *args, **kwargs) -> int:
+        """engine_wrapper.py:256-264: HBM cache length + DRAM swap-in count."""
+        if self._manager is None:
+            return 0
+        n = self._manager.hbm_length(layer_idx)
+        if n is None:
+            return 0
+        return n + self._swap_in_tokens
+
+    @property
+    def seen_tokens(self) -> int:
+        return self.real_seq_len
+
+    def get_mask_sizes(self, query, layer_idx: int = 0, *args, **kwargs) -> Tuple[int, int]:
+        """engine_wrapper.py:274-301.  `query` is the query length (transformers >= 5) or the
+        cache_position tensor (4.57, as the reference was written for)."""
+        query_len = int(query.shape[0]) if isinstance(query, torch.Tensor) else int(query)
+        if self._manager is None:
+            return query_len, 0
+        phys = self._manager.hbm_length(layer_idx)
+        if phys is None:
+            return query_len, 0
+        if query_len > 1:
+            return phys + query_len, 0
+        tail = self._manager.tail_length(layer_idx)
+        if tail is not None and tail >= self._manager.tail_budget:
+            return phys + self._swap_in_tokens, 0
+        return phys + self._swap_in_tokens + 1, 0
+
+    def _refresh_swap_count(self) -> None:
+        if self._manager is not None:
+            self._swap_in_tokens = self._manager.count_dram_tokens(layer_idx=0)
+
+    @property
+    def is_compileable(self) -> bool:
+        return False
+
+    # ------------------------------------------------------------------ tiered storage passthrough
+    def allocate(self, layer_idx: int, seq_len: int = 0, budget_tokens: Optional[int] = None) -> bool:
+        return self._ensure_manager(layer_idx).allocate(layer_idx, budget_tokens)
+
+    def compress(self, layer_idx: int, device: str = "DRAM") -> int:
+        return self._ensure_manager(layer_idx).compress(layer_idx, device)
+
+    def memory_summary(self) -> Dict[str, Any]:
+        if self._manager is None:
+            return {"hbm_tokens": 0, "dram_entries": 0, "dram_bytes": 0,
+                    "max_hbm_tokens": self.sink_tokens + self.keep_tail}
+        return self._manager.memory_summary()
+
+    @property
+    def dram_table(self):
+        if self._manager is None:
+            return {}
+        return self._manager._dram_table
+
+    def schedule_prefetch(self, chunk_key: str) -> None:
+        """The INT4 tier of this build is resident in HBM (or streamed by the block prefetcher),
+        so there is nothing to stage per chunk."""
+        return None
+
+    def swap_in_quantized(self, chunk_key: str) -> Optional[Dict[str, torch.Tensor]]:
+        if self._manager is None or chunk_key not in self._manager._chunks:
+            return None
+        return self._manager.chunk_codes(chunk_key)
+
+    def fused_attn_on_swapped(self, q: torch.Tensor, chunk_key: str,
+                              sm_scale: Optional[float] = None) -> Optional[torch.Tensor]:
+        """engine_wrapper.py:357-404: attention of q over one chunk's INT4 tokens."""
+        from .fused_dequant_attn import fused_dequant_attn_decode
+        data = self.swap_in_quantized(chunk_key)
+        if data is None:
+            return None
+        B, H, T, _ = data["k_data"].shape
+        return fused_dequant_attn_decode(q, data["k_data"], data["k_scales"].view(B, H, T), data["k_zps"].view(B, H, T),
+                                         data["v_data"], data["v_scales"].view(B, H, T), data["v_zps"].view(B, H, T),
+                                         sm_scale=sm_scale)
+
+
+def heterokv_attention_forward(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
+    """Attention function registered with transformers as "heterokv".
+
+    Decode tokens tagged by FusedHeteroCache.update attend through the manager's
+    fused INT4/fp16 kernel; every other call (prefill chunks) goes to transformers'
+    SDPA attention on the tensors the cache returned, as in the reference."""
+    route = getattr(key, "_hkv_route", None)
+    if route is not None and query.shape[2] == 1:
+        cache, layer_idx, include_dram = route
+        out = cache._manager.attend_decode(layer_idx, query, sm_scale=scaling, include_dram=include_dram)
+        return out.transpose(1, 2).contiguous(), None
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+    return sdpa_attention_forward(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout,
+                                  **kwargs)
+
+
+def register_attention() -> str:
+    """Register heterokv_attention_forward with transformers; returns its name."""
+    from transformers import AttentionInterface
+    AttentionInterface.register(ATTN_IMPLEMENTATION, heterokv_attention_forward)
+    try:
+        from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, sdpa_mask
+        ALL_MASK_ATTENTION_FUNCTIONS.register(ATTN_IMPLEMENTATION, sdpa_mask)
+    except Exception:  # older transformers: masks are built per implementation name elsewhere
+        pass
+    return ATTN_IMPLEMENTATION
+
+
+class ChunkedPrefillEngine:
+    """engine_wrapper.py:411-496: feeds a long prompt through the model in chunks."""
+
+    def __init__(self, model, cache: FusedHeteroCache, chunk_size: int = 2048, verbose: bool = False):
+        self.model = model
+        self.cache = cache
+        self.chunk_size = chunk_size
+        self.verbose = verbose
+
+    @torch.inference_mode()
+    def prefill(self, input_ids: torch.Tensor, position_ids: Optional[torch.Tensor] = None,
+                attention_mask: Optional[torch.Tensor] = None):
+        total_len = input_ids.shape[-1]
+        device = input_ids.device
+        last = None
+        chunk_idx = 0
+        for start in range(0, total_len, self.chunk_size):
+            end = min(start + self.chunk_size, total_len)
+            chunk_ids = input_ids[:, start:end]
+            chunk_pos = (position_ids[:, start:end] if position_ids is not None
+                         else torch.arange(start, end, dtype=torch.long, device=device).unsqueeze(0))
+            # The cache returns [sink | old tail | chunk] for a later chunk, so the chunk's
+            # queries sit after the `phys` cached tokens; the reference restarts
+            # cache_position at 0 for every chunk (:455-460), which under transformers >= 5
+            # lines the causal mask up with the start of that tensor instead.
+            mgr = self.cache._manager
+            phys = (mgr.hbm_length(0) or 0) if mgr is not None else 0
+            chunk_cache_pos = torch.arange(phys, phys + end - start, dtype=torch.long, device=device)
+            chunk_mask = attention_mask[:, :end] if attention_mask is not None else None
+            last = self.model(input_ids=chunk_ids, past_key_values=self.cache, use_cache=True,
+                              position_ids=chunk_pos, attention_mask=chunk_mask, cache_position=chunk_cache_pos)
+            if self.verbose:
+                print("  chunk [%6d:%6d] dram_entries=%d" % (start, end, len(self.cache.dram_table)), flush=True)
+            chunk_idx += 1
+            if chunk_idx % 4 == 0 or end == total_len:
+                gc.collect()
+        return last
+
+
+def build_fused_cache(num_layers: Optional[int] = None, device: str = "cuda:0", sink_tokens: int = 64,
+                      keep_tail: int = 8192, chunk_size: int = 2048, group_size: int = 128,
+                      enable_quant: bool = True, enable_prefetch: bool = True, enable_triton: bool = True,
+                      bandwidth_limiter=None, self_healing: bool = True,
+                      adaptive_self_healing: bool = False) -> FusedHeteroCache:
+    """engine_wrapper.py:503-539."""
+    return FusedHeteroCache(num_layers=num_layers, sink_tokens=sink_tokens, keep_tail=keep_tail,
+                            chunk_size=chunk_size, device=device, group_size=group_size,
+                            enable_quant=enable_quant, enable_prefetch=enable_prefetch,
+                            enable_triton=enable_triton, bandwidth_limiter=bandwidth_limiter,
+                            self_healing=self_healing, adaptive_self_healing=adaptive_self_healing)

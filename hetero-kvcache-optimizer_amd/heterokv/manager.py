@@ -1,0 +1,464 @@
+"""HeteroKVManager: three-zone KV storage on the GPU.
+
+Drop-in for src/memory/manager.py:30-1299 of the reference.  Per layer:
+  * sink zone      -- the first `sink_tokens` tokens, fp16           (manager.py:462-466)
+  * tail zone      -- the most recent `hbm_budget_tokens - sink_tokens`
+                      tokens, fp16, kept as a ring                    (manager.py:480-485,618-664)
+  * heavy hitters  -- tokens slid out of the tail at decode, fp16     (manager.py:686-715)
+  * INT4 middle    -- every token evicted at prefill, quantized and
+                      nibble-packed into 16-token block records by the
+                      append kernel, in eviction order                (manager.py:1231-1299)
+The reference keeps the middle in pinned host memory and copies + dequantizes
+all of it to fp16 on every decode step (manager.py:779-821); here it stays INT4
+in HBM and the split-K kernel reads it in place (`attend_decode`).
+
+Index semantics follow the reference exactly (zone boundaries, eviction
+ranges, chunk keys "l{layer}_e{counter}" with the counter moving only on layer
+0, FIFO heavy-hitter fill, count_dram_tokens).  `positions(layer)` returns the
+absolute token positions in the order the reference returns K/V, for index
+parity checks.  Deliberate differences, all on paths that cannot change an
+attended token: tokens that the reference leaves in its competition queue after
+the heavy-hitter zone is full are not retained (they are never attended again);
+the queue is kept per layer (equal to the reference's shared queue when layers
+update in lockstep, the only way transformers drives a cache); zones store
+fp16 (bf16 inputs are stored as fp16 and returned in the caller's dtype).
+"""
+from collections import OrderedDict, deque
+from typing import Any, Dict, List, Optional, Tuple
+
+import torch
+
+from . import ops
+from ._lib import BLOCK_TOKENS, HEAD_DIM, HeteroKVError
+from .kv_compressor import KVCompressor
+
+
+def _as16(t):
+    return t if t.dtype == torch.float16 else t.to(torch.float16)
+
+
+class _LayerState:
+    def __init__(self, B, H, device, dtype, sink_tokens, tail_budget, hh_budget):
+        self.B, self.H, self.device, self.dtype = B, H, device, dtype
+        self.sink = ops.F16Zone(B, H, max(sink_tokens, 1), device)
+        self.sink_len = 0
+        self.sink_pos: List[int] = []
+        self.ring = max(tail_budget, 1)
+        self.tail = ops.F16Zone(B, H, self.ring, device)
+        self.tail_head = 0
+        self.tail_len = 0
+        self.tail_pos = deque()
+        self.tail_started = False
+        self.hh = ops.F16Zone(B, H, max(hh_budget, 1), device)
+        self.hh_len = 0
+        self.hh_pos: List[int] = []
+        self.hh_started = False
+        self.pool: Optional[ops.Int4Pool] = None
+        self.cap_blocks = 0
+        self.bt: Optional[torch.Tensor] = None
+        self.int4_len = 0
+        self.int4_pos: List[int] = []
+        self.prefilled = False
+        self.seq_offset = 0
+
+    # -------------------------------------------------------------- INT4 pool
+    def ensure_int4(self, n_tokens):
+        need = (n_tokens + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+        if need <= self.cap_blocks:
+            return
+        cap = max(need, 2 * self.cap_blocks, 64)
+        pool = ops.Int4Pool(self.B * cap, self.H, self.device)
+        if self.pool is not None and self.cap_blocks:
+            rb = pool.record_bytes
+            pool.data.view(self.B, cap, rb)[:, :self.cap_blocks] = self.pool.data.view(self.B, self.cap_blocks, rb)
+        self.pool, self.cap_blocks = pool, cap
+        base = torch.arange(self.B, dtype=torch.int32, device=self.device)[:, None] * cap
+        self.bt = (base + torch.arange(cap, dtype=torch.int32, device=self.device)[None]).contiguous()
+
+    # -------------------------------------------------------------- tail ring
+    def tail_tensors(self):
+        """Tail K/V in logical (oldest first) order, fp16 [B, H, tail_len, 128]."""
+        if self.tail_len == 0:
+            e = torch.empty((self.B, self.H, 0, HEAD_DIM), dtype=torch.float16, device=self.device)
+            return e, e.clone()
+        k, v = self.tail.read(self.ring if self.tail_head + self.tail_len > self.ring else self.tail_head + self.tail_len)
+        if self.tail_head == 0:
+            return k[:, :, :self.tail_len], v[:, :, :self.tail_len]
+        idx = (torch.arange(self.tail_len, device=self.device) + self.tail_head) % self.ring
+        return k.index_select(2, idx), v.index_select(2, idx)
+
+    def write_tail(self, k, v):
+        """Replace the tail with k, v (logical order), starting at ring slot 0."""
+        n = k.shape[2]
+        if n:
+            self.tail.write(_as16(k), _as16(v), [0] * self.B)
+        self.tail_head, self.tail_len = 0, n
+
+
+class HeteroKVManager:
+    """Tiered KV manager with the reference's constructor and public methods."""
+
+    def __init__(self, num_layers: int, sink_tokens: int = 64, hbm_budget_tokens: int = 8192,
+                 device: str = "cuda", enable_quant: bool = True, enable_prefetch: bool = True,
+                 group_size: int = 128, bits: int = 4, bandwidth_limiter=None,
+                 enable_method_d: bool = False, method_d_alpha: float = 1.0):
+        if group_size != HEAD_DIM or bits != 4:
+            raise HeteroKVError(-4, "HeteroKVManager stores one INT4 group per 128-value token row "
+                                    "(group_size=128, bits=4); got group_size=%d bits=%d" % (group_size, bits))
+        if enable_method_d:
+            raise HeteroKVError(-4, "query-aware retrieval (Method D) is not part of this build")
+        self.num_layers = num_layers
+        self.sink_tokens = sink_tokens
+        self.hbm_budget_tokens = hbm_budget_tokens
+        self.device = torch.device(device)
+        self.enable_quant = enable_quant
+        self.enable_prefetch = enable_prefetch
+        self.group_size = group_size
+        self.bits = bits
+        self._bandwidth_limiter = bandwidth_limiter
+        self._heavyhitter_budget = max(hbm_budget_tokens // 2, 2048)
+        self._compressor = KVCompressor(group_size=group_size, bits=bits)
+        self._layers: List[Optional[_LayerState]] = [None] * num_layers
+        # chunk key -> (layer, first INT4 slot, token count), in eviction order
+        self._chunks: "OrderedDict[str, Tuple[int, int, int]]" = OrderedDict()
+        self._chunk_eviction_order: List[str] = []
+        self._chunk_attention_scores: Dict[str, float] = {}
+        self._eviction_counter = 0
+        self._queued_tokens = 0      # tokens the reference would leave in its competition queue
+        self._workspace = None
+
+    # ---------------------------------------------------------------- helpers
+    @property
+    def tail_budget(self) -> int:
+        return self.hbm_budget_tokens - self.sink_tokens
+
+    def _state(self, layer_idx, key_states) -> _LayerState:
+        if layer_idx < 0:
+            raise ValueError("Invalid layer %d" % layer_idx)
+        while len(self._layers) <= layer_idx:
+            self._layers.append(None)
+        st = self._layers[layer_idx]
+        if st is None:
+            B, H, _, D = key_states.shape
+            if D != HEAD_DIM:
+                raise HeteroKVError(-4, "head_dim must be 128, got %d" % D)
+            st = _LayerState(B, H, key_states.device, key_states.dtype, self.sink_tokens, self.tail_budget,
+                             self._heavyhitter_budget)
+            self._layers[layer_idx] = st
+        return st
+
+    def _check_input(self, key_states, value_states):
+        if key_states.device.type != "cuda":
+            raise HeteroKVError(-1, "HeteroKVManager keeps KV on a ROCm GPU; got a %s tensor" % key_states.device)
+        if key_states.dim() != 4 or key_states.shape != value_states.shape:
+            raise HeteroKVError(-1, "key/value states must both be [B, H, S, 128]")
+
+    # ---------------------------------------------------------------- public API
+    def allocate(self, layer: int, budget: Optional[int] = None) -> bool:
+        """manager.py:152-170: pools are created lazily; optionally changes the budget."""
+        if layer < 0 or layer >= self.num_layers:
+            raise ValueError("Invalid layer %d, num_layers=%d" % (layer, self.num_layers))
+        if budget is not None:
+            self.hbm_budget_tokens = budget
+        return True
+
+    def update(self, layer_idx: int, key_states: torch.Tensor, value_states: torch.Tensor,
+               mode: str = "prefill", seq_offset: int = 0, materialize: bool = True
+               ) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
+        """manager.py:175-204.  Returns the K/V the reference would hand to attention
+        (prefill: the full input or sink + old tail + chunk; decode: sink + tail + heavy
+        hitters).  With materialize=False the bookkeeping is done and (None, None) is
+        returned for decode, for callers that attend with `attend_decode`."""
+        if mode not in ("prefill", "decode"):
+            raise ValueError("Unknown mode: %s" % mode)
+        self._check_input(key_states, value_states)
+        st = self._state(layer_idx, key_states)
+        if mode == "prefill":
+            if st.prefilled:
+                return self._incremental_prefill(layer_idx, st, key_states, value_states, seq_offset)
+            return self._first_prefill(layer_idx, st, key_states, value_states, seq_offset)
+        return self._decode(layer_idx, st, key_states, value_states, seq_offset, materialize)
+
+    def _first_prefill(self, layer, st, k, v, seq_offset):
+        n = k.shape[2]
+        sink_amt = min(n, self.sink_tokens)
+        if sink_amt:
+            st.sink.write(_as16(k[:, :, :sink_amt]), _as16(v[:, :, :sink_amt]), [0] * st.B)
+        st.sink_len = sink_amt
+        st.sink_pos = list(range(seq_offset, seq_offset + sink_amt))
+        tail_amt = min(n - sink_amt, self.tail_budget)
+        st.write_tail(k[:, :, n - tail_amt:], v[:, :, n - tail_amt:])
+        st.tail_pos = deque(range(seq_offset + n - tail_amt, seq_offset + n))
+        st.tail_started = True
+        body0, body1 = sink_amt, n - tail_amt
+        if self.enable_quant and body1 > body0:
+            self._evict(layer, st, k[:, :, body0:body1], v[:, :, body0:body1], seq_offset + body0)
+        st.hh_len, st.hh_pos, st.hh_started = 0, [], True
+        st.prefilled = True
+        st.seq_offset = seq_offset + n
+        return k, v
+
+    def _incremental_prefill(self, layer, st, k, v, seq_offset):
+        n = k.shape[2]
+        old_k, old_v = st.tail_tensors()
+        old_pos = list(st.tail_pos)
+        combined_k = torch.cat([old_k.to(k.dtype), k], dim=2)
+        combined_v = torch.cat([old_v.to(v.dtype), v], dim=2)
+        sk, sv = st.sink.read(st.sink_len) if st.sink_len else (combined_k[:, :, :0], combined_v[:, :, :0])
+        ret_k = torch.cat([sk.to(k.dtype), combined_k], dim=2)
+        ret_v = torch.cat([sv.to(v.dtype), combined_v], dim=2)
+        combined_pos = old_pos + list(range(seq_offset, seq_offset + n))
+        total = combined_k.shape[2]
+        if total > self.tail_budget:
+            e = total - self.tail_budget
+            if self.enable_quant:
+                self._evict(layer, st, combined_k[:, :, :e], combined_v[:, :, :e], combined_pos[:e])
+            st.write_tail(combined_k[:, :, e:], combined_v[:, :, e:])
+            st.tail_pos = deque(combined_pos[e:])
+        else:
+            st.write_tail(combined_k, combined_v)
+            st.tail_pos = deque(combined_pos)
+        st.seq_offset = seq_offset + n
+        return ret_k, ret_v
+
+    def _decode(self, layer, st, k, v, seq_offset, materialize):
+        if k.shape[2] != 1:
+            raise HeteroKVError(-1, "decode expects one new token, got %d" % k.shape[2])
+        pos = seq_offset
+        k16, v16 = _as16(k), _as16(v)
+        if st.tail_len < self.tail_budget:
+            st.tail.write(k16, v16, [st.tail_head + st.tail_len] * st.B, ring=st.ring)
+            st.tail_len += 1
+            st.tail_pos.append(pos)
+        else:
+            # the oldest tail token leaves: into the heavy-hitter zone while it has room
+            # (manager.py:645-664, 686-715), else it stays queued in the reference and is never
+            # attended again
+            old = st.tail_pos.popleft()
+            if st.hh_len < self._heavyhitter_budget:
+                st.tail.copy_to(st.hh, st.tail_head, st.hh_len, 1)
+                st.hh_len += 1
+                st.hh_pos.append(old)
+            else:
+                self._queued_tokens += 1
+            st.tail.write(k16, v16, [st.tail_head] * st.B, ring=st.ring)
+            st.tail_head = (st.tail_head + 1) % st.ring
+            st.tail_pos.append(pos)
+        st.tail_started = True
+        st.hh_started = True
+        st.seq_offset = seq_offset + 1
+        if not materialize:
+            return None, None
+        kk, vv = self.get_hbm_kv(layer)
+        return kk.to(k.dtype), vv.to(v.dtype)
+
+    def _evict(self, layer, st, k, v, first_pos):
+        """manager.py:1231-1299: quantize + pack into the layer's INT4 blocks, record the chunk."""
+        n = k.shape[2]
+        st.ensure_int4(st.int4_len + n)
+        ops.pack_tokens(st.pool, k, v, torch.full((st.B,), st.int4_len, dtype=torch.int32), st.bt)
+        key = "l%d_e%d" % (layer, self._eviction_counter)
+        self._chunks[key] = (layer, st.int4_len, n)
+        if isinstance(first_pos, int):
+            st.int4_pos.extend(range(first_pos, first_pos + n))
+        else:
+            st.int4_pos.extend(first_pos)
+        st.int4_len += n
+        self._chunk_eviction_order.append(key)
+        self._chunk_attention_scores[key] = 1.0 / (self._eviction_counter + 1)
+        if layer == 0:
+            self._eviction_counter += 1
+
+    def compress(self, layer: int, device: str = "DRAM") -> int:
+        """manager.py:206-233: move every HBM token after the sink to the INT4 tier."""
+        if device.upper() != "DRAM":
+            raise NotImplementedError("Only DRAM compression is currently supported.")
+        st = self._layers[layer] if layer < len(self._layers) else None
+        if st is None:
+            return 0
+        kk, vv = self.get_hbm_kv(layer)
+        total = kk.shape[2]
+        if total <= self.sink_tokens:
+            return 0
+        pos = self.positions(layer, include_dram=False)
+        ks, vs = kk[:, :, self.sink_tokens:], vv[:, :, self.sink_tokens:]
+        self._evict(layer, st, ks, vs, pos[self.sink_tokens:])
+        # the reference keeps only the sink as its concatenated cache; all zones after it empty
+        st.tail_head, st.tail_len, st.tail_pos = 0, 0, deque()
+        st.hh_len, st.hh_pos = 0, []
+        if st.sink_len > self.sink_tokens:
+            st.sink_len = self.sink_tokens
+        return total - self.sink_tokens
+
+    def get_hbm_kv(self, layer_idx: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """manager.py:294-299: sink + tail + heavy hitters (fp16 [B, H, S, 128])."""
+        st = self._layers[layer_idx] if layer_idx < len(self._layers) else None
+        if st is None:
+            raise RuntimeError("Layer %d has not been allocated yet." % layer_idx)
+        parts_k, parts_v = [], []
+        if st.sink_len:
+            a, b = st.sink.read(st.sink_len)
+            parts_k.append(a)
+            parts_v.append(b)
+        tk, tv = st.tail_tensors()
+        parts_k.append(tk)
+        parts_v.append(tv)
+        if st.hh_len:
+            a, b = st.hh.read(st.hh_len)
+            parts_k.append(a)
+            parts_v.append(b)
+        return torch.cat(parts_k, dim=2), torch.cat(parts_v, dim=2)
+
+    def get_seq_offset(self, layer_idx: int) -> int:
+        st = self._layers[layer_idx] if layer_idx < len(self._layers) else None
+        return st.seq_offset if st is not None else 0
+
+    def hbm_length(self, layer_idx: int) -> Optional[int]:
+        """Length of the reference's concatenated HBM cache for this layer (None before use)."""
+        st = self._layers[layer_idx] if layer_idx < len(self._layers) else None
+        if st is None:
+            return None
+        return st.sink_len + st.tail_len + st.hh_len
+
+    def tail_length(self, layer_idx: int) -> Optional[int]:
+        st = self._layers[layer_idx] if layer_idx < len(self._layers) else None
+        return None if st is None or not st.tail_started else st.tail_len
+
+    def positions(self, layer_idx: int, include_dram: bool = False) -> List[int]:
+        """Absolute positions of the tokens the reference returns for this layer, in its
+        order: [DRAM chunks in eviction order] + sink + tail (oldest first) + heavy hitters."""
+        st = self._layers[layer_idx]
+        pre = list(st.int4_pos) if include_dram else []
+        return pre + list(st.sink_pos) + list(st.tail_pos) + list(st.hh_pos)
+
+    # ---------------------------------------------------------------- DRAM tier views
+    @property
+    def _dram_table(self) -> "DramTableView":
+        return DramTableView(self)
+
+    def count_dram_tokens(self, layer_idx: int = 0) -> int:
+        """manager.py:1218-1229: #chunks of the layer times the first chunk's token count."""
+        pre = "l%d_" % layer_idx
+        keys = [k for k in self._chunks if k.startswith(pre)]
+        if not keys:
+            return 0
+        return len(keys) * self._chunks[keys[0]][2]
+
+    def dram_tokens(self, layer_idx: int) -> int:
+        """Exact number of INT4 tokens held for the layer."""
+        st = self._layers[layer_idx] if layer_idx < len(self._layers) else None
+        return 0 if st is None else st.int4_len
+
+    def chunk_codes(self, key: str) -> Dict[str, torch.Tensor]:
+        """Reference-layout view of one evicted chunk (kv_compressor.compress of [B,H,T,128]):
+        k_data/v_data uint8 [B,H,T,128], *_scales float32 [B*H*T], *_zps uint8 [B*H*T]."""
+        layer, start, n = self._chunks[key]
+        st = self._layers[layer]
+        out = {}
+        for which, name in ((0, "k"), (1, "v")):
+            cs, ss, zs = [], [], []
+            for b in range(st.B):
+                c, s, z = ops.unpack_tokens(st.pool, st.bt[b], start + n, which)
+                cs.append(c[:, start:start + n])
+                ss.append(s.view(st.H, -1)[:, start:start + n].reshape(-1))
+                zs.append(z.view(st.H, -1)[:, start:start + n].reshape(-1))
+            out[name + "_data"] = torch.stack(cs)
+            out[name + "_scales"] = torch.cat(ss)
+            out[name + "_zps"] = torch.cat(zs)
+        return out
+
+    def decompress_dram_chunks(self, layer_idx: int):
+        """manager.py:779-821 (Path C): every INT4 token of the layer dequantized to fp16,
+        in eviction order.  Returns (K, V, count) or (None, None, 0)."""
+        st = self._layers[layer_idx] if layer_idx < len(self._layers) else None
+        if st is None or st.int4_len == 0:
+            return None, None, 0
+        outs = []
+        for which in (0, 1):
+            per_b = []
+            for b in range(st.B):
+                c, s, z = ops.unpack_tokens(st.pool, st.bt[b], st.int4_len, which)
+                per_b.append(self._compressor.decompress(c, s, z, target_dtype=torch.float16))
+            outs.append(torch.stack(per_b))
+        return outs[0], outs[1], st.int4_len
+
+    def get_dram_chunks_quantized(self, layer_idx: int, window_size: Optional[int] = None):
+        """manager.py:931-1056 semantics without the Python chunk copies: the chosen chunks'
+        INT4 tokens in reference layout (highest chunk score first, concatenated in eviction
+        order).  window_size None = all chunks."""
+        pre = "l%d_" % layer_idx
+        keys = [k for k in self._chunks if k.startswith(pre)]
+        if not keys:
+            return None
+        if window_size is not None:
+            ranked = sorted(keys, key=lambda k: self._chunk_attention_scores.get(k, 0.0), reverse=True)
+            chosen = set(ranked[:max(1, min(window_size, len(keys)))])
+            keys = [k for k in self._chunk_eviction_order if k in chosen]
+        parts = [self.chunk_codes(k) for k in keys]
+        return {name: torch.cat([p[name] for p in parts], dim=2 if name.endswith("_data") else 0)
+                for name in parts[0]}
+
+    # ---------------------------------------------------------------- fused decode
+    def attend_decode(self, layer_idx: int, query_states: torch.Tensor, sm_scale: Optional[float] = None,
+                      include_dram: bool = True) -> torch.Tensor:
+        """softmax(q K^T * sm_scale) V over [INT4 middle (if include_dram) | sink | tail |
+        heavy hitters] of the layer, in one split-K launch (hkv_decode_attn).
+        query_states: [B, Hq, 1, 128]; returns [B, Hq, 1, 128] in the query's dtype."""
+        st = self._layers[layer_idx]
+        if st is None:
+            raise RuntimeError("Layer %d has not been allocated yet." % layer_idx)
+        if self._workspace is None:
+            self._workspace = ops.DecodeWorkspace(self.device)
+        zones = []
+        if st.sink_len:
+            zones.append((st.sink, None, st.sink_len))
+        if st.tail_len:
+            zones.append((st.tail, None, st.tail_len))
+        if st.hh_len:
+            zones.append((st.hh, None, st.hh_len))
+        n4 = st.int4_len if include_dram else 0
+        q16 = _as16(query_states)
+        out = ops.decode_attention(q16, zones=zones, pool=st.pool if n4 else None,
+                                   block_table=st.bt if n4 else None, int4_max_len=n4,
+                                   sm_scale=sm_scale, workspace=self._workspace)
+        return out.to(query_states.dtype)
+
+    # ---------------------------------------------------------------- summaries
+    def memory_summary(self) -> Dict[str, Any]:
+        """manager.py:387-401.  dram_bytes counts this build's packed INT4 storage."""
+        hbm = sum((st.sink_len + st.tail_len + st.hh_len) for st in self._layers if st is not None)
+        dram_bytes = 0
+        for st in self._layers:
+            if st is not None:
+                dram_bytes += st.B * st.H * st.int4_len * 2 * (HEAD_DIM // 2 + 5)
+        return {"hbm_tokens": hbm, "dram_entries": len(self._chunks), "dram_bytes": dram_bytes,
+                "max_hbm_tokens": self.max_hbm_tokens()}
+
+    def max_hbm_tokens(self) -> int:
+        return self.sink_tokens + self.hbm_budget_tokens + self._heavyhitter_budget
+
+
+class DramTableView:
+    """Read-only mapping chunk key -> reference-layout entry (k_data, k_scales, k_zps,
+    v_data, v_scales, v_zps), materialized on access (dram_storage.py:140-147)."""
+
+    def __init__(self, mgr: HeteroKVManager):
+        self._m = mgr
+
+    def keys(self):
+        return list(self._m._chunks.keys())
+
+    def __iter__(self):
+        return iter(self.keys())
+
+    def __len__(self):
+        return len(self._m._chunks)
+
+    def __contains__(self, key):
+        return key in self._m._chunks
+
+    def __getitem__(self, key):
+        return self._m.chunk_codes(key)
+
+    def items(self):
+        return [(k, self[k]) for k in self.keys()]

@@ -201,8 +201,9 @@ class F16Zone:
     def device(self):
         return self.k.device
 
-    def write(self, k, v, slot_start, ring=False):
-        """Write k, v [B, H, T, 128] fp16 at slots slot_start[b] + t (mod capacity if ring)."""
+    def write(self, k, v, slot_start, ring=0):
+        """Write k, v [B, H, T, 128] fp16 at slots slot_start[b] + t (mod `ring` if ring > 0;
+        ring=True means the whole capacity)."""
         _require_gpu(k, v)
         if k.dtype != torch.float16 or v.dtype != torch.float16:
             raise HeteroKVError(-1, "F16Zone.write: k/v must be fp16")
@@ -218,9 +219,15 @@ class F16Zone:
         a = _lib.ZoneWriteArgs(k=k.data_ptr(), v=v.data_ptr(), src_stride_b=k.stride(0),
                                src_stride_h=k.stride(1), src_stride_t=k.stride(2), batch=B, num_kv_heads=H,
                                head_dim=HEAD_DIM, num_tokens=T, slot_start=ss.data_ptr(),
-                               capacity=self.capacity, ring=1 if ring else 0,
+                               capacity=self.capacity, ring=(self.capacity if ring is True else int(ring)),
                                zone_k=self.k.data_ptr(), zone_v=self.v.data_ptr())
         check(load().hkv_zone_write(ctypes.byref(a), stream_ptr(k.device)), "hkv_zone_write")
+
+    def copy_to(self, dst, src_slot, dst_slot, n):
+        """Copy slots [src_slot, src_slot + n) to dst's [dst_slot, dst_slot + n) (no wrap)."""
+        check(load().hkv_zone_copy(_p(self.k), _p(self.v), self.capacity, src_slot, _p(dst.k), _p(dst.v),
+                                   dst.capacity, dst_slot, self.batch, self.num_kv_heads, HEAD_DIM, n,
+                                   stream_ptr(self.device)), "hkv_zone_copy")
 
     def read(self, n):
         """Slots [0, n) as row-major (K, V) [B, H, n, 128]."""

@@ -165,10 +165,10 @@ int hkv_unpack_tokens(const uint8_t* pool, int64_t pool_blocks, const int32_t* b
                       uint8_t* codes, float* scales, uint8_t* zps, void* stream);
 
 /*
- * Write `num_tokens` fp16/bf16 tokens into an fp16 zone (sink / recent window /
- * heavy hitters).  Token t of sequence b goes to slot slot_start[b] + t (mod
- * capacity when `ring` != 0).  K rows are copied; V goes to transposed tiles.
- * Source dtype must match the zone dtype (fp16).
+ * Write `num_tokens` fp16 tokens into an fp16 zone (sink / recent window /
+ * heavy hitters).  Token t of sequence b goes to slot slot_start[b] + t, taken
+ * modulo `ring` when ring > 0 (a ring of that many slots, ring <= capacity).
+ * K rows are copied; V goes to transposed tiles.
  */
 typedef struct HkvZoneWriteArgs {
     const uint16_t* k;
@@ -177,7 +177,7 @@ typedef struct HkvZoneWriteArgs {
     int32_t batch, num_kv_heads, head_dim, num_tokens;
     const int32_t* slot_start;     /* [batch], device */
     int32_t capacity;              /* slots per (b,h); multiple of 16 */
-    int32_t ring;
+    int32_t ring;                  /* 0 = no wrap, else ring length (<= capacity) */
     uint16_t* zone_k;              /* [batch][H][capacity][128] */
     uint16_t* zone_v;              /* [batch][H][capacity/16][4096 B tiles] */
 } HkvZoneWriteArgs;
@@ -188,6 +188,17 @@ int hkv_zone_write(const HkvZoneWriteArgs* args, void* stream);
 int hkv_zone_read(const uint16_t* zone_k, const uint16_t* zone_v, int32_t batch,
                   int32_t num_kv_heads, int32_t head_dim, int32_t capacity, int32_t n,
                   uint16_t* out_k, uint16_t* out_v, void* stream);
+
+/*
+ * Copy n consecutive slots of one fp16 zone to another (both K rows and V
+ * tiles), slot src_slot + i -> dst_slot + i for every sequence and head.  Used
+ * to move a token evicted from the recent window into the heavy-hitter zone
+ * (manager.py:645-664 and :686-715).  Ranges must not wrap and must lie inside
+ * both capacities.
+ */
+int hkv_zone_copy(const uint16_t* src_k, const uint16_t* src_v, int32_t src_capacity, int32_t src_slot,
+                  uint16_t* dst_k, uint16_t* dst_v, int32_t dst_capacity, int32_t dst_slot,
+                  int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t n, void* stream);
 
 /*
  * Split-K decode attention over [fp16 zones || INT4 pool] for one query token per
