@@ -1,0 +1,512 @@
+// Chunked-prefill attention over [INT4 pool | fp16 zones | causal chunk] on MFMA.
+//
+// Math (fused_dequant_attn.py:242-247,388-390; kernels/fused_dequant_attn.py:371-435
+// is the reference entry point): out[q] = softmax_t(q . K_t * sm_scale) V_t over every
+// INT4 token (dequantized exactly as KVCompressor.decompress to fp16), every fp16 zone
+// token and the chunk's own tokens t <= q (causal), GQA q head i -> kv head i / n_rep.
+//
+// Mapping.  A workgroup = 4 wavefronts = 4 query heads of one kv head (a GQA group)
+// x 32 query rows; the group shares each 64-token K/V tile, which all 256 lanes
+// dequantize / copy into LDS (double buffered, next tile's global loads in flight
+// during the current tile's math).  Per wave and tile, with v_mfma_f32_32x32x16_f16:
+//   S^T[64 tok x 32 q] = K[tok][d] . Q^T      (2 token blocks x 8 k-steps)
+//   O^T[128 d x 32 q] += V^T[d][tok] . P^T    (4 dim blocks x 4 token steps)
+// The S^T accumulator of lane (query n, half h) holds tokens 8j + 4h + i, exactly
+// the 8-token k-slices the P^T operand needs, so P never leaves registers.  LDS rows
+// are XOR-swizzled (16-byte chunks for K, 8-byte units for V^T) against bank conflicts.
+#include "hkv_internal.h"
+
+#include <math.h>
+
+namespace hkv {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+constexpr int kQ = 32;            // query rows per wave
+constexpr int kT = 64;            // tokens per tile
+constexpr int kWavesP = 4;
+constexpr int kThreadsP = 256;
+constexpr int kTileBytes = kT * kHeadDim * 2;     // 16 KB for K, 16 KB for V^T
+constexpr float kLog2eP = 1.4426950408889634f;
+
+struct ZoneP {
+    const uint16_t* k;
+    const uint16_t* v;
+    int cap;
+    int max_len;
+    const int32_t* lens;
+};
+
+struct PrefillParams {
+    int B, Hkv, nrep, Sq;
+    float scale_log2;
+    const uint16_t* q;
+    int64_t q_sb, q_sh, q_st;
+    int nz;
+    ZoneP z[HKV_MAX_F16_ZONES];
+    const uint8_t* pool;
+    int64_t pool_blocks;
+    const int32_t* bt;
+    int bt_stride;
+    const int32_t* int4_lens;
+    int int4_max_len;
+    const uint16_t* ck;          // causal chunk K/V [B][Hkv][Sq][128] (may be null)
+    const uint16_t* cv;
+    int64_t c_sb, c_sh, c_st;
+    uint16_t* out;
+    int64_t o_sb, o_sh, o_st;
+    int* err;
+};
+
+// LDS addresses (bytes) of the swizzled tiles.
+__device__ __forceinline__ int k_addr(int tok, int chunk) { return tok * 256 + ((chunk ^ (tok & 15)) << 4); }
+__device__ __forceinline__ int vt_addr(int dim, int unit) { return kTileBytes + dim * 128 + ((unit ^ (dim & 15)) << 3); }
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return (uint32_t)f2h_rn(a) | ((uint32_t)f2h_rn(b) << 16);
+}
+
+// Staged global data of one tile for one thread (all tile kinds).
+struct Stage {
+    u4 a[4];      // K part (INT4: a[0] = 16 B codes; fp16: 4 x 16 B row pieces)
+    u4 b[4];      // V part (INT4: b[0] = 16 B codes; fp16: 4 x 16 B)
+    float ks, vs[4];
+    uint32_t kz, vz;
+    int kind;     // 0 = INT4, 1 = zone tile, 2 = chunk rows, 3 = empty
+    int valid;    // tokens valid in this thread's slice
+};
+
+// Tile enumeration: INT4 tiles, then each zone's tiles, then the causal chunk's tiles.
+struct TileMap {
+    int n4, nz_t[HKV_MAX_F16_ZONES], nc;
+    int len4, lenz[HKV_MAX_F16_ZONES];
+};
+
+__device__ __forceinline__ void stage_load(const PrefillParams& p, const TileMap& tm, int b, int h, int tile,
+                                           Stage& s) {
+    const int t = threadIdx.x;
+    s.kind = 3;
+    s.valid = 0;
+    int x = tile;
+    if (x < tm.n4) {
+        // INT4: 4 blocks of 16 tokens.  K: thread -> block t/64, token (t/4)%16, 32 dims (t%4).
+        const int lb0 = x * 4;
+        const int blk = t >> 6;
+        const int lb = lb0 + blk;
+        const int nb = (tm.len4 + kBlockTokens - 1) / kBlockTokens;
+        s.kind = 0;
+        int phys = 0;
+        if (lb < nb) {
+            phys = p.bt[(int64_t)b * p.bt_stride + lb];
+            if (phys < 0 || (int64_t)phys >= p.pool_blocks) {
+                if (p.err) atomicOr(p.err, 1);
+                phys = 0;
+            }
+        }
+        const int H = p.Hkv;
+        const uint8_t* rec = p.pool + (int64_t)phys * ((int64_t)H * 2208);
+        const int rr = (t >> 2) & 15, pt = t & 3;
+        const int tok0 = lb * kBlockTokens;
+        s.valid = (lb < nb) ? min(kBlockTokens, tm.len4 - tok0) : 0;
+        if (lb < nb) {
+            s.a[0] = *(const u4*)(rec + h * 1024 + rr * 64 + pt * 16);
+            s.ks = *(const float*)(rec + (int64_t)H * 2048 + h * 64 + rr * 4);
+            s.kz = rec[(int64_t)H * 2176 + h * 16 + rr];
+            // V: words (t%64)*4 .. +3 of this block: tokens 4g..4g+3, g = (t%64)/16
+            const int g = (t & 63) >> 4;
+            s.b[0] = *(const u4*)(rec + (int64_t)H * 1024 + h * 1024 + (t & 63) * 16);
+            const float4 vs4 = *(const float4*)(rec + (int64_t)H * 2112 + h * 64 + g * 16);
+            s.vs[0] = vs4.x;
+            s.vs[1] = vs4.y;
+            s.vs[2] = vs4.z;
+            s.vs[3] = vs4.w;
+            s.vz = *(const uint32_t*)(rec + (int64_t)H * 2192 + h * 16 + g * 4);
+        }
+        return;
+    }
+    x -= tm.n4;
+#pragma unroll
+    for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
+        if (zi < p.nz && x >= 0 && x < tm.nz_t[zi]) {
+            const ZoneP& z = p.z[zi];
+            const int64_t bh = (int64_t)b * p.Hkv + h;
+            const int tok = x * kT + (t >> 2);        // K row of this thread
+            s.kind = 1;
+            s.valid = tm.lenz[zi] - x * kT;           // tokens valid in the tile (may exceed 64)
+            if (tok < tm.lenz[zi]) {
+                const uint16_t* kp = z.k + (bh * z.cap + tok) * kHeadDim + (t & 3) * 32;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s.a[j] = *(const u4*)(kp + 8 * j);
+            }
+            // V: zone tile zt = t/64 of the four 16-token tiles, (g, c) = t%64: 32 halves
+            const int zt = x * 4 + (t >> 6);
+            if (zt * kBlockTokens < tm.lenz[zi]) {
+                const uint16_t* vp = z.v + (bh * (z.cap / kBlockTokens) + zt) * (kBlockTokens * kHeadDim) + (t & 63) * 32;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s.b[j] = *(const u4*)(vp + 8 * j);
+            }
+            x = -1;
+        }
+        if (zi < p.nz && x >= 0) x -= tm.nz_t[zi];
+    }
+    if (x >= 0 && x < tm.nc && p.ck) {
+        const int tok = x * kT + (t >> 2);
+        s.kind = 2;
+        s.valid = p.Sq - x * kT;
+        if (tok < p.Sq) {
+            const uint16_t* kp = p.ck + (int64_t)b * p.c_sb + (int64_t)h * p.c_sh + (int64_t)tok * p.c_st + (t & 3) * 32;
+            const uint16_t* vp = p.cv + (int64_t)b * p.c_sb + (int64_t)h * p.c_sh + (int64_t)tok * p.c_st + (t & 3) * 32;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s.a[j] = *(const u4*)(kp + 8 * j);
+                s.b[j] = *(const u4*)(vp + 8 * j);
+            }
+        }
+    }
+}
+
+// Writes the staged data of one tile into LDS buffer `lds` (K rows + V^T), zeros for
+// slots past the valid length so that masked probabilities multiply finite values.
+__device__ __forceinline__ void stage_store(const Stage& s, uint8_t* lds) {
+    const int t = threadIdx.x;
+    if (s.kind == 0) {
+        const int blk = t >> 6, rr = (t >> 2) & 15, pt = t & 3;
+        const int tok = blk * 16 + rr;
+        const bool ok = rr < s.valid;
+        const float zf = (float)s.kz;
+        const uint32_t w4[4] = {s.a[0].x, s.a[0].y, s.a[0].z, s.a[0].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {          // word j: dims 32pt + 8j .. +8
+            u4 o;
+            uint32_t r[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t pr = (w4[j] >> (4 * i)) & 0x000F000Fu;
+                const float lo = ((float)(pr & 0xF) - zf) * s.ks;
+                const float hi = ((float)(pr >> 16) - zf) * s.ks;
+                r[i] = ok ? pack2(lo, hi) : 0u;
+            }
+            o = u4{r[0], r[1], r[2], r[3]};
+            *(u4*)(lds + k_addr(tok, pt * 4 + j)) = o;
+        }
+        const int g = (t & 63) >> 4, c = t & 15;
+        float zf4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) zf4[i] = (float)((s.vz >> (8 * i)) & 0xFF);
+        const uint32_t v4[4] = {s.b[0].x, s.b[0].y, s.b[0].z, s.b[0].w};
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            const uint32_t w = v4[mm];
+            // x_k at bit (k%2)*16 + (k/2)*4: x0..x3 = tokens 4g..4g+3 at dim c+32mm, x4..x7 at +16
+            float val[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int tk = k & 3;
+                const float code = (float)((w >> nib_shift(k)) & 0xFu);
+                val[k] = (4 * g + tk < s.valid) ? (code - zf4[tk]) * s.vs[tk] : 0.0f;
+            }
+            const int unit = blk * 4 + g;
+            const int d1 = c + 32 * mm, d2 = d1 + 16;
+            *(u2*)(lds + vt_addr(d1, unit)) = u2{pack2(val[0], val[1]), pack2(val[2], val[3])};
+            *(u2*)(lds + vt_addr(d2, unit)) = u2{pack2(val[4], val[5]), pack2(val[6], val[7])};
+        }
+    } else if (s.kind == 1 || s.kind == 2 || s.kind == 3) {
+        const int tok = t >> 2, pt = t & 3;
+        const bool okk = s.kind != 3 && tok < s.valid;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *(u4*)(lds + k_addr(tok, pt * 4 + j)) = okk ? s.a[j] : u4{0u, 0u, 0u, 0u};
+        if (s.kind == 1) {
+            // zone V tile zt: halves [n][i] = V[4g+i][c+16n] -> V^T rows c+16n, unit zt*4+g
+            const int zt = t >> 6, g = (t & 63) >> 4, c = t & 15;
+            const int base_tok = zt * 16 + 4 * g;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int n = 2 * j + e;
+                    u2 val = e == 0 ? u2{s.b[j].x, s.b[j].y} : u2{s.b[j].z, s.b[j].w};
+                    // clear tokens past the length
+                    const uint32_t m01 = (base_tok + 0 < s.valid ? 0x0000FFFFu : 0u) | (base_tok + 1 < s.valid ? 0xFFFF0000u : 0u);
+                    const uint32_t m23 = (base_tok + 2 < s.valid ? 0x0000FFFFu : 0u) | (base_tok + 3 < s.valid ? 0xFFFF0000u : 0u);
+                    val.x &= m01;
+                    val.y &= m23;
+                    *(u2*)(lds + vt_addr(c + 16 * n, zt * 4 + g)) = val;
+                }
+            }
+        } else {
+            // row-major V (chunk) or empty: scatter 32 dims of token `tok` into V^T
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                const int d = pt * 32 + e;
+                const uint32_t w = s.b[e >> 3][(e >> 1) & 3];
+                const uint16_t v = okk ? (uint16_t)(w >> ((e & 1) * 16)) : (uint16_t)0;
+                *(uint16_t*)(lds + vt_addr(d, tok >> 2) + (tok & 3) * 2) = v;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreadsP) void prefill_attn_kernel(PrefillParams p) {
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    const int b = blockIdx.z;
+    const int ngrp = (p.nrep + kWavesP - 1) / kWavesP;
+    const int h = blockIdx.y / ngrp, grp = blockIdx.y % ngrp;
+    const int q0 = blockIdx.x * kQ;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 31, hh = lane >> 5;
+    const int rep = grp * kWavesP + wave;
+    const bool head_ok = rep < p.nrep;
+    const int qh = h * p.nrep + (head_ok ? rep : 0);
+    const int qrow = q0 + n;
+
+    TileMap tm;
+    tm.len4 = p.int4_lens ? min(max(p.int4_lens[b], 0), p.int4_max_len) : p.int4_max_len;
+    tm.n4 = (tm.len4 + kT - 1) / kT;
+#pragma unroll
+    for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
+        tm.lenz[zi] = 0;
+        if (zi < p.nz) tm.lenz[zi] = p.z[zi].lens ? min(max(p.z[zi].lens[b], 0), p.z[zi].max_len) : p.z[zi].max_len;
+        tm.nz_t[zi] = (tm.lenz[zi] + kT - 1) / kT;
+    }
+    // causal chunk tiles up to the last query row of this block
+    tm.nc = p.ck ? (min(q0 + kQ, p.Sq) + kT - 1) / kT : 0;
+    int ntiles = tm.n4 + tm.nc;
+#pragma unroll
+    for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) ntiles += (zi < p.nz) ? tm.nz_t[zi] : 0;
+    const int first_chunk_tile = ntiles - tm.nc;
+
+    // Q^T fragments: lane (query n, half hh) step s -> q[qrow][16s + 8hh .. +8]
+    h8 qf[8];
+    {
+        const bool ok = head_ok && qrow < p.Sq;
+        const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)qh * p.q_sh + (int64_t)(ok ? qrow : 0) * p.q_st + 8 * hh;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const u4 w = ok ? *(const u4*)(qp + 16 * s) : u4{0u, 0u, 0u, 0u};
+            qf[s] = __builtin_bit_cast(h8, w);
+        }
+    }
+    f16v acc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+
+    Stage st;
+    if (ntiles > 0) {
+        stage_load(p, tm, b, h, 0, st);
+        stage_store(st, lds_raw);
+    }
+    __syncthreads();
+    for (int tile = 0; tile < ntiles; ++tile) {
+        uint8_t* cur = lds_raw + (tile & 1) * (2 * kTileBytes);
+        uint8_t* nxt = lds_raw + ((tile + 1) & 1) * (2 * kTileBytes);
+        if (tile + 1 < ntiles) stage_load(p, tm, b, h, tile + 1, st);
+
+        // valid tokens of this tile and causal limit
+        int tvalid = kT;
+        int causal_base = -1;  // chunk position of token 0 of this tile, or -1
+        {
+            int x = tile;
+            if (x < tm.n4) {
+                tvalid = min(kT, tm.len4 - x * kT);
+            } else {
+                x -= tm.n4;
+                bool found = false;
+#pragma unroll
+                for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
+                    if (!found && zi < p.nz) {
+                        if (x < tm.nz_t[zi]) {
+                            tvalid = min(kT, tm.lenz[zi] - x * kT);
+                            found = true;
+                        } else {
+                            x -= tm.nz_t[zi];
+                        }
+                    }
+                }
+                if (!found) {
+                    tvalid = min(kT, p.Sq - x * kT);
+                    causal_base = x * kT;
+                }
+            }
+        }
+
+        // ---- S^T = K . Q^T for two 32-token blocks
+        f16v S[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) S[tb][r] = 0.f;
+            const int tok = tb * 32 + n;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const h8 a = __builtin_bit_cast(h8, *(const u4*)(cur + k_addr(tok, 2 * s + hh)));
+                S[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], S[tb], 0, 0, 0);
+            }
+        }
+        // ---- scores, mask, online softmax (per query = per lane column n)
+        float mt = -INFINITY;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int tok = tb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                bool ok = tok < tvalid;
+                if (causal_base >= 0) ok = ok && (causal_base + tok <= qrow);
+                const float sv = ok ? S[tb][r] * p.scale_log2 : -INFINITY;
+                S[tb][r] = sv;
+                mt = fmaxf(mt, sv);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        if (__ballot(mt > m)) {
+            const float m_new = fmaxf(m, mt);
+            const float alpha = (m_new > m) ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+            l *= alpha;
+            m = m_new;
+        }
+        const float msafe = (m == -INFINITY) ? 0.f : m;
+        h8 P[2][2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = 4 * (2 * u + jj) + i;
+                        const float pv = __builtin_amdgcn_exp2f(S[tb][r] - msafe);
+                        l += pv;
+                        P[tb][u][jj * 4 + i] = (_Float16)pv;
+                    }
+        // ---- O^T += V^T . P^T (4 dim blocks x 4 token steps)
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int unit0 = tb * 8 + 4 * u + hh;      // tokens tb*32 + 16u + 4hh (+8 for jj=1)
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const int dim = 32 * db + n;
+                    const u2 lo = *(const u2*)(cur + vt_addr(dim, unit0));
+                    const u2 hi = *(const u2*)(cur + vt_addr(dim, unit0 + 2));
+                    const h8 a = __builtin_bit_cast(h8, u4{lo.x, lo.y, hi.x, hi.y});
+                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, P[tb][u], acc[db], 0, 0, 0);
+                }
+            }
+        if (tile + 1 < ntiles) stage_store(st, nxt);
+        __syncthreads();
+    }
+    (void)first_chunk_tile;
+
+    l += __shfl_xor(l, 32);
+    if (head_ok && qrow < p.Sq) {
+        const float inv = l > 0.f ? 1.0f / l : 0.f;
+        uint16_t* op = p.out + (int64_t)b * p.o_sb + (int64_t)qh * p.o_sh + (int64_t)qrow * p.o_st;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = 32 * db + 8 * j + 4 * hh;
+                *(u2*)(op + d) = u2{pack2(acc[db][4 * j + 0] * inv, acc[db][4 * j + 1] * inv),
+                                    pack2(acc[db][4 * j + 2] * inv, acc[db][4 * j + 3] * inv)};
+            }
+    }
+}
+
+}  // namespace
+}  // namespace hkv
+
+using namespace hkv;
+
+extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
+    clear_error();
+    HKV_REQUIRE(a != nullptr, HKV_ERR_ARG, "hkv_prefill_attn: null args");
+    HKV_REQUIRE(a->head_dim == kHeadDim, HKV_ERR_UNSUPPORTED, "hkv_prefill_attn: head_dim %d != 128", a->head_dim);
+    HKV_REQUIRE(a->batch > 0 && a->num_kv_heads > 0 && a->num_q_heads > 0 && a->num_queries > 0, HKV_ERR_ARG,
+                "hkv_prefill_attn: bad sizes");
+    HKV_REQUIRE(a->num_q_heads % a->num_kv_heads == 0, HKV_ERR_ARG,
+                "hkv_prefill_attn: num_q_heads %d not a multiple of num_kv_heads %d", a->num_q_heads,
+                a->num_kv_heads);
+    HKV_REQUIRE(a->num_f16_zones >= 0 && a->num_f16_zones <= HKV_MAX_F16_ZONES, HKV_ERR_ARG,
+                "hkv_prefill_attn: num_f16_zones out of range");
+    HKV_REQUIRE(a->q && a->out, HKV_ERR_ARG, "hkv_prefill_attn: null q/out");
+    HKV_REQUIRE((((uintptr_t)a->q) & 15) == 0 && a->q_stride_b % 8 == 0 && a->q_stride_h % 8 == 0 &&
+                    a->q_stride_t % 8 == 0,
+                HKV_ERR_ARG, "hkv_prefill_attn: q must be 16-byte aligned with strides multiple of 8");
+    HKV_REQUIRE((((uintptr_t)a->out) & 7) == 0 && a->out_stride_b % 4 == 0 && a->out_stride_h % 4 == 0 &&
+                    a->out_stride_t % 4 == 0,
+                HKV_ERR_ARG, "hkv_prefill_attn: out must be 8-byte aligned with strides multiple of 4");
+    if (a->chunk_k || a->chunk_v) {
+        HKV_REQUIRE(a->chunk_k && a->chunk_v, HKV_ERR_ARG, "hkv_prefill_attn: chunk K and V must both be given");
+        HKV_REQUIRE((((uintptr_t)a->chunk_k | (uintptr_t)a->chunk_v) & 15) == 0 && a->chunk_stride_b % 8 == 0 &&
+                        a->chunk_stride_h % 8 == 0 && a->chunk_stride_t % 8 == 0,
+                    HKV_ERR_ARG, "hkv_prefill_attn: chunk K/V must be 16-byte aligned, strides multiple of 8");
+    }
+    HKV_REQUIRE(a->int4_max_len >= 0, HKV_ERR_ARG, "hkv_prefill_attn: int4_max_len < 0");
+    if (a->int4_max_len > 0) {
+        HKV_REQUIRE(a->pool && a->block_table && a->pool_blocks > 0, HKV_ERR_ARG,
+                    "hkv_prefill_attn: INT4 zone without pool/block table");
+        HKV_REQUIRE((int64_t)a->bt_stride * kBlockTokens >= a->int4_max_len, HKV_ERR_CAPACITY,
+                    "hkv_prefill_attn: block table stride too small");
+    }
+    for (int i = 0; i < a->num_f16_zones; ++i) {
+        const HkvF16Zone& z = a->f16[i];
+        HKV_REQUIRE(z.max_len >= 0 && z.max_len <= z.capacity && z.capacity % kBlockTokens == 0, HKV_ERR_ARG,
+                    "hkv_prefill_attn: zone %d length/capacity invalid", i);
+        if (z.max_len > 0)
+            HKV_REQUIRE(z.k && z.v && (((uintptr_t)z.k | (uintptr_t)z.v) & 15) == 0, HKV_ERR_ARG,
+                        "hkv_prefill_attn: zone %d k/v null or misaligned", i);
+    }
+    const int nrep = a->num_q_heads / a->num_kv_heads;
+    const int ngrp = (nrep + kWavesP - 1) / kWavesP;
+    HKV_REQUIRE((int64_t)a->num_kv_heads * ngrp < 65536 && a->batch < 65536, HKV_ERR_ARG,
+                "hkv_prefill_attn: grid too large");
+    PrefillParams p;
+    p.B = a->batch;
+    p.Hkv = a->num_kv_heads;
+    p.nrep = nrep;
+    p.Sq = a->num_queries;
+    p.scale_log2 = a->sm_scale * kLog2eP;
+    p.q = a->q;
+    p.q_sb = a->q_stride_b;
+    p.q_sh = a->q_stride_h;
+    p.q_st = a->q_stride_t;
+    p.nz = a->num_f16_zones;
+    for (int i = 0; i < HKV_MAX_F16_ZONES; ++i) {
+        const bool on = i < p.nz;
+        p.z[i].k = on ? a->f16[i].k : nullptr;
+        p.z[i].v = on ? a->f16[i].v : nullptr;
+        p.z[i].cap = on ? a->f16[i].capacity : 0;
+        p.z[i].max_len = on ? a->f16[i].max_len : 0;
+        p.z[i].lens = on ? a->f16[i].lens : nullptr;
+    }
+    p.pool = a->pool;
+    p.pool_blocks = a->pool_blocks;
+    p.bt = a->block_table;
+    p.bt_stride = a->bt_stride;
+    p.int4_lens = a->int4_lens;
+    p.int4_max_len = a->int4_max_len;
+    p.ck = a->chunk_k;
+    p.cv = a->chunk_v;
+    p.c_sb = a->chunk_stride_b;
+    p.c_sh = a->chunk_stride_h;
+    p.c_st = a->chunk_stride_t;
+    p.out = a->out;
+    p.o_sb = a->out_stride_b;
+    p.o_sh = a->out_stride_h;
+    p.o_st = a->out_stride_t;
+    p.err = a->err_flag;
+    const dim3 grid((a->num_queries + kQ - 1) / kQ, a->num_kv_heads * ngrp, a->batch);
+    hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kThreadsP), 4 * kTileBytes, (hipStream_t)stream, p);
+    HKV_LAUNCH_CHECK("prefill_attn_kernel");
+    return HKV_OK;
+}

@@ -9,11 +9,11 @@ plus the block-pool / fp16-zone primitives in ``heterokv.ops``.
 """
 from ._lib import HeteroKVError, load  # noqa: F401
 from .kv_compressor import KVCompressor  # noqa: F401
-from .fused_dequant_attn import fused_dequant_attn_decode  # noqa: F401
+from .fused_dequant_attn import fused_dequant_attn_decode, fused_dequant_attn_forward  # noqa: F401
 from . import ops  # noqa: F401
 from .manager import HeteroKVManager  # noqa: F401
 from .engine_wrapper import (FusedHeteroCache, ChunkedPrefillEngine, build_fused_cache,  # noqa: F401
                              register_attention)
 
-__all__ = ["HeteroKVError", "KVCompressor", "fused_dequant_attn_decode", "ops", "load", "HeteroKVManager",
+__all__ = ["HeteroKVError", "KVCompressor", "fused_dequant_attn_decode", "fused_dequant_attn_forward", "ops", "load", "HeteroKVManager",
            "FusedHeteroCache", "ChunkedPrefillEngine", "build_fused_cache", "register_attention"]

@@ -77,6 +77,19 @@ class DecodeArgs(ctypes.Structure):
                 ("workspace", vp), ("workspace_bytes", ctypes.c_size_t), ("splits_hint", i32)]
 
 
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [("batch", i32), ("num_q_heads", i32), ("num_kv_heads", i32), ("head_dim", i32),
+                ("num_queries", i32), ("sm_scale", ctypes.c_float),
+                ("q", vp), ("q_stride_b", i64), ("q_stride_h", i64), ("q_stride_t", i64),
+                ("num_f16_zones", i32), ("f16", F16Zone * MAX_F16_ZONES),
+                ("pool", vp), ("pool_blocks", i64), ("block_table", vp), ("bt_stride", i32),
+                ("int4_lens", vp), ("int4_max_len", i32),
+                ("chunk_k", vp), ("chunk_v", vp),
+                ("chunk_stride_b", i64), ("chunk_stride_h", i64), ("chunk_stride_t", i64),
+                ("out", vp), ("out_stride_b", i64), ("out_stride_h", i64), ("out_stride_t", i64),
+                ("err_flag", vp)]
+
+
 # (name, restype, argtypes) of every symbol include/heterokv.h declares.
 SYMBOLS = [
     ("hkv_abi_version", ctypes.c_int, []),
@@ -92,6 +105,7 @@ SYMBOLS = [
     ("hkv_zone_copy", ctypes.c_int, [vp, vp, i32, i32, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
     ("hkv_decode_workspace_bytes", ctypes.c_size_t, [i32, i32, i32, i32, i32, vp, i32]),
     ("hkv_decode_attn", ctypes.c_int, [ctypes.POINTER(DecodeArgs), vp]),
+    ("hkv_prefill_attn", ctypes.c_int, [ctypes.POINTER(PrefillArgs), vp]),
 ]
 
 _lock = threading.Lock()

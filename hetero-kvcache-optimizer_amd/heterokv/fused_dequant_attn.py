@@ -1,7 +1,8 @@
 """Fused dequant-attention entry points on the GPU.
 
 Drop-ins for the reference's src/quantization/kernels/fused_dequant_attn.py:301-368
-(``fused_dequant_attn_decode``) with the numerics of its torch path
+(``fused_dequant_attn_decode``) and :371-435 (``fused_dequant_attn_forward``) with the
+numerics of its torch path
 (src/quantization/fused_dequant_attn.py:326-331,388-390):
     K = (Kq - zp) * s, V = (Vq - zp) * s, out = softmax(q K^T * sm_scale) V,
 sm_scale defaulting to 1/sqrt(head_dim).  Unlike the reference's Triton kernel
@@ -10,7 +11,8 @@ exactly that formula, and it also accepts GQA (q heads a multiple of kv heads).
 
 The reference passes unpacked codes (one uint8 per value) with per-token
 scales/zps [B, H, S]; they are repacked into INT4 block records on the device
-(hkv_repack_codes) and attended by the split-K kernel (hkv_decode_attn).
+(hkv_repack_codes) and attended by the split-K decode kernel (hkv_decode_attn) or the
+MFMA prefill kernel (hkv_prefill_attn).
 """
 import math
 from typing import Optional
@@ -54,4 +56,33 @@ def fused_dequant_attn_decode(q: torch.Tensor, k_data: torch.Tensor, k_scales: t
     q16 = q if q.dtype == torch.float16 else q.to(torch.float16)
     out = ops.decode_attention(q16, zones=(), pool=pool, block_table=bt, int4_lens=None, int4_max_len=S,
                                sm_scale=sm_scale)
+    return out.to(q.dtype)
+
+
+def _repack_reference(q, k_data, k_scales, k_zps, v_data, v_scales, v_zps):
+    B = q.shape[0]
+    kd, vd = _as_4d(k_data), _as_4d(v_data)
+    Hkv, S = kd.shape[1], kd.shape[2]
+    nblk = (S + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+    pool = ops.Int4Pool(B * nblk, Hkv, q.device)
+    bt = torch.arange(B * nblk, dtype=torch.int32, device=q.device).reshape(B, nblk)
+    start = torch.zeros(B, dtype=torch.int32, device=q.device)
+    ops.repack_codes(pool, kd, vd, k_scales.reshape(B, Hkv, S), v_scales.reshape(B, Hkv, S),
+                     k_zps.reshape(B, Hkv, S), v_zps.reshape(B, Hkv, S), start, bt)
+    return pool, bt, S
+
+
+def fused_dequant_attn_forward(q: torch.Tensor, k_data: torch.Tensor, k_scales: torch.Tensor,
+                               k_zps: torch.Tensor, v_data: torch.Tensor, v_scales: torch.Tensor,
+                               v_zps: torch.Tensor, sm_scale: Optional[float] = None) -> torch.Tensor:
+    """q [B, Hq, Sq, D] fp16/bf16 against quantized K/V [B, Hkv, S, D] (all keys visible,
+    as the reference's torch path) -> [B, Hq, Sq, D] in q.dtype."""
+    if q.dim() != 4:
+        raise HeteroKVError(-1, "Forward expects [B,H,S,D], got %s" % (tuple(q.shape),))
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(q.shape[-1])
+    pool, bt, S = _repack_reference(q, k_data, k_scales, k_zps, v_data, v_scales, v_zps)
+    q16 = q if q.dtype == torch.float16 else q.to(torch.float16)
+    out = ops.prefill_attention(q16, pool=pool, block_table=bt, int4_max_len=S, sm_scale=sm_scale)
+    pool.check_errors()
     return out.to(q.dtype)

@@ -339,3 +339,69 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
     a.splits_hint = int(splits)
     check(load().hkv_decode_attn(ctypes.byref(a), stream_ptr(dev)), "hkv_decode_attn")
     return out.unsqueeze(2) if squeeze else out
+
+
+# ----------------------------------------------------------------------- prefill attention
+def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
+                      chunk_k=None, chunk_v=None, sm_scale=None, out=None):
+    """Chunked-prefill attention (hkv_prefill_attn).
+
+    q: [B, Hq, Sq, 128] fp16.  Every query attends to all fp16-zone tokens and all INT4
+    tokens, plus -- when chunk_k/chunk_v [B, Hkv, Sq, 128] fp16 are given -- causally to
+    the chunk itself.  Returns fp16 [B, Hq, Sq, 128].
+    """
+    _require_gpu(q, chunk_k, chunk_v)
+    if q.dtype != torch.float16 or q.dim() != 4 or q.shape[-1] != HEAD_DIM:
+        raise HeteroKVError(-1, "prefill_attention: q must be fp16 [B, Hq, Sq, 128]")
+    if q.stride(-1) != 1 or q.data_ptr() % 16 or any(st % 8 for st in q.stride()[:3]):
+        q = q.contiguous()
+    B, Hq, Sq, _ = q.shape
+    Hkv = pool.num_kv_heads if pool is not None else (zones[0][0].num_kv_heads if zones else
+                                                       (chunk_k.shape[1] if chunk_k is not None else None))
+    if Hkv is None:
+        raise HeteroKVError(-1, "prefill_attention: no key/value source given")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(HEAD_DIM)
+    dev = q.device
+    if out is None:
+        out = torch.empty((B, Hq, Sq, HEAD_DIM), dtype=torch.float16, device=dev)
+    a = _lib.PrefillArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.num_queries = B, Hq, Hkv, HEAD_DIM, Sq
+    a.sm_scale = float(sm_scale)
+    a.q, a.q_stride_b, a.q_stride_h, a.q_stride_t = q.data_ptr(), q.stride(0), q.stride(1), q.stride(2)
+    keep = []
+    a.num_f16_zones = len(zones)
+    for i, (z, lens, max_len) in enumerate(zones):
+        lt = None
+        if lens is not None:
+            lt = _i32(lens, dev)
+            keep.append(lt)
+        a.f16[i] = _lib.F16Zone(k=z.k.data_ptr(), v=z.v.data_ptr(), capacity=z.capacity, max_len=int(max_len),
+                                lens=lt.data_ptr() if lt is not None else 0)
+    err = None
+    if int4_max_len > 0:
+        bt = _i32(block_table, dev)
+        if bt.dim() == 1:
+            bt = bt.unsqueeze(0)
+        keep.append(bt)
+        a.pool, a.pool_blocks = pool.data.data_ptr(), pool.num_blocks
+        a.block_table, a.bt_stride = bt.data_ptr(), bt.shape[1]
+        err = pool.err
+        if int4_lens is not None:
+            il = _i32(int4_lens, dev)
+            keep.append(il)
+            a.int4_lens = il.data_ptr()
+    a.int4_max_len = int(int4_max_len)
+    if chunk_k is not None:
+        if chunk_k.shape != (B, Hkv, Sq, HEAD_DIM) or chunk_v.shape != chunk_k.shape:
+            raise HeteroKVError(-1, "prefill_attention: chunk K/V must be [B, Hkv, Sq, 128]")
+        if chunk_k.dtype != torch.float16 or chunk_v.dtype != torch.float16:
+            raise HeteroKVError(-1, "prefill_attention: chunk K/V must be fp16")
+        if chunk_k.stride() != chunk_v.stride() or chunk_k.stride(-1) != 1:
+            chunk_k, chunk_v = chunk_k.contiguous(), chunk_v.contiguous()
+        a.chunk_k, a.chunk_v = chunk_k.data_ptr(), chunk_v.data_ptr()
+        a.chunk_stride_b, a.chunk_stride_h, a.chunk_stride_t = chunk_k.stride(0), chunk_k.stride(1), chunk_k.stride(2)
+    a.out, a.out_stride_b, a.out_stride_h, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1), out.stride(2)
+    a.err_flag = err.data_ptr() if err is not None else 0
+    check(load().hkv_prefill_attn(ctypes.byref(a), stream_ptr(dev)), "hkv_prefill_attn")
+    return out

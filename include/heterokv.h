@@ -241,6 +241,37 @@ size_t hkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t nu
 
 int hkv_decode_attn(const HkvDecodeArgs* args, void* stream);
 
+/*
+ * Chunked-prefill attention (fused_dequant_attn_forward with GQA, kernels/
+ * fused_dequant_attn.py:371-435; numerics fused_dequant_attn.py:242-247): every
+ * query row of q attends to all tokens of the fp16 zones and of the INT4 pool
+ * (dequantized to fp16 exactly as KVCompressor.decompress) and, when chunk_k/chunk_v
+ * are given, causally to the chunk's own tokens (row i sees chunk rows 0..i).
+ * fp16 in, fp16 out, fp32 accumulation on MFMA.
+ */
+typedef struct HkvPrefillArgs {
+    int32_t batch, num_q_heads, num_kv_heads, head_dim, num_queries;
+    float sm_scale;
+    const uint16_t* q;             /* [batch][num_q_heads][num_queries][128] with strides */
+    int64_t q_stride_b, q_stride_h, q_stride_t;
+    int32_t num_f16_zones;
+    HkvF16Zone f16[HKV_MAX_F16_ZONES];
+    const uint8_t* pool;
+    int64_t pool_blocks;
+    const int32_t* block_table;
+    int32_t bt_stride;
+    const int32_t* int4_lens;
+    int32_t int4_max_len;
+    const uint16_t* chunk_k;       /* optional causal chunk [batch][num_kv_heads][num_queries][128] */
+    const uint16_t* chunk_v;
+    int64_t chunk_stride_b, chunk_stride_h, chunk_stride_t;
+    uint16_t* out;                 /* [batch][num_q_heads][num_queries][128] with strides */
+    int64_t out_stride_b, out_stride_h, out_stride_t;
+    int32_t* err_flag;             /* optional: bit 0 set if a block id was out of range */
+} HkvPrefillArgs;
+
+int hkv_prefill_attn(const HkvPrefillArgs* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

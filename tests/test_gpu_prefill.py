@@ -1,0 +1,134 @@
+"""GPU parity: MFMA chunked-prefill attention (hkv_prefill_attn) against the float64
+oracle over [INT4 (Path C fp16 dequant) | fp16 zones | causal chunk]; 2e-3 max-abs."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import compressor as oc
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TOL = 2e-3
+
+
+def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0):
+    from heterokv import ops
+    g = torch.Generator().manual_seed(seed)
+    hist = sink + max(mids) + max(recents)
+    K = torch.randn((B, Hkv, hist, 128), generator=g)
+    K[..., [7, 31, 64, 100]] *= 8
+    K = K.half()
+    V = torch.randn((B, Hkv, hist, 128), generator=g).half()
+    CK = torch.randn((B, Hkv, Sq, 128), generator=g).half()
+    CV = torch.randn((B, Hkv, Sq, 128), generator=g).half()
+    q = (torch.randn((B, Hq, Sq, 128), generator=g) * q_scale / math.sqrt(128)).half()
+    zones = []
+    if sink:
+        zs = ops.F16Zone(B, Hkv, sink, DEV)
+        zs.write(K[:, :, :sink].to(DEV), V[:, :, :sink].to(DEV), [0] * B)
+        zones.append((zs, None, sink))
+    if max(recents):
+        rmax = max(recents)
+        zr = ops.F16Zone(B, Hkv, rmax, DEV)
+        kr = torch.zeros((B, Hkv, rmax, 128), dtype=torch.float16)
+        vr = torch.zeros_like(kr)
+        for b in range(B):
+            s0 = sink + mids[b]
+            kr[b, :, :recents[b]] = K[b, :, s0:s0 + recents[b]]
+            vr[b, :, :recents[b]] = V[b, :, s0:s0 + recents[b]]
+        zr.write(kr.to(DEV), vr.to(DEV), [0] * B)
+        zones.append((zr, torch.tensor(recents, dtype=torch.int32).to(DEV), rmax))
+    nbs = [(m + 15) // 16 for m in mids]
+    nbmax = max(max(nbs), 1)
+    pool = ops.Int4Pool(sum(nbs) + 1, Hkv, DEV)
+    perm = torch.randperm(sum(nbs) + 1, generator=g).to(torch.int32)
+    bt = torch.zeros((B, nbmax), dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        bt[b, :nbs[b]] = perm[off:off + nbs[b]]
+        off += nbs[b]
+        if mids[b]:
+            ops.pack_tokens(pool, K[b:b + 1, :, sink:sink + mids[b]].to(DEV), V[b:b + 1, :, sink:sink + mids[b]].to(DEV),
+                            [0], bt[b:b + 1])
+    out = ops.prefill_attention(q.to(DEV), zones=zones, pool=pool, block_table=bt.to(DEV),
+                                int4_lens=torch.tensor(mids, dtype=torch.int32).to(DEV), int4_max_len=max(mids),
+                                chunk_k=CK.to(DEV) if causal else None, chunk_v=CV.to(DEV) if causal else None)
+    torch.cuda.synchronize()
+    pool.check_errors()
+    got = out.float().cpu().numpy()
+    for b in range(B):
+        m, r = mids[b], recents[b]
+        ks = [K[b, :, :sink].double().numpy()]
+        vs = [V[b, :, :sink].double().numpy()]
+        if m:
+            kc, kss, kz = oc.compress(K[b, :, sink:sink + m].numpy(), 128)
+            vc, vss, vz = oc.compress(V[b, :, sink:sink + m].numpy(), 128)
+            ks.append(oa.dequant_rows(kc, kss.reshape(Hkv, m), kz.reshape(Hkv, m)))
+            vs.append(oa.dequant_rows(vc, vss.reshape(Hkv, m), vz.reshape(Hkv, m)))
+        ks.append(K[b, :, sink + m:sink + m + r].double().numpy())
+        vs.append(V[b, :, sink + m:sink + m + r].double().numpy())
+        nh = sum(x.shape[1] for x in ks)
+        mask = np.ones((Sq, nh), dtype=bool)
+        if causal:
+            ks.append(CK[b].double().numpy())
+            vs.append(CV[b].double().numpy())
+            mask = np.concatenate([mask, np.tril(np.ones((Sq, Sq), dtype=bool))], axis=1)
+        ref = oa.attend(q[b].double().numpy(), np.concatenate(ks, 1), np.concatenate(vs, 1), mask=mask)
+        err = np.abs(got[b] - ref).max()
+        print("  b=%d max abs err %.3e" % (b, err), flush=True)
+        assert np.all(np.isfinite(got[b]))
+        assert err <= TOL
+
+
+def test_small_all_sources():
+    print("case: prefill B=1 8/2 Sq=70 sink 20 + INT4 150 + recent 37 + causal", flush=True)
+    _case(1, 1, 8, 2, 70, 20, [150], [37])
+
+
+def test_gqa7_c5_geometry():
+    print("case: prefill 28/4 Sq=33", flush=True)
+    _case(2, 1, 28, 4, 33, 64, [300], [100])
+
+
+def test_int4_only_no_causal():
+    print("case: prefill INT4 only", flush=True)
+    _case(3, 1, 4, 4, 50, 0, [500], [0], causal=False)
+
+
+def test_causal_only_sharp():
+    print("case: causal chunk only, sharp softmax", flush=True)
+    _case(4, 1, 8, 2, 130, 0, [0], [0], q_scale=8.0)
+
+
+def test_ragged_batch():
+    print("case: prefill B=2 ragged", flush=True)
+    _case(5, 2, 8, 2, 64, 64, [1000, 17], [200, 3])
+
+
+def test_medium_c4_like():
+    print("case: prefill 32/8 Sq=256, 64 + 4096 INT4 + 256 recent + causal", flush=True)
+    _case(6, 1, 32, 8, 256, 64, [4096], [256])
+
+
+def test_reference_api_fused_dequant_attn_forward():
+    print("case: fused_dequant_attn_forward drop-in", flush=True)
+    from heterokv import fused_dequant_attn_forward
+    g = torch.Generator().manual_seed(7)
+    H, S, Sq = 4, 333, 40
+    q = torch.randn((1, H, Sq, 128), generator=g).half()
+    K = torch.randn((1, H, S, 128), generator=g).half()
+    V = torch.randn((1, H, S, 128), generator=g).half()
+    kc, ks, kz = oc.compress(K.numpy(), 128)
+    vc, vs, vz = oc.compress(V.numpy(), 128)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    out = fused_dequant_attn_forward(q.to(DEV), t(kc), t(ks).reshape(1, H, S), t(kz).reshape(1, H, S).float(),
+                                     t(vc), t(vs).reshape(1, H, S), t(vz).reshape(1, H, S).float())
+    kd = oa.dequant_rows(kc[0], ks.reshape(H, S), kz.reshape(H, S))
+    vd = oa.dequant_rows(vc[0], vs.reshape(H, S), vz.reshape(H, S))
+    ref = oa.attend(q[0].double().numpy(), kd, vd)
+    err = np.abs(out[0].float().cpu().numpy() - ref).max()
+    print("  max abs err %.3e" % err, flush=True)
+    assert out.shape == (1, H, Sq, 128) and err <= TOL
