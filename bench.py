@@ -111,6 +111,71 @@ def cpu_baseline(q, K, V, budget_s=10.0):
                             % (n, el))
 
 
+P_SQ, P_SINK, P_MID, P_RECENT = 2048, 64, 131072, 4096
+# 4*Hq*D per (query, visible key): history fully visible, the chunk causally
+P_FLOPS = 4 * HQ * D * P_SQ * (P_SINK + P_MID + P_RECENT) + 4 * HQ * D * (P_SQ * (P_SQ + 1) // 2)
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(torch, ops, args):
+    """One step = one hkv_prefill_attn launch: 2048 fp16 queries (32 q / 8 kv heads) against
+    64 fp16 sink + 131072 INT4 + 4096 fp16 recent tokens plus the chunk itself (causal)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(4)
+    hist = P_SINK + P_MID + P_RECENT
+    K = torch.randn((1, HKV, hist, D), generator=g, device=dev)
+    K[..., OUTLIERS] *= 8
+    K = K.half()
+    V = torch.randn((1, HKV, hist, D), generator=g, device=dev).half()
+    CK = torch.randn((1, HKV, P_SQ, D), generator=g, device=dev).half()
+    CV = torch.randn((1, HKV, P_SQ, D), generator=g, device=dev).half()
+    q = (torch.randn((1, HQ, P_SQ, D), generator=g, device=dev) / math.sqrt(D)).half()
+    sink = ops.F16Zone(1, HKV, P_SINK, dev)
+    sink.write(K[:, :, :P_SINK], V[:, :, :P_SINK], [0])
+    rec = ops.F16Zone(1, HKV, P_RECENT, dev)
+    rec.write(K[:, :, P_SINK + P_MID:], V[:, :, P_SINK + P_MID:], [0])
+    nb = P_MID // 16
+    pool = ops.Int4Pool(nb, HKV, dev)
+    bt = torch.arange(nb, dtype=torch.int32, device=dev)[None]
+    ops.pack_tokens(pool, K[:, :, P_SINK:P_SINK + P_MID], V[:, :, P_SINK:P_SINK + P_MID],
+                    torch.zeros(1, dtype=torch.int32, device=dev), bt)
+    del K, V
+    out = torch.empty((1, HQ, P_SQ, D), dtype=torch.float16, device=dev)
+    zones = [(sink, None, P_SINK), (rec, None, P_RECENT)]
+
+    def launch():
+        ops.prefill_attention(q, zones=zones, pool=pool, block_table=bt, int4_max_len=P_MID,
+                              chunk_k=CK, chunk_v=CV, out=out)
+
+    for _ in range(max(args.warmup, 1)):
+        launch()
+    torch.cuda.synchronize()
+    pool.check_errors()
+    stream = torch.cuda.current_stream(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(args.steps):
+        launch()
+    ev1.record(stream)
+    ev1.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    tflops = P_FLOPS / (ms * 1e-3) / 1e12
+    line = {
+        "metric": "INT4-KV chunked-prefill attention TFLOP/s (MFMA roofline fraction)",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic (seeded N(0,1) K/V, x8 K outlier channels)",
+        "config": {"workload": "chunked prefill: 2048 fp16 queries, 32 q / 8 kv heads, head_dim 128, over "
+                               "64 fp16 sink + 131072 INT4 + 4096 fp16 recent + causal chunk",
+                   "flops_per_step": P_FLOPS},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +185,9 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
+                    help="decode: the headline single-layer decode (default); prefill: the chunked-prefill "
+                         "kernel on a 2048-token chunk over 64 + 131072 INT4 + 4096 tokens (MFMA bound)")
     ap.add_argument("--copy-calibration", type=float, default=0.0,
                     help="run only torch's device copy of this many MB (20 launches) so that rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
@@ -144,6 +212,9 @@ def main():
         return
 
     from heterokv import ops
+
+    if args.workload == "prefill":
+        return bench_prefill(torch, ops, args)
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
