@@ -68,6 +68,9 @@ struct DecodeParams {
     ZoneP z[HKV_MAX_F16_ZONES];
     const uint8_t* pool;
     int64_t pool_blocks;
+    const uint8_t* staging;   // records addressed by negative block ids
+    int64_t staging_blocks;
+    int fallback_id;          // id substituted for an out-of-range one (a valid record)
     const int32_t* bt;
     int bt_stride;
     const int32_t* int4_lens;
@@ -113,11 +116,13 @@ struct F16Tile {
     u4 v[4];      // V^T tile: halves [n][i] for tokens 4g+i, dims c+16n
 };
 
-// `phys` is the (already validated) physical block id; every load of a block is
-// issued back to back so several blocks stay in flight.
+// `phys` is the (already validated, wave-uniform) block id: >= 0 a pool record,
+// < 0 staging record ~phys.  Every load of a block is issued back to back so
+// several blocks stay in flight.
 __device__ __forceinline__ void load_int4(const DecodeParams& p, int h, int phys, int c, int g, Int4Blk& d) {
     const int H = p.Hkv;
-    const uint8_t* rec = p.pool + (int64_t)phys * ((int64_t)H * 2208);
+    const uint8_t* rec = phys >= 0 ? p.pool + (int64_t)phys * ((int64_t)H * 2208)
+                                   : p.staging + (int64_t)(~phys) * ((int64_t)H * 2208);
     d.k = *(const u4*)(rec + h * kHeadCodeBytes + c * kCodeRowBytes + g * 16);
     d.v = *(const u4*)(rec + (int64_t)H * 1024 + h * kHeadCodeBytes + (g * 16 + c) * 16);
     d.ks = *(const f4*)(rec + (int64_t)H * 2048 + h * 64 + g * 16);
@@ -127,12 +132,13 @@ __device__ __forceinline__ void load_int4(const DecodeParams& p, int h, int phys
 }
 
 // Block ids of logical blocks [lb0, lb0 + 64) of sequence b, one per lane, with
-// out-of-range ids replaced by 0 and reported once through p.err.
+// out-of-range ids replaced by a valid one and reported once through p.err.
 __device__ __forceinline__ int load_block_ids(const DecodeParams& p, int b, int lb0, int lb1, int lane) {
-    int id = 0;
+    int id = p.fallback_id;
     if (lb0 + lane < lb1) id = p.bt[(int64_t)b * p.bt_stride + lb0 + lane];
-    const bool bad = (lb0 + lane < lb1) && (id < 0 || (int64_t)id >= p.pool_blocks);
-    if (bad) id = 0;
+    const bool bad = (lb0 + lane < lb1) &&
+                     (id >= 0 ? (int64_t)id >= p.pool_blocks : (int64_t)(~id) >= p.staging_blocks);
+    if (bad) id = p.fallback_id;
     if (__ballot(bad) && lane == 0 && p.err) atomicOr(p.err, 1);
     return id;
 }
@@ -618,8 +624,12 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
                 HKV_ERR_ARG, "hkv_decode_attn: q must be 16-byte aligned with strides multiple of 8");
     HKV_REQUIRE(a->int4_max_len >= 0, HKV_ERR_ARG, "hkv_decode_attn: int4_max_len < 0");
     if (a->int4_max_len > 0) {
-        HKV_REQUIRE(a->pool && a->block_table && a->pool_blocks > 0, HKV_ERR_ARG,
-                    "hkv_decode_attn: INT4 zone without pool/block table");
+        HKV_REQUIRE(a->block_table && ((a->pool && a->pool_blocks > 0) || (a->staging && a->staging_blocks > 0)),
+                    HKV_ERR_ARG, "hkv_decode_attn: INT4 zone without pool/staging records or block table");
+        HKV_REQUIRE(a->pool_blocks >= 0 && a->staging_blocks >= 0 && a->staging_blocks <= (1ll << 31),
+                    HKV_ERR_ARG, "hkv_decode_attn: bad pool/staging block counts");
+        HKV_REQUIRE(a->staging_blocks == 0 || (((uintptr_t)a->staging) & 15) == 0, HKV_ERR_ARG,
+                    "hkv_decode_attn: staging must be 16-byte aligned");
         HKV_REQUIRE((int64_t)a->bt_stride * kBlockTokens >= a->int4_max_len, HKV_ERR_CAPACITY,
                     "hkv_decode_attn: block table stride %d too small for %d INT4 tokens", a->bt_stride,
                     a->int4_max_len);
@@ -664,7 +674,10 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
         p.z[i].lens = i < p.nz ? z.lens : nullptr;
     }
     p.pool = a->pool;
-    p.pool_blocks = a->pool_blocks;
+    p.pool_blocks = a->pool ? a->pool_blocks : 0;
+    p.staging = a->staging;
+    p.staging_blocks = a->staging ? a->staging_blocks : 0;
+    p.fallback_id = p.pool_blocks > 0 ? 0 : -1;
     p.bt = a->block_table;
     p.bt_stride = a->bt_stride;
     p.int4_lens = a->int4_lens;

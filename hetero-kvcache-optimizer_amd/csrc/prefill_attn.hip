@@ -51,6 +51,9 @@ struct PrefillParams {
     ZoneP z[HKV_MAX_F16_ZONES];
     const uint8_t* pool;
     int64_t pool_blocks;
+    const uint8_t* staging;      // records addressed by negative block ids
+    int64_t staging_blocks;
+    int fallback_id;             // id substituted for an out-of-range one (a valid record)
     const int32_t* bt;
     int bt_stride;
     const int32_t* int4_lens;
@@ -100,16 +103,17 @@ __device__ __forceinline__ void stage_load(const PrefillParams& p, const TileMap
         const int lb = lb0 + blk;
         const int nb = (tm.len4 + kBlockTokens - 1) / kBlockTokens;
         s.kind = 0;
-        int phys = 0;
+        int phys = p.fallback_id;
         if (lb < nb) {
             phys = p.bt[(int64_t)b * p.bt_stride + lb];
-            if (phys < 0 || (int64_t)phys >= p.pool_blocks) {
+            if (phys >= 0 ? (int64_t)phys >= p.pool_blocks : (int64_t)(~phys) >= p.staging_blocks) {
                 if (p.err) atomicOr(p.err, 1);
-                phys = 0;
+                phys = p.fallback_id;
             }
         }
         const int H = p.Hkv;
-        const uint8_t* rec = p.pool + (int64_t)phys * ((int64_t)H * 2208);
+        const uint8_t* rec = phys >= 0 ? p.pool + (int64_t)phys * ((int64_t)H * 2208)
+                                       : p.staging + (int64_t)(~phys) * ((int64_t)H * 2208);
         const int rr = (t >> 2) & 15, pt = t & 3;
         const int tok0 = lb * kBlockTokens;
         s.valid = (lb < nb) ? min(kBlockTokens, tm.len4 - tok0) : 0;
@@ -453,8 +457,12 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
     }
     HKV_REQUIRE(a->int4_max_len >= 0, HKV_ERR_ARG, "hkv_prefill_attn: int4_max_len < 0");
     if (a->int4_max_len > 0) {
-        HKV_REQUIRE(a->pool && a->block_table && a->pool_blocks > 0, HKV_ERR_ARG,
-                    "hkv_prefill_attn: INT4 zone without pool/block table");
+        HKV_REQUIRE(a->block_table && ((a->pool && a->pool_blocks > 0) || (a->staging && a->staging_blocks > 0)),
+                    HKV_ERR_ARG, "hkv_prefill_attn: INT4 zone without pool/staging records or block table");
+        HKV_REQUIRE(a->pool_blocks >= 0 && a->staging_blocks >= 0 && a->staging_blocks <= (1ll << 31),
+                    HKV_ERR_ARG, "hkv_prefill_attn: bad pool/staging block counts");
+        HKV_REQUIRE((((uintptr_t)a->pool | (uintptr_t)a->staging) & 15) == 0, HKV_ERR_ARG,
+                    "hkv_prefill_attn: pool/staging must be 16-byte aligned");
         HKV_REQUIRE((int64_t)a->bt_stride * kBlockTokens >= a->int4_max_len, HKV_ERR_CAPACITY,
                     "hkv_prefill_attn: block table stride too small");
     }
@@ -490,7 +498,10 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
         p.z[i].lens = on ? a->f16[i].lens : nullptr;
     }
     p.pool = a->pool;
-    p.pool_blocks = a->pool_blocks;
+    p.pool_blocks = a->pool ? a->pool_blocks : 0;
+    p.staging = a->staging;
+    p.staging_blocks = a->staging ? a->staging_blocks : 0;
+    p.fallback_id = p.pool_blocks > 0 ? 0 : -1;
     p.bt = a->block_table;
     p.bt_stride = a->bt_stride;
     p.int4_lens = a->int4_lens;

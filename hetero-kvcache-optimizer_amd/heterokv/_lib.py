@@ -13,7 +13,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libheterokv.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_U8 = 0, 1, 2, 3
 MAX_F16_ZONES = 3
 BLOCK_TOKENS = 16
@@ -74,7 +74,8 @@ class DecodeArgs(ctypes.Structure):
                 ("pool", vp), ("pool_blocks", i64), ("block_table", vp), ("bt_stride", i32),
                 ("int4_lens", vp), ("int4_max_len", i32),
                 ("out", vp), ("out_stride_b", i64), ("out_stride_h", i64),
-                ("workspace", vp), ("workspace_bytes", ctypes.c_size_t), ("splits_hint", i32)]
+                ("workspace", vp), ("workspace_bytes", ctypes.c_size_t), ("splits_hint", i32),
+                ("staging", vp), ("staging_blocks", i64)]
 
 
 class PrefillArgs(ctypes.Structure):
@@ -87,7 +88,16 @@ class PrefillArgs(ctypes.Structure):
                 ("chunk_k", vp), ("chunk_v", vp),
                 ("chunk_stride_b", i64), ("chunk_stride_h", i64), ("chunk_stride_t", i64),
                 ("out", vp), ("out_stride_b", i64), ("out_stride_h", i64), ("out_stride_t", i64),
-                ("err_flag", vp)]
+                ("err_flag", vp), ("staging", vp), ("staging_blocks", i64)]
+
+
+class CopyDesc(ctypes.Structure):
+    _fields_ = [("dst", vp), ("src", vp), ("bytes", ctypes.c_size_t)]
+
+
+class PfStats(ctypes.Structure):
+    _fields_ = [("bytes_h2d", ctypes.c_uint64), ("copies_h2d", ctypes.c_uint64),
+                ("bytes_d2h", ctypes.c_uint64), ("arena_bytes", ctypes.c_uint64)]
 
 
 # (name, restype, argtypes) of every symbol include/heterokv.h declares.
@@ -106,6 +116,19 @@ SYMBOLS = [
     ("hkv_decode_workspace_bytes", ctypes.c_size_t, [i32, i32, i32, i32, i32, vp, i32]),
     ("hkv_decode_attn", ctypes.c_int, [ctypes.POINTER(DecodeArgs), vp]),
     ("hkv_prefill_attn", ctypes.c_int, [ctypes.POINTER(PrefillArgs), vp]),
+    ("hkv_pf_create", ctypes.c_int, [i32, ctypes.c_size_t, i32, ctypes.POINTER(vp)]),
+    ("hkv_pf_destroy", ctypes.c_int, [vp]),
+    ("hkv_pf_host_ptr", vp, [vp, ctypes.c_size_t]),
+    ("hkv_pf_stream", vp, [vp]),
+    ("hkv_pf_stage_out", ctypes.c_int, [vp, vp, ctypes.c_size_t, ctypes.c_size_t, vp]),
+    ("hkv_pf_submit", ctypes.c_int, [vp, ctypes.POINTER(CopyDesc), i32, i32, i32]),
+    ("hkv_pf_record", ctypes.c_int, [vp, i32]),
+    ("hkv_pf_wait", ctypes.c_int, [vp, i32, vp]),
+    ("hkv_pf_mark", ctypes.c_int, [vp, i32, vp]),
+    ("hkv_pf_stall_ms", ctypes.c_int, [vp, i32, ctypes.POINTER(ctypes.c_float)]),
+    ("hkv_pf_stats", ctypes.c_int, [vp, ctypes.POINTER(PfStats)]),
+    ("hkv_pf_synchronize", ctypes.c_int, [vp]),
+    ("hkv_gather_blocks", ctypes.c_int, [vp, i64, vp, i64, vp, i64, i64, vp, vp, vp]),
 ]
 
 _lock = threading.Lock()

@@ -158,6 +158,27 @@ class FusedHeteroCache(DynamicCache):
             return {}
         return self._manager._dram_table
 
+    def offload_to_host(self, fraction: float, seed: int = 0) -> int:
+        """Move a seeded `fraction` of every layer's INT4 block records to pinned host memory;
+        decode then prefetches each layer's records one layer ahead (HeteroKVManager.offload_to_host)."""
+        if self._manager is None:
+            return 0
+        return self._manager.offload_to_host(fraction, seed)
+
+    @property
+    def retrieval_window(self):
+        """None: attend every INT4 chunk (Path C); int or "adaptive": top-w chunks (Path A)."""
+        return None if self._manager is None else self._manager.retrieval_window
+
+    @retrieval_window.setter
+    def retrieval_window(self, w):
+        self._ensure_manager(0).retrieval_window = w
+
+    def prefetch_stats(self, reset: bool = True) -> Dict[str, Any]:
+        if self._manager is None:
+            return {"stall_ms": 0.0, "per_layer": []}
+        return self._manager.prefetch_stats(reset)
+
     def schedule_prefetch(self, chunk_key: str) -> None:
         """The INT4 tier of this build is resident in HBM (or streamed by the block prefetcher),
         so there is nothing to stage per chunk."""

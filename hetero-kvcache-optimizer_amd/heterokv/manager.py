@@ -26,11 +26,13 @@ fp16 (bf16 inputs are stored as fp16 and returned in the caller's dtype).
 from collections import OrderedDict, deque
 from typing import Any, Dict, List, Optional, Tuple
 
+import numpy as np
 import torch
 
 from . import ops
 from ._lib import BLOCK_TOKENS, HEAD_DIM, HeteroKVError
 from .kv_compressor import KVCompressor
+from .prefetcher import AdaptivePrefetchController, Prefetcher
 
 
 def _as16(t):
@@ -54,26 +56,49 @@ class _LayerState:
         self.hh_pos: List[int] = []
         self.hh_started = False
         self.pool: Optional[ops.Int4Pool] = None
-        self.cap_blocks = 0
-        self.bt: Optional[torch.Tensor] = None
+        self.pool_used = 0                         # pool records in use
+        self.bt: Optional[torch.Tensor] = None     # device int32 [B, cap]: logical block -> record id
+        self.bt_host: Optional[np.ndarray] = None  # host mirror of bt
+        self.nb = 0                                # logical blocks allocated per sequence
         self.int4_len = 0
         self.int4_pos: List[int] = []
         self.prefilled = False
         self.seq_offset = 0
+        # host tier: records ~0 .. ~(n_host-1) live in the pinned arena at host_off, in
+        # (logical block, sequence) order; host_lbs[k] is the logical block of record k
+        self.n_host = 0
+        self.host_off = 0
+        self.host_lbs: Optional[np.ndarray] = None
+        self.version = 0                           # bumped whenever bt or pool change
+        self.resident_cache = None
 
     # -------------------------------------------------------------- INT4 pool
     def ensure_int4(self, n_tokens):
+        """Allocate pool records for logical blocks up to n_tokens (new records are
+        appended; earlier ones, resident or host, keep their ids)."""
         need = (n_tokens + BLOCK_TOKENS - 1) // BLOCK_TOKENS
-        if need <= self.cap_blocks:
+        if need <= self.nb:
             return
-        cap = max(need, 2 * self.cap_blocks, 64)
-        pool = ops.Int4Pool(self.B * cap, self.H, self.device)
-        if self.pool is not None and self.cap_blocks:
-            rb = pool.record_bytes
-            pool.data.view(self.B, cap, rb)[:, :self.cap_blocks] = self.pool.data.view(self.B, self.cap_blocks, rb)
-        self.pool, self.cap_blocks = pool, cap
-        base = torch.arange(self.B, dtype=torch.int32, device=self.device)[:, None] * cap
-        self.bt = (base + torch.arange(cap, dtype=torch.int32, device=self.device)[None]).contiguous()
+        B = self.B
+        cap = self.bt_host.shape[1] if self.bt_host is not None else 0
+        if need > cap:
+            bh = np.zeros((B, max(need, 2 * cap, 64)), dtype=np.int32)
+            if cap:
+                bh[:, :cap] = self.bt_host
+            self.bt_host = bh
+        add = need - self.nb
+        used = self.pool_used + B * add
+        pcap = self.pool.num_blocks if self.pool is not None else 0
+        if used > pcap:
+            pool = ops.Int4Pool(max(used, 2 * pcap, 64 * B), self.H, self.device)
+            if self.pool is not None and self.pool_used:
+                pool.data[:self.pool_used].copy_(self.pool.data[:self.pool_used])
+            self.pool = pool
+        self.bt_host[:, self.nb:need] = (self.pool_used + np.arange(B, dtype=np.int32)[:, None] * add +
+                                         np.arange(add, dtype=np.int32)[None, :])
+        self.pool_used, self.nb = used, need
+        self.bt = torch.from_numpy(self.bt_host).to(self.device)
+        self.version += 1
 
     # -------------------------------------------------------------- tail ring
     def tail_tensors(self):
@@ -126,6 +151,21 @@ class HeteroKVManager:
         self._eviction_counter = 0
         self._queued_tokens = 0      # tokens the reference would leave in its competition queue
         self._workspace = None
+        # host tier (offload_to_host) and its prefetch schedule
+        self._pf: Optional[Prefetcher] = None
+        self._staging: List[ops.Int4Pool] = []
+        self._buf_owner: List[int] = []
+        self._next_buf = 0
+        self._pending: Dict[int, Tuple[int, Any]] = {}   # layer -> (staging buffer, selection)
+        self._waited: List[int] = []
+        self._selection_of: Dict[int, Any] = {}
+        self._window_tables: Dict[Any, Tuple[torch.Tensor, int]] = {}
+        # retrieval of the INT4 middle at decode: None = every chunk (decompress_dram_chunks,
+        # manager.py:779-821); an int or "adaptive" = the top-w chunks by score
+        # (get_dram_chunks_quantized_adaptive, manager.py:931-1056)
+        self.retrieval_window: Any = None
+        self._adaptive_controller = AdaptivePrefetchController()
+        self._last_attention_weights: Optional[torch.Tensor] = None
 
     # ---------------------------------------------------------------- helpers
     @property
@@ -354,11 +394,12 @@ class HeteroKVManager:
         k_data/v_data uint8 [B,H,T,128], *_scales float32 [B*H*T], *_zps uint8 [B*H*T]."""
         layer, start, n = self._chunks[key]
         st = self._layers[layer]
+        pool, bt = self._resident_view(st)
         out = {}
         for which, name in ((0, "k"), (1, "v")):
             cs, ss, zs = [], [], []
             for b in range(st.B):
-                c, s, z = ops.unpack_tokens(st.pool, st.bt[b], start + n, which)
+                c, s, z = ops.unpack_tokens(pool, bt[b], start + n, which)
                 cs.append(c[:, start:start + n])
                 ss.append(s.view(st.H, -1)[:, start:start + n].reshape(-1))
                 zs.append(z.view(st.H, -1)[:, start:start + n].reshape(-1))
@@ -373,11 +414,12 @@ class HeteroKVManager:
         st = self._layers[layer_idx] if layer_idx < len(self._layers) else None
         if st is None or st.int4_len == 0:
             return None, None, 0
+        pool, bt = self._resident_view(st)
         outs = []
         for which in (0, 1):
             per_b = []
             for b in range(st.B):
-                c, s, z = ops.unpack_tokens(st.pool, st.bt[b], st.int4_len, which)
+                c, s, z = ops.unpack_tokens(pool, bt[b], st.int4_len, which)
                 per_b.append(self._compressor.decompress(c, s, z, target_dtype=torch.float16))
             outs.append(torch.stack(per_b))
         return outs[0], outs[1], st.int4_len
@@ -398,11 +440,204 @@ class HeteroKVManager:
         return {name: torch.cat([p[name] for p in parts], dim=2 if name.endswith("_data") else 0)
                 for name in parts[0]}
 
+    # ---------------------------------------------------------------- host tier
+    def offload_to_host(self, fraction: float, seed: int = 0, layers: Optional[List[int]] = None) -> int:
+        """Move a seeded random `fraction` of each layer's INT4 block records to a pinned host
+        arena (the reference's DRAM tier, dram_storage.py:106-138, as one contiguous run per
+        layer).  Only full blocks move, so later appends always land in HBM.  The records
+        chosen for layer l are those of numpy.random.default_rng([seed, l]).choice over the
+        layer's full blocks.  Returns the number of records moved.  One call per manager."""
+        if self._pf is not None:
+            raise HeteroKVError(-1, "offload_to_host: the host tier is already set up")
+        if not 0.0 <= fraction <= 1.0:
+            raise ValueError("fraction must be in [0, 1]")
+        if layers is None:
+            layers = [i for i, st in enumerate(self._layers) if st is not None]
+        plan = []
+        for li in layers:
+            st = self._layers[li]
+            if st is None or st.int4_len == 0:
+                continue
+            full = st.int4_len // BLOCK_TOKENS
+            total = st.B * st.nb
+            n_host = min(int(round(fraction * total)), st.B * full)
+            if n_host == 0:
+                continue
+            rng = np.random.default_rng([seed, li])
+            chosen = np.sort(rng.choice(st.B * full, size=n_host, replace=False))   # c = lb * B + b
+            plan.append((li, st, chosen))
+        if not plan:
+            return 0
+        rb = ops.record_bytes(plan[0][1].H)
+        arena = sum(len(c) * ops.record_bytes(st.H) for _, st, c in plan)
+        self._pf = Prefetcher(self.device, arena, num_slots=max(len(self._layers), 1))
+        off = 0
+        moved = 0
+        for li, st, chosen in plan:
+            rb = ops.record_bytes(st.H)
+            lb, b = chosen // st.B, chosen % st.B
+            is_host = np.zeros((st.B, st.nb), dtype=bool)
+            is_host[b, lb] = True
+            tmp = ops.Int4Pool(len(chosen), st.H, self.device)
+            ops.gather_blocks(st.pool, st.bt_host[b, lb], tmp)
+            self._pf.stage_out(tmp.data[:len(chosen)], off)
+            rb_idx, rl_idx = np.nonzero(~is_host)                                  # resident, row-major
+            res_ids = st.bt_host[rb_idx, rl_idx]
+            pool = ops.Int4Pool(max(len(res_ids), st.B * 64), st.H, self.device)
+            ops.gather_blocks(st.pool, res_ids, pool)
+            bh = st.bt_host.copy()
+            bh[rb_idx, rl_idx] = np.arange(len(res_ids), dtype=np.int32)
+            bh[b, lb] = ~np.arange(len(chosen), dtype=np.int32)
+            torch.cuda.current_stream(self.device).synchronize()
+            for pl in (tmp, pool):
+                pl.check_errors()
+            st.pool, st.pool_used, st.bt_host = pool, len(res_ids), bh
+            st.bt = torch.from_numpy(bh).to(self.device)
+            st.n_host, st.host_off, st.host_lbs = len(chosen), off, lb.astype(np.int64)
+            st.version += 1
+            st.resident_cache = None
+            off += len(chosen) * rb
+            moved += len(chosen)
+        biggest = max(st.n_host for _, st, _ in plan)
+        self._staging = [ops.Int4Pool(biggest, plan[0][1].H, self.device) for _ in range(2)]
+        self._buf_owner = [-1, -1]
+        return moved
+
+    def host_blocks(self, layer_idx: int) -> int:
+        st = self._layers[layer_idx] if layer_idx < len(self._layers) else None
+        return 0 if st is None else st.n_host
+
+    def _resident_view(self, st: _LayerState):
+        """(pool, block table) holding every INT4 record of the layer in HBM: the layer's
+        own when nothing is on the host, else a gathered copy (for inspection paths)."""
+        if st.n_host == 0:
+            return st.pool, st.bt
+        if st.resident_cache is not None and st.resident_cache[0] == st.version:
+            return st.resident_cache[1], st.resident_cache[2]
+        rb = ops.record_bytes(st.H)
+        stage = ops.Int4Pool(st.n_host, st.H, self.device)
+        stage.data.view(-1)[:st.n_host * rb].copy_(self._pf.host_tensor(st.host_off, st.n_host * rb))
+        full = ops.Int4Pool(st.B * st.nb, st.H, self.device)
+        ops.gather_blocks(st.pool, st.bt_host[:, :st.nb].reshape(-1), full, staging=stage)
+        full.check_errors()
+        bt = torch.arange(st.B * st.nb, dtype=torch.int32, device=self.device).view(st.B, st.nb)
+        st.resident_cache = (st.version, full, bt)
+        return full, bt
+
+    def _layer_chunks(self, layer_idx: int) -> List[str]:
+        pre = "l%d_" % layer_idx
+        return [k for k in self._chunks if k.startswith(pre)]
+
+    def _selection(self, layer_idx: int):
+        """Chunk keys attended at this decode step (None = all), computed once per layer
+        and step: the window size comes from retrieval_window or, for "adaptive", from the
+        controller (called once per layer, as manager.py:965-968 does)."""
+        if layer_idx in self._selection_of:
+            return self._selection_of[layer_idx]
+        sel = None
+        if self.retrieval_window is not None:
+            keys = self._layer_chunks(layer_idx)
+            if keys:
+                if self.retrieval_window == "adaptive":
+                    w = int(self._adaptive_controller.compute_window(
+                        attention_weights=self._last_attention_weights, cache_miss=False))
+                else:
+                    w = int(self.retrieval_window)
+                w = max(1, min(w, len(keys)))
+                ranked = sorted(keys, key=lambda k: self._chunk_attention_scores.get(k, 0.0), reverse=True)
+                chosen = set(ranked[:w])
+                sel = tuple(k for k in self._chunk_eviction_order if k in chosen)
+        self._selection_of[layer_idx] = sel
+        return sel
+
+    def _window_table(self, layer_idx: int, st: _LayerState, sel):
+        """Block table over the selected chunks' blocks, in eviction order, and their token
+        count.  Chunks must start on a block boundary and, except the layer's last, end on one."""
+        key = (layer_idx, sel, st.version)
+        hit = self._window_tables.get(key)
+        if hit is not None:
+            return hit
+        lbs, n4 = [], 0
+        for k in sel:
+            _, start, n = self._chunks[k]
+            if start % BLOCK_TOKENS or (n % BLOCK_TOKENS and start + n != st.int4_len):
+                raise HeteroKVError(-4, "windowed retrieval needs 16-token aligned chunks (%s: %d+%d)" %
+                                    (k, start, n))
+            if lbs and n4 % BLOCK_TOKENS:
+                raise HeteroKVError(-4, "windowed retrieval: only the last selected chunk may be partial")
+            lbs.extend(range(start // BLOCK_TOKENS, (start + n + BLOCK_TOKENS - 1) // BLOCK_TOKENS))
+            n4 += n
+        bt = torch.from_numpy(np.ascontiguousarray(st.bt_host[:, lbs])).to(self.device)
+        self._window_tables = {k2: v for k2, v in self._window_tables.items() if k2[0] != layer_idx}
+        self._window_tables[key] = (bt, n4)
+        return bt, n4
+
+    def _host_runs(self, st: _LayerState, sel) -> List[Tuple[int, int]]:
+        """Ranges [k0, k1) of the layer's host records needed for selection `sel`."""
+        if sel is None:
+            return [(0, st.n_host)]
+        runs = []
+        for k in sel:
+            _, start, n = self._chunks[k]
+            lb0, lb1 = start // BLOCK_TOKENS, (start + n + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+            k0 = int(np.searchsorted(st.host_lbs, lb0, "left"))
+            k1 = int(np.searchsorted(st.host_lbs, lb1, "left"))
+            if k1 > k0:
+                if runs and runs[-1][1] == k0:
+                    runs[-1] = (runs[-1][0], k1)
+                else:
+                    runs.append((k0, k1))
+        return runs
+
+    def _submit(self, layer_idx: int, sel) -> int:
+        st = self._layers[layer_idx]
+        buf = self._next_buf
+        self._next_buf = (buf + 1) % len(self._staging)
+        prev = self._buf_owner[buf]
+        if prev >= 0 and self._pending.get(prev, (None,))[0] == buf:
+            del self._pending[prev]        # its copy is overwritten before use: fetch again later
+        rb = ops.record_bytes(st.H)
+        dst = self._staging[buf].data
+        copies = [(dst[k0].data_ptr(), self._pf.host_ptr(st.host_off + k0 * rb), (k1 - k0) * rb)
+                  for k0, k1 in self._host_runs(st, sel)]
+        self._pf.submit(copies, slot=layer_idx, after_slot=prev)
+        self._buf_owner[buf] = layer_idx
+        self._pending[layer_idx] = (buf, sel)
+        return buf
+
+    def _prefetch_after(self, layer_idx: int) -> None:
+        """Submit the copies of the next layer (cyclically) that holds host records."""
+        L = len(self._layers)
+        for d in range(1, L):
+            j = (layer_idx + d) % L
+            st = self._layers[j]
+            if st is None or st.n_host == 0:
+                continue
+            sel = self._selection(j)
+            p = self._pending.get(j)
+            if p is None or p[1] != sel:
+                self._submit(j, sel)
+            return
+
+    def prefetch_stats(self, reset: bool = True) -> Dict[str, Any]:
+        """Stall of every layer that waited for host records since the last call: per layer
+        max(0, t(copies done) - t(kernel needs them)) in ms (synchronizes on those events)."""
+        per = [(li, self._pf.stall_ms(li)) for li in self._waited] if self._pf is not None else []
+        if reset:
+            self._waited = []
+        out = {"stall_ms": sum(ms for _, ms in per), "per_layer": per}
+        if self._pf is not None:
+            out.update(self._pf.stats())
+        return out
+
     # ---------------------------------------------------------------- fused decode
     def attend_decode(self, layer_idx: int, query_states: torch.Tensor, sm_scale: Optional[float] = None,
                       include_dram: bool = True) -> torch.Tensor:
         """softmax(q K^T * sm_scale) V over [INT4 middle (if include_dram) | sink | tail |
-        heavy hitters] of the layer, in one split-K launch (hkv_decode_attn).
+        heavy hitters] of the layer, in one split-K launch (hkv_decode_attn).  With a host
+        tier, the layer's host records are copied into a staging buffer on the prefetcher's
+        side stream (normally already submitted while the previous layer ran) and the next
+        host-tier layer's copies are submitted before this layer's kernel.
         query_states: [B, Hq, 1, 128]; returns [B, Hq, 1, 128] in the query's dtype."""
         st = self._layers[layer_idx]
         if st is None:
@@ -417,22 +652,45 @@ class HeteroKVManager:
         if st.hh_len:
             zones.append((st.hh, None, st.hh_len))
         n4 = st.int4_len if include_dram else 0
+        bt = st.bt
+        sel = None
+        if n4:
+            sel = self._selection(layer_idx)
+            if sel is not None:
+                bt, n4 = self._window_table(layer_idx, st, sel)
+        staged = n4 > 0 and st.n_host > 0 and bool(self._host_runs(st, sel))
+        buf = None
+        if staged:
+            p = self._pending.get(layer_idx)
+            buf = p[0] if (p is not None and p[1] == sel) else self._submit(layer_idx, sel)
+        if self._pf is not None and self.enable_prefetch:
+            self._prefetch_after(layer_idx)
+        if staged:
+            self._pf.wait(layer_idx)
         q16 = _as16(query_states)
         out = ops.decode_attention(q16, zones=zones, pool=st.pool if n4 else None,
-                                   block_table=st.bt if n4 else None, int4_max_len=n4,
-                                   sm_scale=sm_scale, workspace=self._workspace)
+                                   block_table=bt if n4 else None, int4_max_len=n4,
+                                   sm_scale=sm_scale, workspace=self._workspace,
+                                   staging=self._staging[buf] if staged else None)
+        if staged:
+            self._pf.mark(layer_idx)
+            self._pending.pop(layer_idx, None)
+            self._waited.append(layer_idx)
+        self._selection_of.pop(layer_idx, None)
         return out.to(query_states.dtype)
 
     # ---------------------------------------------------------------- summaries
     def memory_summary(self) -> Dict[str, Any]:
-        """manager.py:387-401.  dram_bytes counts this build's packed INT4 storage."""
+        """manager.py:387-401.  dram_bytes counts this build's packed INT4 storage (HBM and
+        host records alike); host_bytes the part in the pinned host arena."""
         hbm = sum((st.sink_len + st.tail_len + st.hh_len) for st in self._layers if st is not None)
         dram_bytes = 0
         for st in self._layers:
             if st is not None:
                 dram_bytes += st.B * st.H * st.int4_len * 2 * (HEAD_DIM // 2 + 5)
+        host = sum(st.n_host * ops.record_bytes(st.H) for st in self._layers if st is not None)
         return {"hbm_tokens": hbm, "dram_entries": len(self._chunks), "dram_bytes": dram_bytes,
-                "max_hbm_tokens": self.max_hbm_tokens()}
+                "host_bytes": host, "max_hbm_tokens": self.max_hbm_tokens()}
 
     def max_hbm_tokens(self) -> int:
         return self.sink_tokens + self.hbm_budget_tokens + self._heavyhitter_budget

@@ -270,13 +270,19 @@ class DecodeWorkspace:
         return v
 
 
+def _int4_source(pool, staging):
+    src = pool if pool is not None else staging
+    return src.num_kv_heads if src is not None else None
+
+
 def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
-                     sm_scale=None, workspace=None, out=None, splits=0):
+                     sm_scale=None, workspace=None, out=None, splits=0, staging=None):
     """Split-K decode attention over fp16 zones and the INT4 pool.
 
     q: [B, Hq, 128] or [B, Hq, 1, 128] fp16.
     zones: sequence of (F16Zone, lens int32 [B] or None, max_len).
     pool / block_table [B, nblk] / int4_lens [B] / int4_max_len: the INT4 zone.
+    staging: Int4Pool whose record i a block-table entry ~i (negative) names.
     splits: ranges per (sequence, kv head); 0 lets the library choose (about one
     workgroup per CU).
     Returns fp16 [B, Hq, 128] (or [B, Hq, 1, 128] if q was 4-D).
@@ -291,7 +297,7 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
     B, Hq, _ = q3.shape
     if len(zones) > _lib.MAX_F16_ZONES:
         raise HeteroKVError(-1, "decode_attention: at most %d fp16 zones" % _lib.MAX_F16_ZONES)
-    Hkv = pool.num_kv_heads if pool is not None else (zones[0][0].num_kv_heads if zones else None)
+    Hkv = _int4_source(pool, staging) or (zones[0][0].num_kv_heads if zones else None)
     if Hkv is None:
         raise HeteroKVError(-1, "decode_attention: no key/value zone given")
     if sm_scale is None:
@@ -317,13 +323,16 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
                                 lens=lt.data_ptr() if lt is not None else 0)
         zl.append(int(max_len))
     if int4_max_len > 0:
-        if pool is None or block_table is None:
+        if (pool is None and staging is None) or block_table is None:
             raise HeteroKVError(-1, "decode_attention: INT4 zone needs a pool and a block table")
         bt = _i32(block_table, dev)
         if bt.dim() == 1:
             bt = bt.unsqueeze(0)
         keep.append(bt)
-        a.pool, a.pool_blocks = pool.data.data_ptr(), pool.num_blocks
+        if pool is not None:
+            a.pool, a.pool_blocks = pool.data.data_ptr(), pool.num_blocks
+        if staging is not None:
+            a.staging, a.staging_blocks = staging.data.data_ptr(), staging.num_blocks
         a.block_table, a.bt_stride = bt.data_ptr(), bt.shape[1]
         if int4_lens is not None:
             il = _i32(int4_lens, dev)
@@ -341,9 +350,36 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
     return out.unsqueeze(2) if squeeze else out
 
 
+# ----------------------------------------------------------------------- record gather
+def gather_blocks(src, ids, dst, staging=None, dst_offset=0):
+    """dst record dst_offset + i = record ids[i] of src (ids >= 0) or of staging (~ids[i]).
+
+    src / staging / dst: Int4Pool with the same record size.  ids: int32 (device or host)."""
+    _require_gpu(dst.data)
+    dev = dst.device
+    ids = _i32(ids, dev).reshape(-1)
+    n = ids.numel()
+    if n == 0:
+        return dst
+    rb = dst.record_bytes
+    for other in (src, staging):
+        if other is not None and other.record_bytes != rb:
+            raise HeteroKVError(-1, "gather_blocks: record sizes differ")
+    if dst_offset < 0 or dst_offset + n > dst.num_blocks:
+        raise HeteroKVError(-3, "gather_blocks: %d records at %d exceed the %d-record destination" %
+                            (n, dst_offset, dst.num_blocks))
+    check(load().hkv_gather_blocks(src.data.data_ptr() if src is not None else None,
+                                   src.num_blocks if src is not None else 0,
+                                   staging.data.data_ptr() if staging is not None else None,
+                                   staging.num_blocks if staging is not None else 0,
+                                   ids.data_ptr(), n, rb, dst.data[dst_offset].data_ptr(), dst.err.data_ptr(),
+                                   stream_ptr(dev)), "hkv_gather_blocks")
+    return dst
+
+
 # ----------------------------------------------------------------------- prefill attention
 def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
-                      chunk_k=None, chunk_v=None, sm_scale=None, out=None):
+                      chunk_k=None, chunk_v=None, sm_scale=None, out=None, staging=None):
     """Chunked-prefill attention (hkv_prefill_attn).
 
     q: [B, Hq, Sq, 128] fp16.  Every query attends to all fp16-zone tokens and all INT4
@@ -356,8 +392,8 @@ def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, 
     if q.stride(-1) != 1 or q.data_ptr() % 16 or any(st % 8 for st in q.stride()[:3]):
         q = q.contiguous()
     B, Hq, Sq, _ = q.shape
-    Hkv = pool.num_kv_heads if pool is not None else (zones[0][0].num_kv_heads if zones else
-                                                       (chunk_k.shape[1] if chunk_k is not None else None))
+    Hkv = _int4_source(pool, staging) or (zones[0][0].num_kv_heads if zones else
+                                          (chunk_k.shape[1] if chunk_k is not None else None))
     if Hkv is None:
         raise HeteroKVError(-1, "prefill_attention: no key/value source given")
     if sm_scale is None:
@@ -384,9 +420,14 @@ def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, 
         if bt.dim() == 1:
             bt = bt.unsqueeze(0)
         keep.append(bt)
-        a.pool, a.pool_blocks = pool.data.data_ptr(), pool.num_blocks
+        if pool is None and staging is None:
+            raise HeteroKVError(-1, "prefill_attention: INT4 zone needs a pool and a block table")
+        if pool is not None:
+            a.pool, a.pool_blocks = pool.data.data_ptr(), pool.num_blocks
+        if staging is not None:
+            a.staging, a.staging_blocks = staging.data.data_ptr(), staging.num_blocks
         a.block_table, a.bt_stride = bt.data_ptr(), bt.shape[1]
-        err = pool.err
+        err = (pool if pool is not None else staging).err
         if int4_lens is not None:
             il = _i32(int4_lens, dev)
             keep.append(il)

@@ -16,6 +16,8 @@
  *   HeteroKVManager zone storage   src/memory/manager.py:416-674 (sink / tail / heavy-hitter)
  *   _evict_to_dram + DRAM chunks   src/memory/manager.py:1231-1299, src/memory/dram_storage.py:106-138
  *   decompress_dram_chunks (Path C gather order)   src/memory/manager.py:779-821
+ *   DRAMStorageManager (host tier)                 src/memory/dram_storage.py:20-222
+ *   AsyncPrefetcher (side-stream H2D)              src/policy/prefetcher.py:21-123
  *
  * INT4 block pool.  Tokens of the quantized middle zone live in 16-token
  * blocks.  One block record holds every kv head of those 16 tokens:
@@ -41,6 +43,11 @@
  *   V: word (g*16+c)*4+m of a head's 1024 B holds, for tokens 4g..4g+3,
  *      x0..x3 = dim c+32m and x4..x7 = dim c+32m+16   (g<4, c<16, m<4).
  *
+ * Host tier.  A block-table entry id >= 0 names record `id` of `pool`; an entry
+ * id < 0 names record ~id (= -id-1) of `staging`, an HBM buffer that the
+ * prefetcher below fills from pinned host memory before the kernel runs.  The
+ * append kernels (hkv_pack_tokens, hkv_repack_codes) only write pool records.
+ *
  * fp16 zones (sink, recent window, heavy hitters).  K is row-major
  * [B][H][cap][128]; V is stored in 16-token transposed tiles
  * [B][H][cap/16][4 g][16 c][8 n][4 i] fp16 holding V[token 4g+i][dim c+16n].
@@ -56,7 +63,7 @@
 extern "C" {
 #endif
 
-#define HKV_ABI_VERSION 1
+#define HKV_ABI_VERSION 2
 
 /* dtype codes */
 #define HKV_DTYPE_F16  0
@@ -233,6 +240,8 @@ typedef struct HkvDecodeArgs {
     void* workspace;               /* hkv_decode_workspace_bytes(); zero-filled once before first use */
     size_t workspace_bytes;
     int32_t splits_hint;           /* 0 = auto */
+    const uint8_t* staging;        /* records addressed by negative block ids (may be NULL) */
+    int64_t staging_blocks;
 } HkvDecodeArgs;
 
 size_t hkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
@@ -268,9 +277,75 @@ typedef struct HkvPrefillArgs {
     uint16_t* out;                 /* [batch][num_q_heads][num_queries][128] with strides */
     int64_t out_stride_b, out_stride_h, out_stride_t;
     int32_t* err_flag;             /* optional: bit 0 set if a block id was out of range */
+    const uint8_t* staging;        /* records addressed by negative block ids (may be NULL) */
+    int64_t staging_blocks;
 } HkvPrefillArgs;
 
 int hkv_prefill_attn(const HkvPrefillArgs* args, void* stream);
+
+/*
+ * Host-tier prefetcher (replaces DRAMStorageManager's per-tensor pinned dict,
+ * dram_storage.py:106-194, and AsyncPrefetcher's side stream, prefetcher.py:33-111).
+ * A handle owns a pinned host arena (hipHostMalloc), a side stream created at
+ * the default priority, and `num_slots` event sets ("ready", "need", "free").  A
+ * slot names one prefetch (typically one per layer); the HBM staging buffers it
+ * fills are the caller's.  With two staging buffers reused across layers:
+ *   hkv_pf_submit(slot l+1, after slot l-1)  while layer l computes: the copies
+ *                                            wait for layer l-1's "free" mark
+ *   hkv_pf_wait(slot l+1, compute stream)    before layer l+1's kernel
+ *   hkv_pf_mark(slot l+1, compute stream)    after layer l+1's kernel
+ * No call blocks the host except hkv_pf_stall_ms and hkv_pf_synchronize.  One
+ * handle is used by one host thread.
+ */
+typedef struct HkvPrefetcher HkvPrefetcher;
+
+typedef struct HkvCopyDesc {
+    void* dst;                     /* device destination */
+    const void* src;               /* host source (pinned arena memory for an async copy) */
+    size_t bytes;
+} HkvCopyDesc;
+
+typedef struct HkvPfStats {
+    uint64_t bytes_h2d;            /* bytes submitted host -> device */
+    uint64_t copies_h2d;           /* copy descriptors submitted */
+    uint64_t bytes_d2h;            /* bytes staged out device -> host */
+    uint64_t arena_bytes;
+} HkvPfStats;
+
+/* arena_bytes may be 0 (no arena); num_slots in [1, 256]. */
+int hkv_pf_create(int32_t device, size_t arena_bytes, int32_t num_slots, HkvPrefetcher** out);
+int hkv_pf_destroy(HkvPrefetcher* pf);
+/* Host address of arena byte `offset` (NULL if outside the arena). */
+void* hkv_pf_host_ptr(HkvPrefetcher* pf, size_t offset);
+/* The side stream (hipStream_t as void*), for work the caller adds after a submit. */
+void* hkv_pf_stream(HkvPrefetcher* pf);
+/* Device -> arena copy of `bytes` at arena offset `host_offset`, on `stream`. */
+int hkv_pf_stage_out(HkvPrefetcher* pf, const void* src_device, size_t host_offset, size_t bytes,
+                     void* stream);
+/* Side stream: wait for slot after_slot's last "free" mark (after_slot < 0: no wait),
+ * copy the descriptors, record `slot`'s "ready". */
+int hkv_pf_submit(HkvPrefetcher* pf, const HkvCopyDesc* descs, int32_t n, int32_t slot,
+                  int32_t after_slot);
+/* Side stream: record the slot's "ready" event again (after caller work on hkv_pf_stream). */
+int hkv_pf_record(HkvPrefetcher* pf, int32_t slot);
+/* Compute stream: record "need" and wait for the slot's "ready". */
+int hkv_pf_wait(HkvPrefetcher* pf, int32_t slot, void* compute_stream);
+/* Compute stream: record the slot's "free" mark after the kernels that read it. */
+int hkv_pf_mark(HkvPrefetcher* pf, int32_t slot, void* compute_stream);
+/* Blocks until the slot's events complete; *ms = max(0, ready - need) of its last wait
+ * (the time the compute stream sat waiting for the copies); 0 if either is missing. */
+int hkv_pf_stall_ms(HkvPrefetcher* pf, int32_t slot, float* ms);
+int hkv_pf_stats(HkvPrefetcher* pf, HkvPfStats* out);
+int hkv_pf_synchronize(HkvPrefetcher* pf);
+
+/*
+ * Block gather (index kernel): dst record i = src record ids[i] for i < n, where
+ * an id < 0 names record ~id of `src_staging`.  Used to compact a pool and to
+ * collect the records that leave for the host tier into one contiguous run.
+ */
+int hkv_gather_blocks(const uint8_t* src_pool, int64_t src_blocks, const uint8_t* src_staging,
+                      int64_t staging_blocks, const int32_t* ids, int64_t n, int64_t record_bytes,
+                      uint8_t* dst, int32_t* err_flag, void* stream);
 
 #ifdef __cplusplus
 }

@@ -32,7 +32,7 @@ def test_header_symbols_exported(lib):
 
 
 def test_version_and_record_size(lib):
-    assert lib.hkv_abi_version() == 1
+    assert lib.hkv_abi_version() == 2
     assert lib.hkv_block_bytes(8, 128) == 17664
     assert lib.hkv_block_bytes(4, 128) == 8832
     assert lib.hkv_block_bytes(8, 64) == -1
@@ -47,7 +47,8 @@ def test_struct_layouts_match_c_compiler(tmp_path):
         pytest.skip("gcc not available")
     structs = {"HkvPackArgs": _lib.PackArgs, "HkvRepackArgs": _lib.RepackArgs,
                "HkvZoneWriteArgs": _lib.ZoneWriteArgs, "HkvF16Zone": _lib.F16Zone,
-               "HkvDecodeArgs": _lib.DecodeArgs}
+               "HkvDecodeArgs": _lib.DecodeArgs, "HkvPrefillArgs": _lib.PrefillArgs,
+               "HkvCopyDesc": _lib.CopyDesc, "HkvPfStats": _lib.PfStats}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "%s"' % HEADER, "int main(void){"]
     for cname, py in structs.items():
         lines.append('printf("%s size %%zu\\n", sizeof(%s));' % (cname, cname))
@@ -108,3 +109,23 @@ def test_workspace_size(lib):
     # header + counters + partial states for up to 64 ranges per (sequence, kv head):
     # 8 pairs x 64 ranges x 4 heads x 132 floats
     assert n == 256 + 256 + 8 * 64 * 4 * 132 * 4
+
+
+def test_prefetcher_and_gather_argument_errors(lib):
+    from heterokv import _lib
+    assert lib.hkv_pf_submit(None, None, 0, 0, 0) == -1
+    assert b"null" in lib.hkv_last_error()
+    assert lib.hkv_pf_wait(None, 0, None) == -1
+    assert lib.hkv_pf_mark(None, 0, None) == -1
+    assert lib.hkv_pf_record(None, 0) == -1
+    st = _lib.PfStats()
+    assert lib.hkv_pf_stats(None, ctypes.byref(st)) == -1
+    assert lib.hkv_pf_host_ptr(None, 0) is None
+    assert lib.hkv_pf_stream(None) is None
+    assert lib.hkv_pf_destroy(None) == 0
+    out = ctypes.c_void_p()
+    assert lib.hkv_pf_create(0, 0, 0, ctypes.byref(out)) == -1     # num_slots must be >= 1
+    # gather: empty is a no-op, bad record size / null buffers are argument errors
+    assert lib.hkv_gather_blocks(None, 0, None, 0, None, 0, 8832, None, None, None) == 0
+    assert lib.hkv_gather_blocks(4096, 4, None, 0, 4096, 2, 8830, 4096, None, None) == -1
+    assert lib.hkv_gather_blocks(4096, 4, None, 2, 4096, 2, 8832, 4096, None, None) == -1
