@@ -176,6 +176,215 @@ def bench_prefill(torch, ops, args):
     print(json.dumps(line), flush=True)
 
 
+T_LAYERS, T_HQ, T_HKV, T_HIDDEN, T_INTER, T_VOCAB = 28, 28, 4, 3584, 18944, 152064
+T_CTX, T_CHUNK, T_SINK, T_KEEP, T_HOST_FRAC = 131072, 2048, 64, 4160, 0.75
+
+
+def _tiered_model(torch, dev):
+    """Random-init bf16 Qwen2-style decoder: 28 layers, hidden 3584, 28 q / 4 kv heads,
+    head_dim 128, MLP 18944, vocabulary 152064 (Qwen2-VL-7B's text decoder sizes)."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    from heterokv.engine_wrapper import register_attention
+    cfg = Qwen2Config(vocab_size=T_VOCAB, hidden_size=T_HIDDEN, intermediate_size=T_INTER,
+                      num_hidden_layers=T_LAYERS, num_attention_heads=T_HQ, num_key_value_heads=T_HKV,
+                      max_position_embeddings=T_CTX + 4096, rope_theta=1e6, rms_norm_eps=1e-6,
+                      tie_word_embeddings=False, attn_implementation=register_attention())
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Qwen2ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    return model.eval()
+
+
+def _decode_tokens(torch, model, cache, tok, pos, n, dev):
+    """n greedy decode steps; each ends with a synchronize (the host reads the token id).
+    Returns the next token, position, per-token seconds and per-token prefetch stats."""
+    times, stats = [], []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        out = model(input_ids=tok, past_key_values=cache, position_ids=torch.tensor([[pos]], device=dev),
+                    use_cache=True, logits_to_keep=1)
+        tok = out.logits[:, -1:].argmax(-1)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        stats.append(cache.prefetch_stats())
+        pos += 1
+    return tok, pos, times, stats
+
+
+def _summ(times, stats):
+    import statistics
+    t = statistics.median(times)
+    stall = statistics.median([s["stall_ms"] for s in stats]) if stats else 0.0
+    return {"tok_per_s": round(1.0 / t, 3), "ms_per_token": round(t * 1e3, 3),
+            "prefetch_stall_ms_per_token": round(stall, 3),
+            "stall_fraction": round(stall / (t * 1e3), 4)}
+
+
+def cpu_baseline_tiered(torch, model, budget_s=20.0):
+    """The reference's decode step restated on the host cores for ONE of the 28 layers at
+    the 131072-token shape (Path C: dequantize all 126912 INT4 tokens of the layer to fp16,
+    float64 attention over them plus 64 sink + 4096 recent tokens, 28 q / 4 kv heads) and
+    that layer's projections and MLP in float32 torch; the per-token figure scales the layer
+    time by 28 and adds the final norm + lm_head GEMV."""
+    import numpy as np
+    from oracle import attention as oa
+    from oracle import compressor as oc
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:
+        threads = 1
+    mid = T_CTX - T_KEEP
+    g = np.random.default_rng(5)
+    kn = g.standard_normal((T_HKV, mid, D), dtype=np.float32).astype(np.float16)
+    vn = g.standard_normal((T_HKV, mid, D), dtype=np.float32).astype(np.float16)
+    kc, ks, kz = oc.compress(kn, 128)
+    vc, vs, vz = oc.compress(vn, 128)
+    hk = g.standard_normal((T_HKV, T_KEEP, D)).astype(np.float16).astype(np.float64)
+    hv = g.standard_normal((T_HKV, T_KEEP, D)).astype(np.float16).astype(np.float64)
+    layer = model.model.layers[0]
+    w = {n: p.detach().float().cpu() for n, p in layer.named_parameters()}
+    lm = model.lm_head.weight.detach().float().cpu()
+    x = torch.randn(1, T_HIDDEN)
+
+    def layer_step():
+        h = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * w["input_layernorm.weight"]
+        q = h @ w["self_attn.q_proj.weight"].T + w["self_attn.q_proj.bias"]
+        h @ w["self_attn.k_proj.weight"].T
+        h @ w["self_attn.v_proj.weight"].T
+        kd = oa.dequant_rows(kc, ks.reshape(T_HKV, mid), kz.reshape(T_HKV, mid))
+        vd = oa.dequant_rows(vc, vs.reshape(T_HKV, mid), vz.reshape(T_HKV, mid))
+        a = oa.attend(q.view(T_HQ, 1, D).double().numpy(), np.concatenate([kd, hk], 1), np.concatenate([vd, hv], 1))
+        o = torch.from_numpy(a.reshape(1, T_HQ * D)).float() @ w["self_attn.o_proj.weight"].T
+        h2 = x + o
+        h3 = h2 * torch.rsqrt(h2.pow(2).mean(-1, keepdim=True) + 1e-6) * w["post_attention_layernorm.weight"]
+        gte = torch.nn.functional.silu(h3 @ w["mlp.gate_proj.weight"].T) * (h3 @ w["mlp.up_proj.weight"].T)
+        return h2 + gte @ w["mlp.down_proj.weight"].T
+
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        layer_step()
+        n += 1
+        if time.perf_counter() - t0 >= budget_s / 2 or n >= 3:
+            break
+    t_layer = (time.perf_counter() - t0) / n
+    t1 = time.perf_counter()
+    x @ lm.T
+    t_head = time.perf_counter() - t1
+    t_tok = T_LAYERS * t_layer + t_head
+    return dict(value=1.0 / t_tok, unit="tok/s", cores=threads, kind="port",
+                sample="%d timed pass(es) of one decoder layer at 131072 tokens (Path C dequant of 126912 INT4 "
+                       "tokens + float64 attention + fp32 projections/MLP, %.2f s each), x28 + lm_head GEMV"
+                       % (n, t_layer))
+
+
+def bench_tiered(torch, args):
+    """End-to-end tiered decode at 131072 tokens: chunked prefill (2048-token chunks, fused
+    prefill kernel), then 75% of every layer's INT4 block records moved to pinned host memory;
+    decode with each layer's host records copied on the side stream one layer ahead."""
+    from heterokv.engine_wrapper import ChunkedPrefillEngine, FusedHeteroCache
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.perf_counter()
+    model = _tiered_model(torch, dev)
+    torch.cuda.synchronize()
+    print("[tiered] model ready in %.1f s" % (time.perf_counter() - t0), file=sys.stderr, flush=True)
+    ids = torch.randint(0, T_VOCAB, (1, T_CTX), generator=torch.Generator().manual_seed(1)).to(dev)
+    cache = FusedHeteroCache(num_layers=T_LAYERS, sink_tokens=T_SINK, keep_tail=T_KEEP, chunk_size=T_CHUNK,
+                             device=str(dev), fused_prefill=True)
+    t0 = time.perf_counter()
+    with torch.inference_mode():
+        eng = ChunkedPrefillEngine(model, cache, chunk_size=T_CHUNK)
+        for start in range(0, T_CTX, 16 * T_CHUNK):
+            part = ids[:, :start + 16 * T_CHUNK]
+            eng.prefill(part[:, start:], position_ids=torch.arange(start, part.shape[1], device=dev)[None])
+            torch.cuda.synchronize()
+            print("[tiered] prefill %d / %d tokens, %.1f s" % (part.shape[1], T_CTX, time.perf_counter() - t0),
+                  file=sys.stderr, flush=True)
+    prefill_s = time.perf_counter() - t0
+    mgr = cache._manager
+    int4_tokens = mgr.dram_tokens(0)
+    out = {}
+    with torch.inference_mode():
+        tok, pos = ids[:, -1:], T_CTX
+        # all INT4 records resident in HBM
+        tok, pos, _, _ = _decode_tokens(torch, model, cache, tok, pos, args.warmup, dev)
+        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, args.steps, dev)
+        out["resident"] = _summ(tm, st)
+        print("[tiered] resident: %s" % out["resident"], file=sys.stderr, flush=True)
+        moved = cache.offload_to_host(T_HOST_FRAC, seed=0)
+        torch.cuda.synchronize()
+        host_bytes = mgr.memory_summary()["host_bytes"]
+        # full retrieval (Path C): every host record crosses PCIe every token
+        tok, pos, _, _ = _decode_tokens(torch, model, cache, tok, pos, args.warmup, dev)
+        b0 = mgr.prefetch_stats()["bytes_h2d"]
+        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, args.steps, dev)
+        full = _summ(tm, st)
+        full["h2d_bytes_per_token"] = (st[-1]["bytes_h2d"] - b0) // max(args.steps, 1)
+        out["full"] = full
+        print("[tiered] full retrieval: %s" % full, file=sys.stderr, flush=True)
+        # the same without look-ahead (copies issued when the layer needs them)
+        mgr.enable_prefetch = False
+        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, max(args.steps // 2, 1), dev)
+        out["full_no_lookahead"] = _summ(tm, st)
+        mgr.enable_prefetch = True
+        # windowed retrieval (Path A): the top-w_t chunks, w_t from the adaptive controller
+        cache.retrieval_window = "adaptive"
+        tok, pos, _, _ = _decode_tokens(torch, model, cache, tok, pos, args.warmup, dev)
+        b0 = mgr.prefetch_stats()["bytes_h2d"]
+        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, args.steps, dev)
+        win = _summ(tm, st)
+        win["h2d_bytes_per_token"] = (st[-1]["bytes_h2d"] - b0) // max(args.steps, 1)
+        win["window_chunks"] = int(mgr._adaptive_controller.stats["current_w"])
+        out["windowed"] = win
+        print("[tiered] windowed retrieval: %s" % win, file=sys.stderr, flush=True)
+        # host -> HBM copy rate of one layer's records on the side stream
+        pf, st0 = mgr._pf, mgr._layers[0]
+        rb = st0.n_host * mgr._staging[0].record_bytes
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record()
+        pf.submit([(mgr._staging[0].data.data_ptr(), pf.host_ptr(st0.host_off), rb)], slot=0)
+        pf.wait(0)
+        ev1.record()
+        ev1.synchronize()
+        h2d_gbs = rb / (ev0.elapsed_time(ev1) * 1e-3) / 1e9
+    weights = sum(p.numel() * p.element_size() for p in model.parameters())
+    kv_hbm = (int4_tokens * T_HKV * 2 * (D // 2 + 5) * (1 - T_HOST_FRAC) + T_KEEP * T_HKV * D * 2 * 2) * T_LAYERS
+    tok_bytes = weights + kv_hbm
+    ms = full["ms_per_token"]
+    gbs = tok_bytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_tiered(torch, model, args.cpu_budget * 2)
+    line = {
+        "metric": "end-to-end decode tok/s at 131072-token context with 75% of INT4 KV blocks in pinned host "
+                  "DRAM (full retrieval)",
+        "value": full["tok_per_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights, seeded random token ids)",
+        "config": {"workload": "tiered decode: 28-layer Qwen2-style decoder (hidden 3584, 28 q / 4 kv heads, "
+                               "head_dim 128, MLP 18944, vocab 152064), 131072-token prompt prefilled in 2048-token "
+                               "chunks, sink 64 + recent 4096 fp16, INT4 middle with 75% of its 16-token blocks "
+                               "in pinned host memory, batch 1, greedy",
+                   "int4_tokens_per_layer": int4_tokens, "host_records_moved": moved, "host_bytes": host_bytes,
+                   "prefill_seconds": round(prefill_s, 1), "h2d_gbs_one_layer_copy": round(h2d_gbs, 2),
+                   "hbm_bytes_per_token": int(tok_bytes)},
+        "variants": out,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": ({k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()}
+                         if cpu else None),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -185,9 +394,11 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "tiered"], default="decode",
                     help="decode: the headline single-layer decode (default); prefill: the chunked-prefill "
-                         "kernel on a 2048-token chunk over 64 + 131072 INT4 + 4096 tokens (MFMA bound)")
+                         "kernel on a 2048-token chunk over 64 + 131072 INT4 + 4096 tokens (MFMA bound); "
+                         "tiered: end-to-end 28-layer decode at 131072 tokens with 75%% of the INT4 KV in "
+                         "pinned host memory (use small --steps/--warmup, e.g. 8 / 2)")
     ap.add_argument("--copy-calibration", type=float, default=0.0,
                     help="run only torch's device copy of this many MB (20 launches) so that rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
@@ -215,6 +426,8 @@ def main():
 
     if args.workload == "prefill":
         return bench_prefill(torch, ops, args)
+    if args.workload == "tiered":
+        return bench_tiered(torch, args)
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

@@ -26,10 +26,16 @@
 // (atomic ticket after a release fence) merges the S partial states with
 // independent loads and writes the output, so the whole op is one launch.
 // Workgroup ids interleave the pairs so that all ranges of a pair land on one
-// XCD (dispatch is round-robin over XCDs by workgroup id).
+// XCD (dispatch is round-robin over XCDs by workgroup id).  When every range of
+// a pair shares an XCD (pairs a multiple of the XCD count), the hand-off stays
+// in that XCD's L2: plain stores, an L2 atomic ticket and L1-bypassing loads.
+// Otherwise it goes through memory with agent-scope (sc1) accesses.  Each
+// workgroup checks its XCD id against the assumed placement and reports a
+// mismatch in the error word (bit 2).
 #include "hkv_internal.h"
 
 #include <math.h>
+#include <string.h>
 
 namespace hkv {
 namespace {
@@ -44,7 +50,10 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 constexpr int kWaves = 8;                 // waves per workgroup
 constexpr int kThreads = kWaves * 64;
 constexpr int kPartStride = kHeadDim + 4;  // o[128], m, l, 2 pad (16-byte rows)
-constexpr int kPrefetch = 2;               // INT4 block pairs in flight per wave
+#ifndef HKV_DECODE_PREFETCH
+#define HKV_DECODE_PREFETCH 2
+#endif
+constexpr int kPrefetch = HKV_DECODE_PREFETCH;  // INT4 block pairs in flight per wave
 constexpr int kMaxSplits = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 // Bytes one kv head reads per item (the weights that balance the ranges).
@@ -78,9 +87,13 @@ struct DecodeParams {
     uint16_t* out;
     int64_t o_sb, o_sh;
     int* err;
-    int* counters;
+    int* counters;            // agent-scope tickets, one int per pair
+    int* counters_l2;         // XCD-local tickets, one 256-byte line per pair
     float* partials;
     int max_splits;
+    int64_t part_pair_stride;  // floats between the partial blocks of consecutive pairs (256-byte multiple)
+    int xcc_local;             // 1: all ranges of a pair run on one XCD (see above)
+    int nxcc;                  // XCDs the dispatcher round-robins over
 };
 
 // Partial states cross workgroups (and XCDs) through agent-scope relaxed atomic
@@ -93,6 +106,14 @@ __device__ __forceinline__ void st_agent(float* p, float v) {
 }
 __device__ __forceinline__ float ld_agent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// L1-bypassing (sc0) loads through a buffer resource: coherent at the XCD's L2.
+__device__ __forceinline__ float ld_l2(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 1));
+}
+__device__ __forceinline__ f4 ld_l2_f4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 1));
 }
 
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
@@ -333,6 +354,10 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
     const int nrep = p.nrep;
+    if (p.xcc_local && p.nxcc > 1 && threadIdx.x == 0) {
+        const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15;   // HW_REG_XCC_ID
+        if (xcc % p.nxcc != (int)(blockIdx.x % p.nxcc) && p.err) atomicOr(p.err, 4);
+    }
 
     const int len4 = p.int4_lens ? min(max(p.int4_lens[b], 0), p.int4_max_len) : p.int4_max_len;
     int lenz[HKV_MAX_F16_ZONES];
@@ -378,10 +403,15 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             const int cn = min(64, lb1 - cb);
             const int ids = load_block_ids(p, b, cb, cb + cn, lane);
             Int4Blk bufA[kPrefetch], bufB[kPrefetch];
+            // sched_barrier keeps each slot's loads together and in slot order, in the
+            // prologue as in the loop, so the waits before a slot's use only cover that
+            // slot and the later slots stay in flight
 #pragma unroll
             for (int k = 0; k < kPrefetch; ++k) {
+                __builtin_amdgcn_sched_barrier(0);
                 load_int4(p, h, __builtin_amdgcn_readlane(ids, min(2 * k, cn - 1)), c, g, bufA[k]);
                 load_int4(p, h, __builtin_amdgcn_readlane(ids, min(2 * k + 1, cn - 1)), c, g, bufB[k]);
+                __builtin_amdgcn_sched_barrier(0);
             }
             for (int base = 0; base < cn; base += 2 * kPrefetch) {
 #pragma unroll
@@ -390,8 +420,10 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                     const int nA = (i < cn ? min(kBlockTokens, len4 - (cb + i) * kBlockTokens) : 0);
                     const int nB = (i + 1 < cn ? min(kBlockTokens, len4 - (cb + i + 1) * kBlockTokens) : 0);
                     step_int4_pair(bufA[k], bufB[k], nA, nB, g, qf, p.scale_log2, acc, m, l);
+                    __builtin_amdgcn_sched_barrier(0);
                     load_int4(p, h, __builtin_amdgcn_readlane(ids, min(i + 2 * kPrefetch, cn - 1)), c, g, bufA[k]);
                     load_int4(p, h, __builtin_amdgcn_readlane(ids, min(i + 2 * kPrefetch + 1, cn - 1)), c, g, bufB[k]);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
         }
@@ -406,15 +438,20 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                 const ZoneP& z = p.z[zi];
                 const int len = lenz[zi];
                 F16Tile buf[2];
+                __builtin_amdgcn_sched_barrier(0);
                 load_f16(z, bh, t0, c, g, buf[0]);
+                __builtin_amdgcn_sched_barrier(0);
                 load_f16(z, bh, min(t0 + 1, t1 - 1), c, g, buf[1]);
+                __builtin_amdgcn_sched_barrier(0);
                 for (int base = t0; base < t1; base += 2) {
 #pragma unroll
                     for (int k = 0; k < 2; ++k) {
                         const int t = base + k;
                         step_f16(buf[k], t < t1 ? min(kBlockTokens, len - t * kBlockTokens) : 0, g, qf,
                                  p.scale_log2, acc, m, l);
+                        __builtin_amdgcn_sched_barrier(0);
                         load_f16(z, bh, min(t + 2, t1 - 1), c, g, buf[k]);
+                        __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             }
@@ -444,7 +481,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     __syncthreads();
 
     const int nout = nrep * kHeadDim;
-    float* part = p.partials + ((int64_t)bh * nsplit + split) * (nrep * kPartStride);
+    float* part = p.partials + (int64_t)bh * p.part_pair_stride + (int64_t)split * (nrep * kPartStride);
     for (int idx = threadIdx.x; idx < nout; idx += kThreads) {
         const int hd = idx >> 7, d = idx & (kHeadDim - 1);
         float M = -INFINITY;
@@ -460,6 +497,12 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         }
         if (nsplit == 1) {
             p.out[(int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d] = f2h_rn(L > 0.f ? O / L : 0.f);
+        } else if (p.xcc_local) {
+            part[hd * kPartStride + d] = O;
+            if (d == 0) {
+                part[hd * kPartStride + kHeadDim] = M;
+                part[hd * kPartStride + kHeadDim + 1] = L;
+            }
         } else {
             st_agent(part + hd * kPartStride + d, O);
             if (d == 0) {
@@ -476,8 +519,13 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
-    if (threadIdx.x == 0)
-        sm_ticket = __hip_atomic_fetch_add(&p.counters[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) {
+        // the stores above have completed (in L2, or in memory for sc1 stores)
+        if (p.xcc_local)
+            sm_ticket = __hip_atomic_fetch_add(&p.counters_l2[bh * 64], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else
+            sm_ticket = __hip_atomic_fetch_add(&p.counters[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __syncthreads();
     if (sm_ticket != nsplit - 1) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -486,7 +534,9 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     // memory round trip.  Thread t owns float4 `u` of one head and the splits
     // s = k, k + K, k + 2K, ... (K = threads per unit); all its loads are
     // independent.  The K per-thread states then merge through LDS.
-    const float* parts = p.partials + (int64_t)bh * nsplit * (nrep * kPartStride);
+    const float* parts = p.partials + (int64_t)bh * p.part_pair_stride;
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)parts, 0, (int)(nsplit * nrep * kPartStride * sizeof(float)), 0x00020000);
     const int units = nrep * (kHeadDim / 4);
     const int K = kThreads / units;                  // >= 1 because nrep <= 16
     float* sm = smem;                                // [K][units][6] = (M, L, O[4])
@@ -501,10 +551,17 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int sj = s0 + j * K;
-                const float* ps = parts + (int64_t)min(sj, nsplit - 1) * (nrep * kPartStride) + hd * kPartStride;
-                ms[j] = sj < nsplit ? ld_agent(ps + kHeadDim) : -INFINITY;
-                ls[j] = ld_agent(ps + kHeadDim + 1);
-                os[j] = f4{ld_agent(ps + d4), ld_agent(ps + d4 + 1), ld_agent(ps + d4 + 2), ld_agent(ps + d4 + 3)};
+                const int off = min(sj, nsplit - 1) * (nrep * kPartStride) + hd * kPartStride;
+                if (p.xcc_local) {
+                    ms[j] = sj < nsplit ? ld_l2(prs, (off + kHeadDim) * 4) : -INFINITY;
+                    ls[j] = ld_l2(prs, (off + kHeadDim + 1) * 4);
+                    os[j] = ld_l2_f4(prs, (off + d4) * 4);
+                } else {
+                    const float* ps = parts + off;
+                    ms[j] = sj < nsplit ? ld_agent(ps + kHeadDim) : -INFINITY;
+                    ls[j] = ld_agent(ps + kHeadDim + 1);
+                    os[j] = f4{ld_agent(ps + d4), ld_agent(ps + d4 + 1), ld_agent(ps + d4 + 2), ld_agent(ps + d4 + 3)};
+                }
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -545,7 +602,12 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) op[v] = f2h_rn(O[v] * inv);
     }
-    if (threadIdx.x == 0) __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) {
+        if (p.xcc_local)
+            __hip_atomic_store(&p.counters_l2[bh * 64], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else
+            __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 constexpr size_t kWsHeader = 256;
@@ -579,10 +641,30 @@ int choose_splits(int BH, int int4_max_len, const int32_t* f16_max_lens, int nz,
     return (int)s;
 }
 
+// Workspace: [header (error word) | agent tickets | XCD-local tickets (256 B each) |
+// partial states, one 256-byte aligned block per (sequence, kv head)].
+size_t pair_part_bytes(int nrep, int nsplit) { return align256((size_t)nsplit * nrep * kPartStride * sizeof(float)); }
+
 size_t workspace_bytes(int B, int Hq, int Hkv, int nsplit) {
     const size_t BH = (size_t)B * Hkv;
     const int nrep = Hq / Hkv;
-    return kWsHeader + align256(BH * sizeof(int)) + BH * (size_t)nsplit * nrep * kPartStride * sizeof(float);
+    return kWsHeader + align256(BH * sizeof(int)) + BH * 256 + BH * pair_part_bytes(nrep, nsplit);
+}
+
+// XCDs that workgroups are dispatched over round-robin: gfx950 has 32 CUs per
+// XCD, so a partition with N CUs spans N / 32 of them.
+int num_xcc() {
+    static int cached = 0;
+    if (cached > 0) return cached;
+    int dev = 0;
+    hipDeviceProp_t prop;
+    int n = 1;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+        strncmp(prop.gcnArchName, "gfx950", 6) == 0 && prop.multiProcessorCount % 32 == 0 &&
+        prop.multiProcessorCount >= 32)
+        n = prop.multiProcessorCount / 32;
+    cached = n;
+    return cached;
 }
 
 size_t lds_bytes(int nrep) {
@@ -688,7 +770,11 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     char* ws = (char*)a->workspace;
     p.err = (int*)ws;
     p.counters = (int*)(ws + kWsHeader);
-    p.partials = (float*)(ws + kWsHeader + align256((size_t)BH * sizeof(int)));
+    p.counters_l2 = (int*)(ws + kWsHeader + align256((size_t)BH * sizeof(int)));
+    p.partials = (float*)(ws + kWsHeader + align256((size_t)BH * sizeof(int)) + (size_t)BH * 256);
+    p.part_pair_stride = (int64_t)(pair_part_bytes(nrep, ms) / sizeof(float));
+    p.nxcc = num_xcc();
+    p.xcc_local = (BH % p.nxcc) == 0 ? 1 : 0;
     p.max_splits = ms;
     const size_t lds = lds_bytes(nrep);
     if (lds > 64 * 1024) {

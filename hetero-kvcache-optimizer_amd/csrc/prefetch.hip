@@ -55,7 +55,7 @@ int check_slot(HkvPrefetcher* pf, int slot) {
 extern "C" int hkv_pf_create(int device, size_t arena_bytes, int num_slots, HkvPrefetcher** out) {
     clear_error();
     HKV_REQUIRE(out != nullptr, HKV_ERR_ARG, "hkv_pf_create: null out");
-    HKV_REQUIRE(num_slots > 0 && num_slots <= 256, HKV_ERR_ARG, "hkv_pf_create: num_slots %d out of range", num_slots);
+    HKV_REQUIRE(num_slots > 0 && num_slots <= 4096, HKV_ERR_ARG, "hkv_pf_create: num_slots %d out of range", num_slots);
     *out = nullptr;
     HKV_HIP_CHECK(hipSetDevice(device));
     HkvPrefetcher* pf = new (std::nothrow) HkvPrefetcher();

@@ -31,6 +31,7 @@ struct ZoneWriteParams {
     int64_t sb, sh, st;
     int H, T;
     const int32_t* slot_start;
+    int slot_base;
     int cap, ring;
     uint16_t* zk;
     uint16_t* zv;
@@ -40,7 +41,7 @@ struct ZoneWriteParams {
 __global__ __launch_bounds__(128) void zone_write_kernel(ZoneWriteParams p) {
     const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int d = threadIdx.x;
-    int slot = p.slot_start[b] + t;
+    int slot = (p.slot_start ? p.slot_start[b] : p.slot_base) + t;
     if (p.ring > 0) {
         slot %= p.ring;
         if (slot < 0) slot += p.ring;
@@ -104,7 +105,7 @@ extern "C" int hkv_zone_write(const HkvZoneWriteArgs* a, void* stream) {
     HKV_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->num_tokens >= 0, HKV_ERR_ARG,
                 "hkv_zone_write: bad sizes");
     if (a->batch == 0 || a->num_tokens == 0) return HKV_OK;
-    HKV_REQUIRE(a->k && a->v && a->slot_start && a->zone_k && a->zone_v, HKV_ERR_ARG,
+    HKV_REQUIRE(a->k && a->v && a->zone_k && a->zone_v, HKV_ERR_ARG,
                 "hkv_zone_write: null pointer");
     HKV_REQUIRE(a->num_kv_heads <= 65535 && a->batch <= 65535, HKV_ERR_ARG, "hkv_zone_write: grid too large");
     HKV_REQUIRE(a->ring >= 0 && a->ring <= a->capacity, HKV_ERR_ARG,
@@ -118,6 +119,7 @@ extern "C" int hkv_zone_write(const HkvZoneWriteArgs* a, void* stream) {
     p.H = a->num_kv_heads;
     p.T = a->num_tokens;
     p.slot_start = a->slot_start;
+    p.slot_base = a->slot_base;
     p.cap = a->capacity;
     p.ring = a->ring;
     p.zk = a->zone_k;

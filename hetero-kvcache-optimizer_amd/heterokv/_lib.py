@@ -59,7 +59,7 @@ class ZoneWriteArgs(ctypes.Structure):
                 ("src_stride_b", i64), ("src_stride_h", i64), ("src_stride_t", i64),
                 ("batch", i32), ("num_kv_heads", i32), ("head_dim", i32), ("num_tokens", i32),
                 ("slot_start", vp), ("capacity", i32), ("ring", i32),
-                ("zone_k", vp), ("zone_v", vp)]
+                ("zone_k", vp), ("zone_v", vp), ("slot_base", i32)]
 
 
 class F16Zone(ctypes.Structure):

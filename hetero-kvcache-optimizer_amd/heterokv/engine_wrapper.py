@@ -7,7 +7,10 @@ memory_summary, ChunkedPrefillEngine and build_fused_cache.
 Attention routes.
   * Prefill (new_len > 1): the reference hands transformers the full chunk (first
     chunk) or sink + old tail + chunk (later chunks) and lets SDPA attend
-    (manager.py:533-535,562-563); the same tensors are returned here.
+    (manager.py:533-535,562-563); the same tensors are returned here.  With
+    fused_prefill=True they are tagged, and the registered attention function runs
+    the MFMA prefill kernel instead of SDPA: the cached prefix as an fp16 zone, the
+    chunk causally (the mask SDPA would get for an unpadded batch).
   * Decode, default (Path C, engine_wrapper.py:236-245): the reference prepends every
     DRAM token, dequantized to fp16, to sink + tail + heavy hitters.  With
     fused_decode=True (default) update() returns the new token's K/V tagged with a
@@ -17,6 +20,8 @@ Attention routes.
     concatenated tensors are materialized and returned.
 The Path C gate is the reference's: DRAM tokens join a layer's attention only
 while _swap_in_tokens > 0, which layer 0 refreshes after its own decode update.
+adaptive_self_healing=True selects the reference's Path A (engine_wrapper.py:204-222):
+only the top-w_t chunks by score join, w_t from AdaptivePrefetchController.
 """
 import gc
 import math
@@ -38,11 +43,12 @@ class FusedHeteroCache(DynamicCache):
                  chunk_size: int = 2048, device: str = "cuda:0", group_size: int = 128,
                  enable_quant: bool = True, enable_prefetch: bool = True, enable_triton: bool = True,
                  bandwidth_limiter=None, self_healing: bool = True, adaptive_self_healing: bool = False,
-                 enable_method_d: bool = False, method_d_alpha: float = 1.0, fused_decode: bool = True):
+                 enable_method_d: bool = False, method_d_alpha: float = 1.0, fused_decode: bool = True,
+                 fused_prefill: bool = False):
         super().__init__()
-        if adaptive_self_healing:
-            raise HeteroKVError(-4, "windowed retrieval (adaptive_self_healing) is not part of this build; "
-                                    "the default full retrieval (Path C) is")
+        if adaptive_self_healing and not fused_decode:
+            raise HeteroKVError(-4, "windowed retrieval (adaptive_self_healing) runs on the fused decode path; "
+                                    "use fused_decode=True")
         self.sink_tokens = sink_tokens
         self.keep_tail = keep_tail
         self.chunk_size = chunk_size
@@ -57,6 +63,8 @@ class FusedHeteroCache(DynamicCache):
         self.enable_method_d = enable_method_d
         self.method_d_alpha = method_d_alpha
         self.fused_decode = fused_decode
+        self.fused_prefill = fused_prefill
+        self._prefill_zone = None
         self._num_layers = num_layers
         self._manager: Optional[HeteroKVManager] = None
         self.real_seq_len: int = 0
@@ -71,6 +79,8 @@ class FusedHeteroCache(DynamicCache):
                                         enable_quant=self.enable_quant, enable_prefetch=self.enable_prefetch,
                                         group_size=self.group_size, bandwidth_limiter=self._bandwidth_limiter,
                                         enable_method_d=self.enable_method_d, method_d_alpha=self.method_d_alpha)
+        if self.adaptive_self_healing:
+            self._manager.retrieval_window = "adaptive"
         return self._manager
 
     # ------------------------------------------------------------------ DynamicCache interface
@@ -91,6 +101,10 @@ class FusedHeteroCache(DynamicCache):
         else:
             out_k, out_v = manager.update(layer_idx, key_states, value_states, mode=mode,
                                           seq_offset=self.real_seq_len)
+            if mode == "prefill" and self.fused_prefill:
+                tag = (self, out_k.shape[-2] - new_len)
+                out_k._hkv_prefill = tag
+                out_v._hkv_prefill = tag
             if include_dram:
                 dram_k, dram_v, count = manager.decompress_dram_chunks(layer_idx)
                 if dram_k is not None and count > 0:
@@ -189,6 +203,24 @@ class FusedHeteroCache(DynamicCache):
             return None
         return self._manager.chunk_codes(chunk_key)
 
+    def _fused_prefill_attention(self, query, key, value, prefix, scaling):
+        """Prefill attention on the MFMA kernel: every query sees the `prefix` cached rows of
+        key/value (written into a reusable fp16 zone) and the chunk rows causally."""
+        from . import ops
+        B, H, S, _ = key.shape
+        zones = []
+        if prefix:
+            z = self._prefill_zone
+            if z is None or z.capacity < prefix or z.batch != B or z.num_kv_heads != H:
+                z = self._prefill_zone = ops.F16Zone(B, H, prefix, key.device)
+            z.write(key[:, :, :prefix].to(torch.float16), value[:, :, :prefix].to(torch.float16), [0] * B)
+            zones.append((z, None, prefix))
+        ck = key[:, :, prefix:].to(torch.float16).contiguous()
+        cv = value[:, :, prefix:].to(torch.float16).contiguous()
+        out = ops.prefill_attention(query.to(torch.float16), zones=zones, chunk_k=ck, chunk_v=cv,
+                                    sm_scale=scaling)
+        return out.to(query.dtype)
+
     def fused_attn_on_swapped(self, q: torch.Tensor, chunk_key: str,
                               sm_scale: Optional[float] = None) -> Optional[torch.Tensor]:
         """engine_wrapper.py:357-404: attention of q over one chunk's INT4 tokens."""
@@ -206,12 +238,18 @@ def heterokv_attention_forward(module, query, key, value, attention_mask, scalin
     """Attention function registered with transformers as "heterokv".
 
     Decode tokens tagged by FusedHeteroCache.update attend through the manager's
-    fused INT4/fp16 kernel; every other call (prefill chunks) goes to transformers'
-    SDPA attention on the tensors the cache returned, as in the reference."""
+    fused INT4/fp16 kernel, prefill chunks tagged by a fused_prefill cache through the
+    MFMA prefill kernel; every other call goes to transformers' SDPA attention on the
+    tensors the cache returned, as in the reference."""
     route = getattr(key, "_hkv_route", None)
     if route is not None and query.shape[2] == 1:
         cache, layer_idx, include_dram = route
         out = cache._manager.attend_decode(layer_idx, query, sm_scale=scaling, include_dram=include_dram)
+        return out.transpose(1, 2).contiguous(), None
+    pre = getattr(key, "_hkv_prefill", None)
+    if pre is not None and query.shape[2] == key.shape[2] - pre[1]:
+        cache, prefix = pre
+        out = cache._fused_prefill_attention(query, key, value, prefix, scaling)
         return out.transpose(1, 2).contiguous(), None
     from transformers.integrations.sdpa_attention import sdpa_attention_forward
     return sdpa_attention_forward(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout,

@@ -156,7 +156,11 @@ class HeteroKVManager:
         self._staging: List[ops.Int4Pool] = []
         self._buf_owner: List[int] = []
         self._next_buf = 0
-        self._pending: Dict[int, Tuple[int, Any]] = {}   # layer -> (staging buffer, selection)
+        # layer -> (staging buffer, selection, event slot).  Each layer owns two event slots
+        # (2 * layer + parity) used alternately, so the events of one step's wait survive
+        # the look-ahead submission of the next step until prefetch_stats reads them.
+        self._pending: Dict[int, Tuple[int, Any, int]] = {}
+        self._slot_parity: Dict[int, int] = {}
         self._waited: List[int] = []
         self._selection_of: Dict[int, Any] = {}
         self._window_tables: Dict[Any, Tuple[torch.Tensor, int]] = {}
@@ -470,7 +474,7 @@ class HeteroKVManager:
             return 0
         rb = ops.record_bytes(plan[0][1].H)
         arena = sum(len(c) * ops.record_bytes(st.H) for _, st, c in plan)
-        self._pf = Prefetcher(self.device, arena, num_slots=max(len(self._layers), 1))
+        self._pf = Prefetcher(self.device, arena, num_slots=2 * max(len(self._layers), 1))
         off = 0
         moved = 0
         for li, st, chosen in plan:
@@ -589,21 +593,25 @@ class HeteroKVManager:
                     runs.append((k0, k1))
         return runs
 
-    def _submit(self, layer_idx: int, sel) -> int:
+    def _submit(self, layer_idx: int, sel) -> Tuple[int, Any, int]:
         st = self._layers[layer_idx]
         buf = self._next_buf
         self._next_buf = (buf + 1) % len(self._staging)
-        prev = self._buf_owner[buf]
+        prev_slot = self._buf_owner[buf]
+        prev = prev_slot // 2 if prev_slot >= 0 else -1
         if prev >= 0 and self._pending.get(prev, (None,))[0] == buf:
             del self._pending[prev]        # its copy is overwritten before use: fetch again later
+        parity = self._slot_parity.get(layer_idx, 0)
+        self._slot_parity[layer_idx] = parity ^ 1
+        slot = 2 * layer_idx + parity
         rb = ops.record_bytes(st.H)
         dst = self._staging[buf].data
         copies = [(dst[k0].data_ptr(), self._pf.host_ptr(st.host_off + k0 * rb), (k1 - k0) * rb)
                   for k0, k1 in self._host_runs(st, sel)]
-        self._pf.submit(copies, slot=layer_idx, after_slot=prev)
-        self._buf_owner[buf] = layer_idx
-        self._pending[layer_idx] = (buf, sel)
-        return buf
+        self._pf.submit(copies, slot=slot, after_slot=prev_slot)
+        self._buf_owner[buf] = slot
+        self._pending[layer_idx] = (buf, sel, slot)
+        return self._pending[layer_idx]
 
     def _prefetch_after(self, layer_idx: int) -> None:
         """Submit the copies of the next layer (cyclically) that holds host records."""
@@ -622,7 +630,7 @@ class HeteroKVManager:
     def prefetch_stats(self, reset: bool = True) -> Dict[str, Any]:
         """Stall of every layer that waited for host records since the last call: per layer
         max(0, t(copies done) - t(kernel needs them)) in ms (synchronizes on those events)."""
-        per = [(li, self._pf.stall_ms(li)) for li in self._waited] if self._pf is not None else []
+        per = [(slot // 2, self._pf.stall_ms(slot)) for slot in self._waited] if self._pf is not None else []
         if reset:
             self._waited = []
         out = {"stall_ms": sum(ms for _, ms in per), "per_layer": per}
@@ -659,23 +667,25 @@ class HeteroKVManager:
             if sel is not None:
                 bt, n4 = self._window_table(layer_idx, st, sel)
         staged = n4 > 0 and st.n_host > 0 and bool(self._host_runs(st, sel))
-        buf = None
+        buf = slot = None
         if staged:
             p = self._pending.get(layer_idx)
-            buf = p[0] if (p is not None and p[1] == sel) else self._submit(layer_idx, sel)
+            if p is None or p[1] != sel:
+                p = self._submit(layer_idx, sel)
+            buf, _, slot = p
         if self._pf is not None and self.enable_prefetch:
             self._prefetch_after(layer_idx)
         if staged:
-            self._pf.wait(layer_idx)
+            self._pf.wait(slot)
         q16 = _as16(query_states)
         out = ops.decode_attention(q16, zones=zones, pool=st.pool if n4 else None,
                                    block_table=bt if n4 else None, int4_max_len=n4,
                                    sm_scale=sm_scale, workspace=self._workspace,
                                    staging=self._staging[buf] if staged else None)
         if staged:
-            self._pf.mark(layer_idx)
+            self._pf.mark(slot)
             self._pending.pop(layer_idx, None)
-            self._waited.append(layer_idx)
+            self._waited.append(slot)
         self._selection_of.pop(layer_idx, None)
         return out.to(query_states.dtype)
 

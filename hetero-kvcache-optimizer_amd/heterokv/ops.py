@@ -203,7 +203,8 @@ class F16Zone:
 
     def write(self, k, v, slot_start, ring=0):
         """Write k, v [B, H, T, 128] fp16 at slots slot_start[b] + t (mod `ring` if ring > 0;
-        ring=True means the whole capacity)."""
+        ring=True means the whole capacity).  An int slot_start (or a list of equal ints)
+        is passed by value: no host-to-device copy."""
         _require_gpu(k, v)
         if k.dtype != torch.float16 or v.dtype != torch.float16:
             raise HeteroKVError(-1, "F16Zone.write: k/v must be fp16")
@@ -215,12 +216,20 @@ class F16Zone:
         if B != self.batch or H != self.num_kv_heads:
             raise HeteroKVError(-1, "F16Zone.write: shape %s does not match zone [%d, %d]" %
                                 (tuple(k.shape), self.batch, self.num_kv_heads))
-        ss = _i32(slot_start, k.device)
+        if isinstance(slot_start, (list, tuple)) and slot_start and all(s == slot_start[0] for s in slot_start):
+            slot_start = int(slot_start[0])
+        ss, base = None, 0
+        if isinstance(slot_start, int):
+            base = slot_start
+        else:
+            ss = _i32(slot_start, k.device)
+            if ss.numel() < B:
+                raise HeteroKVError(-1, "F16Zone.write: %d start slots for %d sequences" % (ss.numel(), B))
         a = _lib.ZoneWriteArgs(k=k.data_ptr(), v=v.data_ptr(), src_stride_b=k.stride(0),
                                src_stride_h=k.stride(1), src_stride_t=k.stride(2), batch=B, num_kv_heads=H,
-                               head_dim=HEAD_DIM, num_tokens=T, slot_start=ss.data_ptr(),
+                               head_dim=HEAD_DIM, num_tokens=T, slot_start=ss.data_ptr() if ss is not None else None,
                                capacity=self.capacity, ring=(self.capacity if ring is True else int(ring)),
-                               zone_k=self.k.data_ptr(), zone_v=self.v.data_ptr())
+                               zone_k=self.k.data_ptr(), zone_v=self.v.data_ptr(), slot_base=base)
         check(load().hkv_zone_write(ctypes.byref(a), stream_ptr(k.device)), "hkv_zone_write")
 
     def copy_to(self, dst, src_slot, dst_slot, n):

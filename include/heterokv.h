@@ -173,20 +173,22 @@ int hkv_unpack_tokens(const uint8_t* pool, int64_t pool_blocks, const int32_t* b
 
 /*
  * Write `num_tokens` fp16 tokens into an fp16 zone (sink / recent window /
- * heavy hitters).  Token t of sequence b goes to slot slot_start[b] + t, taken
- * modulo `ring` when ring > 0 (a ring of that many slots, ring <= capacity).
- * K rows are copied; V goes to transposed tiles.
+ * heavy hitters).  Token t of sequence b goes to slot slot_start[b] + t (or
+ * slot_base + t when slot_start is NULL), taken modulo `ring` when ring > 0 (a
+ * ring of that many slots, ring <= capacity).  K rows are copied; V goes to
+ * transposed tiles.
  */
 typedef struct HkvZoneWriteArgs {
     const uint16_t* k;
     const uint16_t* v;
     int64_t src_stride_b, src_stride_h, src_stride_t;
     int32_t batch, num_kv_heads, head_dim, num_tokens;
-    const int32_t* slot_start;     /* [batch], device */
+    const int32_t* slot_start;     /* [batch], device; NULL -> slot_base for every sequence */
     int32_t capacity;              /* slots per (b,h); multiple of 16 */
     int32_t ring;                  /* 0 = no wrap, else ring length (<= capacity) */
     uint16_t* zone_k;              /* [batch][H][capacity][128] */
     uint16_t* zone_v;              /* [batch][H][capacity/16][4096 B tiles] */
+    int32_t slot_base;
 } HkvZoneWriteArgs;
 
 int hkv_zone_write(const HkvZoneWriteArgs* args, void* stream);
@@ -312,7 +314,7 @@ typedef struct HkvPfStats {
     uint64_t arena_bytes;
 } HkvPfStats;
 
-/* arena_bytes may be 0 (no arena); num_slots in [1, 256]. */
+/* arena_bytes may be 0 (no arena); num_slots in [1, 4096]. */
 int hkv_pf_create(int32_t device, size_t arena_bytes, int32_t num_slots, HkvPrefetcher** out);
 int hkv_pf_destroy(HkvPrefetcher* pf);
 /* Host address of arena byte `offset` (NULL if outside the arena). */

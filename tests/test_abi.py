@@ -106,9 +106,9 @@ def test_decode_argument_errors(lib):
 def test_workspace_size(lib):
     from heterokv import ops
     n = ops.decode_workspace_bytes(1, 32, 8, 28608, [64, 4096])
-    # header + counters + partial states for up to 64 ranges per (sequence, kv head):
-    # 8 pairs x 64 ranges x 4 heads x 132 floats
-    assert n == 256 + 256 + 8 * 64 * 4 * 132 * 4
+    # header + agent tickets + one 256-byte XCD-local ticket per pair + partial states for
+    # up to 64 ranges per (sequence, kv head): 8 pairs x 64 ranges x 4 heads x 132 floats
+    assert n == 256 + 256 + 8 * 256 + 8 * 64 * 4 * 132 * 4
 
 
 def test_prefetcher_and_gather_argument_errors(lib):

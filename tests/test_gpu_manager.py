@@ -204,3 +204,37 @@ def test_tiny_qwen2_end_to_end_with_registered_attention():
             print("  step %d max |logit diff| %.3e" % (step, err), flush=True)
             assert err < 5e-2
             tok = lf[:, -1:].argmax(-1)
+
+
+@pytest.mark.parametrize("adaptive", [False, True])
+def test_tiny_qwen2_fused_prefill_matches_sdpa(adaptive):
+    print("case: tiny Qwen2, fused prefill vs SDPA prefill, adaptive=%s" % adaptive, flush=True)
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    from heterokv.engine_wrapper import ChunkedPrefillEngine, FusedHeteroCache, register_attention
+    name = register_attention()
+    torch.manual_seed(0)
+    cfg = Qwen2Config(vocab_size=512, hidden_size=448, intermediate_size=1024, num_hidden_layers=2,
+                      num_attention_heads=7, num_key_value_heads=1, head_dim=128, max_position_embeddings=4096,
+                      attn_implementation=name)
+    model = Qwen2ForCausalLM(cfg).to(DEV, torch.float16).eval()
+    ids = torch.randint(0, 512, (1, 352), generator=torch.Generator().manual_seed(1)).to(DEV)
+    kw = dict(num_layers=2, sink_tokens=16, keep_tail=80, chunk_size=64, device=DEV, adaptive_self_healing=adaptive)
+    cache_f = FusedHeteroCache(fused_prefill=True, **kw)
+    cache_s = FusedHeteroCache(**kw)
+    with torch.inference_mode():
+        lf = ChunkedPrefillEngine(model, cache_f, chunk_size=64).prefill(ids).logits
+        ls = ChunkedPrefillEngine(model, cache_s, chunk_size=64).prefill(ids).logits
+        err = (lf.float() - ls.float()).abs().max().item()
+        print("  last chunk max |logit diff| %.3e" % err, flush=True)
+        assert err < 5e-2
+        tok = ids[:, -1:]
+        for step in range(3):
+            p = torch.tensor([[352 + step]], device=DEV)
+            a = model(input_ids=tok, past_key_values=cache_f, position_ids=p, use_cache=True).logits
+            b = model(input_ids=tok, past_key_values=cache_s, position_ids=p, use_cache=True).logits
+            err = (a.float() - b.float()).abs().max().item()
+            print("  decode step %d max |logit diff| %.3e" % (step, err), flush=True)
+            assert err < 5e-2
+            tok = a[:, -1:].argmax(-1)
+    if adaptive:
+        assert cache_f._manager.retrieval_window == "adaptive"

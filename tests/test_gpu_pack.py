@@ -158,3 +158,25 @@ def test_f16_zone_write_read_and_ring():
     rk, rv = z.read(48)
     assert torch.equal(rk[0, :, 40:48].cpu(), k2[0, :, :8]) and torch.equal(rk[0, :, :12].cpu(), k2[0, :, 8:])
     assert torch.equal(rv[0, :, 12:40].cpu(), v[0, :, 12:40])
+
+
+def test_f16_zone_write_per_sequence_slots_and_uniform_base():
+    print("case: fp16 zone write, per-sequence slots vs by-value base", flush=True)
+    from heterokv import ops
+    B, H, cap = 3, 2, 32
+    g = torch.Generator().manual_seed(10)
+    k = torch.randn((B, H, 5, 128), generator=g).half()
+    v = torch.randn((B, H, 5, 128), generator=g).half()
+    z = ops.F16Zone(B, H, cap, DEV)
+    z.write(k.to(DEV), v.to(DEV), torch.tensor([0, 7, 29], dtype=torch.int32), ring=True)
+    rk, rv = z.read(cap)
+    for b, s in enumerate([0, 7, 29]):
+        slots = [(s + t) % cap for t in range(5)]
+        assert torch.equal(rk[b][:, slots].cpu(), k[b]) and torch.equal(rv[b][:, slots].cpu(), v[b])
+    z2 = ops.F16Zone(B, H, cap, DEV)
+    z2.write(k.to(DEV), v.to(DEV), 11)
+    z3 = ops.F16Zone(B, H, cap, DEV)
+    z3.write(k.to(DEV), v.to(DEV), torch.tensor([11, 11, 11], dtype=torch.int32))
+    assert torch.equal(z2.k, z3.k) and torch.equal(z2.v, z3.v)
+    rk, _ = z2.read(16)
+    assert torch.equal(rk[:, :, 11:16].cpu(), k)

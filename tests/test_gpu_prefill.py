@@ -113,6 +113,11 @@ def test_medium_c4_like():
     _case(6, 1, 32, 8, 256, 64, [4096], [256])
 
 
+def test_qwen2_7b_gqa_geometry():
+    print("case: prefill 28/4 (n_rep 7) Sq=100, 64 + 600 INT4 + 300 recent + causal", flush=True)
+    _case(8, 1, 28, 4, 100, 64, [600], [300])
+
+
 def test_reference_api_fused_dequant_attn_forward():
     print("case: fused_dequant_attn_forward drop-in", flush=True)
     from heterokv import fused_dequant_attn_forward
