@@ -141,15 +141,15 @@ struct F16Tile {
 // < 0 staging record ~phys.  Every load of a block is issued back to back so
 // several blocks stay in flight.
 __device__ __forceinline__ void load_int4(const DecodeParams& p, int h, int phys, int c, int g, Int4Blk& d) {
-    const int H = p.Hkv;
-    const uint8_t* rec = phys >= 0 ? p.pool + (int64_t)phys * ((int64_t)H * 2208)
-                                   : p.staging + (int64_t)(~phys) * ((int64_t)H * 2208);
-    d.k = *(const u4*)(rec + h * kHeadCodeBytes + c * kCodeRowBytes + g * 16);
-    d.v = *(const u4*)(rec + (int64_t)H * 1024 + h * kHeadCodeBytes + (g * 16 + c) * 16);
-    d.ks = *(const f4*)(rec + (int64_t)H * 2048 + h * 64 + g * 16);
-    d.vs = *(const f4*)(rec + (int64_t)H * 2112 + h * 64 + g * 16);
-    d.kz = rec[(int64_t)H * 2176 + h * 16 + c];
-    d.vz = *(const uint32_t*)(rec + (int64_t)H * 2192 + h * 16 + g * 4);
+    const int64_t rb = (int64_t)p.Hkv * kHeadPartBytes;
+    const uint8_t* part = (phys >= 0 ? p.pool + (int64_t)phys * rb : p.staging + (int64_t)(~phys) * rb) +
+                          RecordLayout::part(h);
+    d.k = *(const u4*)(part + kPartKc + c * kCodeRowBytes + g * 16);
+    d.v = *(const u4*)(part + kPartVc + (g * 16 + c) * 16);
+    d.ks = *(const f4*)(part + kPartKs + g * 16);
+    d.vs = *(const f4*)(part + kPartVs + g * 16);
+    d.kz = part[kPartKz + c];
+    d.vz = *(const uint32_t*)(part + kPartVz + g * 4);
 }
 
 // Block ids of logical blocks [lb0, lb0 + 64) of sequence b, one per lane, with

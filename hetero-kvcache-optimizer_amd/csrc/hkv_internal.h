@@ -47,17 +47,21 @@ constexpr int kBlockTokens = 16;
 constexpr int kCodeRowBytes = kHeadDim / 2;          // 64 B of packed codes per token row
 constexpr int kHeadCodeBytes = kBlockTokens * kCodeRowBytes;  // 1024 B per (block, head)
 
-// Block record offsets (bytes) for H kv heads; see heterokv.h.
+// Block record layout (bytes); see heterokv.h.  A record holds H head parts of
+// kHeadPartBytes each; inside a part: K codes, V codes, K scales, V scales, K zero
+// points, V zero points.
+constexpr int kHeadPartBytes = 2208;
+constexpr int kPartKc = 0, kPartVc = 1024, kPartKs = 2048, kPartVs = 2112, kPartKz = 2176, kPartVz = 2192;
 struct RecordLayout {
-    int64_t kc, vc, ks, vs, kz, vz, bytes;
-    __host__ __device__ explicit RecordLayout(int H)
-        : kc(0),
-          vc((int64_t)H * 1024),
-          ks((int64_t)H * 2048),
-          vs((int64_t)H * 2048 + (int64_t)H * 64),
-          kz((int64_t)H * 2048 + (int64_t)H * 128),
-          vz((int64_t)H * 2048 + (int64_t)H * 144),
-          bytes((int64_t)H * 2208) {}
+    int64_t bytes;
+    __host__ __device__ explicit RecordLayout(int H) : bytes((int64_t)H * kHeadPartBytes) {}
+    __host__ __device__ static int64_t part(int h) { return (int64_t)h * kHeadPartBytes; }
+    __host__ __device__ static int64_t kc(int h) { return part(h) + kPartKc; }
+    __host__ __device__ static int64_t vc(int h) { return part(h) + kPartVc; }
+    __host__ __device__ static int64_t ks(int h) { return part(h) + kPartKs; }
+    __host__ __device__ static int64_t vs(int h) { return part(h) + kPartVs; }
+    __host__ __device__ static int64_t kz(int h) { return part(h) + kPartKz; }
+    __host__ __device__ static int64_t vz(int h) { return part(h) + kPartVz; }
 };
 
 // ---------------------------------------------------------------- numeric helpers

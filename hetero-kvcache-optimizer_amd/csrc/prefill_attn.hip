@@ -111,25 +111,25 @@ __device__ __forceinline__ void stage_load(const PrefillParams& p, const TileMap
                 phys = p.fallback_id;
             }
         }
-        const int H = p.Hkv;
-        const uint8_t* rec = phys >= 0 ? p.pool + (int64_t)phys * ((int64_t)H * 2208)
-                                       : p.staging + (int64_t)(~phys) * ((int64_t)H * 2208);
+        const int64_t rb = (int64_t)p.Hkv * kHeadPartBytes;
+        const uint8_t* part = (phys >= 0 ? p.pool + (int64_t)phys * rb : p.staging + (int64_t)(~phys) * rb) +
+                              RecordLayout::part(h);
         const int rr = (t >> 2) & 15, pt = t & 3;
         const int tok0 = lb * kBlockTokens;
         s.valid = (lb < nb) ? min(kBlockTokens, tm.len4 - tok0) : 0;
         if (lb < nb) {
-            s.a[0] = *(const u4*)(rec + h * 1024 + rr * 64 + pt * 16);
-            s.ks = *(const float*)(rec + (int64_t)H * 2048 + h * 64 + rr * 4);
-            s.kz = rec[(int64_t)H * 2176 + h * 16 + rr];
+            s.a[0] = *(const u4*)(part + kPartKc + rr * 64 + pt * 16);
+            s.ks = *(const float*)(part + kPartKs + rr * 4);
+            s.kz = part[kPartKz + rr];
             // V: words (t%64)*4 .. +3 of this block: tokens 4g..4g+3, g = (t%64)/16
             const int g = (t & 63) >> 4;
-            s.b[0] = *(const u4*)(rec + (int64_t)H * 1024 + h * 1024 + (t & 63) * 16);
-            const float4 vs4 = *(const float4*)(rec + (int64_t)H * 2112 + h * 64 + g * 16);
+            s.b[0] = *(const u4*)(part + kPartVc + (t & 63) * 16);
+            const float4 vs4 = *(const float4*)(part + kPartVs + g * 16);
             s.vs[0] = vs4.x;
             s.vs[1] = vs4.y;
             s.vs[2] = vs4.z;
             s.vs[3] = vs4.w;
-            s.vz = *(const uint32_t*)(rec + (int64_t)H * 2192 + h * 16 + g * 4);
+            s.vz = *(const uint32_t*)(part + kPartVz + g * 4);
         }
         return;
     }

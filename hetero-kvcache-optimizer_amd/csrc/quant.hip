@@ -110,7 +110,7 @@ __device__ __forceinline__ void write_block_words(const uint8_t (&codes)[2][kBlo
             uint32_t w = 0;
 #pragma unroll
             for (int k = 0; k < 8; ++k) w |= (uint32_t)codes[0][r][8 * j + k] << nib_shift(k);
-            *(uint32_t*)(rec + L.kc + h * kHeadCodeBytes + r * kCodeRowBytes + j * 4) = w;
+            *(uint32_t*)(rec + L.kc(h) + r * kCodeRowBytes + j * 4) = w;
         }
     }
     // V word t = (g*16 + c)*4 + m: tokens 4g..4g+3, dims c+32m (x0..x3) and c+32m+16 (x4..x7).
@@ -127,7 +127,7 @@ __device__ __forceinline__ void write_block_words(const uint8_t (&codes)[2][kBlo
             }
         }
         if (mask) {
-            uint32_t* dst = (uint32_t*)(rec + L.vc + h * kHeadCodeBytes) + t;
+            uint32_t* dst = (uint32_t*)(rec + L.vc(h)) + t;
             if (mask != 0xFFFFFFFFu) w |= (*dst & ~mask);
             *dst = w;
         }
@@ -181,8 +181,8 @@ __global__ __launch_bounds__(256) void pack_tokens_kernel(PackParams p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) codes[kv][slot][part * 16 + i] = (uint8_t)quant_code(vals[i], q);
         if (part == 0) {
-            float* sc = (float*)(rec + (kv ? L.vs : L.ks)) + h * kBlockTokens + slot;
-            uint8_t* zp = rec + (kv ? L.vz : L.kz) + h * kBlockTokens + slot;
+            float* sc = (float*)(rec + (kv ? L.vs(h) : L.ks(h))) + slot;
+            uint8_t* zp = rec + (kv ? L.vz(h) : L.kz(h)) + slot;
             *sc = q.scale;
             *zp = q.zp;
         }
@@ -244,8 +244,8 @@ __global__ __launch_bounds__(256) void repack_codes_kernel(RepackParams p) {
             const float sc = (kv ? p.vs : p.ks)[mi];
             const void* zsrc = kv ? p.vz : p.kz;
             const uint8_t zp = p.zp_is_float ? (uint8_t)((const float*)zsrc)[mi] : ((const uint8_t*)zsrc)[mi];
-            ((float*)(rec + (kv ? L.vs : L.ks)))[h * kBlockTokens + slot] = sc;
-            (rec + (kv ? L.vz : L.kz))[h * kBlockTokens + slot] = zp;
+            ((float*)(rec + (kv ? L.vs(h) : L.ks(h))))[slot] = sc;
+            (rec + (kv ? L.vz(h) : L.kz(h)))[slot] = zp;
         }
     }
     __syncthreads();
@@ -270,19 +270,19 @@ __global__ __launch_bounds__(256) void unpack_tokens_kernel(
         const int s = tok % kBlockTokens;
         uint32_t code;
         if (which == 0) {
-            const uint32_t w = *(const uint32_t*)(rec + L.kc + h * kHeadCodeBytes + s * kCodeRowBytes + (d >> 3) * 4);
+            const uint32_t w = *(const uint32_t*)(rec + L.kc(h) + s * kCodeRowBytes + (d >> 3) * 4);
             code = (w >> nib_shift(d & 7)) & 0xFu;
         } else {
             const int g = s >> 2, ii = s & 3, c = d & 15, n = d >> 4;
             const int m = n >> 1, k = ii + (n & 1) * 4;
-            const uint32_t w = ((const uint32_t*)(rec + L.vc + h * kHeadCodeBytes))[(g * 16 + c) * 4 + m];
+            const uint32_t w = ((const uint32_t*)(rec + L.vc(h)))[(g * 16 + c) * 4 + m];
             code = (w >> nib_shift(k)) & 0xFu;
         }
         if (codes) codes[i] = (uint8_t)code;
         if (d == 0) {
             const int64_t gi = (int64_t)h * T + tok;
-            if (scales) scales[gi] = ((const float*)(rec + (which ? L.vs : L.ks)))[h * kBlockTokens + s];
-            if (zps) zps[gi] = (rec + (which ? L.vz : L.kz))[h * kBlockTokens + s];
+            if (scales) scales[gi] = ((const float*)(rec + (which ? L.vs(h) : L.ks(h))))[s];
+            if (zps) zps[gi] = (rec + (which ? L.vz(h) : L.kz(h)))[s];
         }
     }
 }

@@ -20,15 +20,17 @@
  *   AsyncPrefetcher (side-stream H2D)              src/policy/prefetcher.py:21-123
  *
  * INT4 block pool.  Tokens of the quantized middle zone live in 16-token
- * blocks.  One block record holds every kv head of those 16 tokens:
+ * blocks.  One block record holds every kv head of those 16 tokens as H
+ * contiguous 2208-byte head parts (part h at byte h*2208), so the reader of one
+ * kv head streams one contiguous run per block:
  *
- *   offset                     contents
- *   0                          K codes  [H][16 tokens][64 B]    (packed, see below)
- *   H*1024                     V codes  [H][1024 B]             (packed, transposed tiles)
- *   H*2048                     K scales [H][16] float32
- *   H*2048 + H*64              V scales [H][16] float32
- *   H*2048 + H*128             K zero points [H][16] uint8
- *   H*2048 + H*144             V zero points [H][16] uint8
+ *   offset in a head part      contents
+ *   0                          K codes  [16 tokens][64 B]       (packed, see below)
+ *   1024                       V codes  [1024 B]                (packed, transposed tiles)
+ *   2048                       K scales [16] float32
+ *   2112                       V scales [16] float32
+ *   2176                       K zero points [16] uint8
+ *   2192                       V zero points [16] uint8
  *   record size = H * 2208 bytes                                 (head_dim 128)
  *
  * A token's 128 values form one quantization group, exactly as the reference
@@ -40,7 +42,7 @@
  * x_k at bit (k%2)*16 + (k/2)*4, so (w >> 4i) & 0x000F000F yields the pair
  * (x_2i, x_2i+1) as two 16-bit lanes.
  *   K: word j of a token row (j=0..15) holds dims 8j..8j+7 as x0..x7.
- *   V: word (g*16+c)*4+m of a head's 1024 B holds, for tokens 4g..4g+3,
+ *   V: word (g*16+c)*4+m of a head part's 1024 B holds, for tokens 4g..4g+3,
  *      x0..x3 = dim c+32m and x4..x7 = dim c+32m+16   (g<4, c<16, m<4).
  *
  * Host tier.  A block-table entry id >= 0 names record `id` of `pool`; an entry

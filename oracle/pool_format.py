@@ -2,8 +2,8 @@
 from their specification in include/heterokv.h (TEST INFRASTRUCTURE ONLY, see
 oracle/__init__.py).  Used to check the HIP packer byte for byte.
 
-Block record (16 tokens, H kv heads, head_dim 128):
-  [K codes H*1024][V codes H*1024][K scales H*16 f32][V scales H*16 f32][K zps H*16][V zps H*16]
+Block record (16 tokens, H kv heads, head_dim 128): H contiguous 2208-byte head parts,
+part i at i*2208 = [K codes 1024][V codes 1024][K scales 16 f32][V scales 16 f32][K zps 16][V zps 16]
 Packed word: 8 codes x0..x7, x_k at bit (k%2)*16 + (k//2)*4.
   K: word j of a token row = dims 8j..8j+7.
   V: word (g*16+c)*4+m of a head = tokens 4g..4g+3 at dim c+32m (x0..x3) and c+32m+16 (x4..x7).
@@ -23,9 +23,13 @@ def record_bytes(h):
     return h * 2208
 
 
-def offsets(h):
-    return dict(kc=0, vc=h * 1024, ks=h * 2048, vs=h * 2048 + h * 64, kz=h * 2048 + h * 128,
-                vz=h * 2048 + h * 144)
+PART_BYTES = 2208
+PART = dict(kc=0, vc=1024, ks=2048, vs=2112, kz=2176, vz=2192)
+
+
+def offsets(i):
+    """Byte offsets of head i's K codes, V codes, K scales, V scales, K zps, V zps."""
+    return {k: i * PART_BYTES + v for k, v in PART.items()}
 
 
 def pack_k_rows(codes):
@@ -77,15 +81,19 @@ def unpack_v_block(packed):
 def build_record(kcodes, vcodes, kscales, vscales, kzps, vzps):
     """Per-head arrays for one block ([H,16,128] codes, [H,16] meta) -> record bytes."""
     h = kcodes.shape[0]
-    off = offsets(h)
     rec = np.zeros(record_bytes(h), dtype=np.uint8)
+    ks = np.asarray(kscales, dtype="<f4").reshape(h, 16)
+    vs = np.asarray(vscales, dtype="<f4").reshape(h, 16)
+    kz = np.asarray(kzps, dtype=np.uint8).reshape(h, 16)
+    vz = np.asarray(vzps, dtype=np.uint8).reshape(h, 16)
     for i in range(h):
-        rec[off["kc"] + i * 1024: off["kc"] + (i + 1) * 1024] = pack_k_rows(kcodes[i]).reshape(-1)
-        rec[off["vc"] + i * 1024: off["vc"] + (i + 1) * 1024] = pack_v_block(vcodes[i])
-    rec[off["ks"]: off["ks"] + h * 64] = np.asarray(kscales, dtype="<f4").reshape(-1).view(np.uint8)
-    rec[off["vs"]: off["vs"] + h * 64] = np.asarray(vscales, dtype="<f4").reshape(-1).view(np.uint8)
-    rec[off["kz"]: off["kz"] + h * 16] = np.asarray(kzps, dtype=np.uint8).reshape(-1)
-    rec[off["vz"]: off["vz"] + h * 16] = np.asarray(vzps, dtype=np.uint8).reshape(-1)
+        off = offsets(i)
+        rec[off["kc"]: off["kc"] + 1024] = pack_k_rows(kcodes[i]).reshape(-1)
+        rec[off["vc"]: off["vc"] + 1024] = pack_v_block(vcodes[i])
+        rec[off["ks"]: off["ks"] + 64] = ks[i].view(np.uint8)
+        rec[off["vs"]: off["vs"] + 64] = vs[i].view(np.uint8)
+        rec[off["kz"]: off["kz"] + 16] = kz[i]
+        rec[off["vz"]: off["vz"] + 16] = vz[i]
     return rec
 
 

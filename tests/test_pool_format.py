@@ -45,8 +45,26 @@ def test_round_trips_random():
 
 def test_record_offsets_and_size():
     assert pf.record_bytes(8) == 17664 and pf.record_bytes(4) == 8832
-    o = pf.offsets(8)
-    assert (o["vc"], o["ks"], o["vs"], o["kz"], o["vz"]) == (8192, 16384, 16896, 17408, 17536)
+    # head i's part starts at i * 2208; inside it K codes, V codes, K scales, V scales,
+    # K zps, V zps (1024 + 1024 + 64 + 64 + 16 + 16 bytes)
+    o = pf.offsets(0)
+    assert (o["kc"], o["vc"], o["ks"], o["vs"], o["kz"], o["vz"]) == (0, 1024, 2048, 2112, 2176, 2192)
+    o = pf.offsets(5)
+    assert (o["kc"], o["vz"]) == (11040, 11040 + 2192)
+    assert o["vz"] + 16 == pf.offsets(6)["kc"]
+
+
+def test_record_parts_are_contiguous_per_head():
+    rng = np.random.default_rng(3)
+    H = 3
+    kc = rng.integers(0, 16, (H, 16, 128), dtype=np.uint8)
+    vc = rng.integers(0, 16, (H, 16, 128), dtype=np.uint8)
+    ks, vs = rng.random((H, 16), dtype=np.float32), rng.random((H, 16), dtype=np.float32)
+    kz, vz = rng.integers(0, 16, (H, 16), dtype=np.uint8), rng.integers(0, 16, (H, 16), dtype=np.uint8)
+    rec = pf.build_record(kc, vc, ks, vs, kz, vz)
+    for i in range(H):
+        one = pf.build_record(kc[i:i + 1], vc[i:i + 1], ks[i:i + 1], vs[i:i + 1], kz[i:i + 1], vz[i:i + 1])
+        assert np.array_equal(rec[i * 2208:(i + 1) * 2208], one)
 
 
 def test_v_tile_layout():
