@@ -176,6 +176,81 @@ def bench_prefill(torch, ops, args):
     print(json.dumps(line), flush=True)
 
 
+def bench_paged(torch, ops, args):
+    """Batched paged decode: 16 sequences, contexts uniform in [8192, 32768] (seeded), 32 q / 8 kv
+    heads, each context = 64 fp16 sink + INT4 middle + 4096 fp16 recent; the INT4 middle lives in
+    16-token blocks of one pool addressed through a seeded random-permutation block table."""
+    dev = torch.device("cuda:0")
+    Bp = 16
+    gen = torch.Generator().manual_seed(7)
+    ctx = torch.randint(8192, 32769, (Bp,), generator=gen)
+    mids = (ctx - SINK - RECENT).tolist()
+    nbs = [(m + 15) // 16 for m in mids]
+    nbmax = max(nbs)
+    total = sum(nbs)
+    perm = torch.randperm(total, generator=gen).to(torch.int32)
+    bt = torch.zeros((Bp, nbmax), dtype=torch.int32)
+    off = 0
+    for b, nb in enumerate(nbs):
+        bt[b, :nb] = perm[off:off + nb]
+        off += nb
+    g = torch.Generator(device=dev).manual_seed(8)
+    pool = ops.Int4Pool(total, HKV, dev)
+    bt_d = bt.to(dev)
+    for b in range(Bp):
+        K = torch.randn((1, HKV, mids[b], D), generator=g, device=dev)
+        K[..., OUTLIERS] *= 8
+        V = torch.randn((1, HKV, mids[b], D), generator=g, device=dev)
+        ops.pack_tokens(pool, K.half(), V.half(), torch.zeros(1, dtype=torch.int32, device=dev), bt_d[b:b + 1])
+    pool.check_errors()
+    sink = ops.F16Zone(Bp, HKV, SINK, dev)
+    rec = ops.F16Zone(Bp, HKV, RECENT, dev)
+    sink.write(torch.randn((Bp, HKV, SINK, D), generator=g, device=dev).half(),
+               torch.randn((Bp, HKV, SINK, D), generator=g, device=dev).half(), 0)
+    rec.write(torch.randn((Bp, HKV, RECENT, D), generator=g, device=dev).half(),
+              torch.randn((Bp, HKV, RECENT, D), generator=g, device=dev).half(), 0)
+    q = (torch.randn((Bp, HQ, D), generator=g, device=dev) / math.sqrt(D)).half()
+    lens = torch.tensor(mids, dtype=torch.int32, device=dev)
+    out = torch.empty((Bp, HQ, D), dtype=torch.float16, device=dev)
+    ws = ops.DecodeWorkspace(dev)
+
+    def launch():
+        ops.decode_attention(q, zones=[(sink, None, SINK), (rec, None, RECENT)], pool=pool, block_table=bt_d,
+                             int4_lens=lens, int4_max_len=max(mids), workspace=ws, out=out)
+
+    for _ in range(max(args.warmup, 1)):
+        launch()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(args.steps):
+        launch()
+    ev1.record(stream)
+    ev1.synchronize()
+    if ws.error_flag():
+        raise RuntimeError("decode kernel reported an out-of-range block id")
+    ms = ev0.elapsed_time(ev1) / args.steps
+    step_bytes = sum(2 * HKV * (m * (D // 2 + 5) + (SINK + RECENT) * D * 2) for m in mids) + 2 * Bp * HQ * D * 2
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "INT4-KV batched paged decode-attn GB/s (HBM roofline fraction)",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic (seeded N(0,1) K/V, x8 K outlier channels)",
+        "config": {"workload": "batched paged decode: batch 16, contexts uniform in [8192, 32768] (64 fp16 sink + "
+                               "INT4 middle + 4096 fp16 recent), 32 q / 8 kv heads, head_dim 128, INT4 blocks via "
+                               "a random-permutation block table; %d pool blocks; one pool (fits the 256 MB "
+                               "Infinity Cache only partly)" % total,
+                   "contexts": ctx.tolist(), "bytes_per_step": step_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 T_LAYERS, T_HQ, T_HKV, T_HIDDEN, T_INTER, T_VOCAB = 28, 28, 4, 3584, 18944, 152064
 T_CTX, T_CHUNK, T_SINK, T_KEEP, T_HOST_FRAC = 131072, 2048, 64, 4160, 0.75
 
@@ -394,11 +469,12 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--workload", choices=["decode", "prefill", "tiered"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged"], default="decode",
                     help="decode: the headline single-layer decode (default); prefill: the chunked-prefill "
                          "kernel on a 2048-token chunk over 64 + 131072 INT4 + 4096 tokens (MFMA bound); "
                          "tiered: end-to-end 28-layer decode at 131072 tokens with 75%% of the INT4 KV in "
-                         "pinned host memory (use small --steps/--warmup, e.g. 8 / 2)")
+                         "pinned host memory (use small --steps/--warmup, e.g. 8 / 2); paged: batch-16 paged "
+                         "decode, contexts 8K-32K")
     ap.add_argument("--copy-calibration", type=float, default=0.0,
                     help="run only torch's device copy of this many MB (20 launches) so that rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
@@ -428,6 +504,8 @@ def main():
         return bench_prefill(torch, ops, args)
     if args.workload == "tiered":
         return bench_tiered(torch, args)
+    if args.workload == "paged":
+        return bench_paged(torch, ops, args)
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
