@@ -24,6 +24,7 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
+typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
@@ -255,6 +256,166 @@ __device__ __forceinline__ void stage_store(const Stage& s, uint8_t* lds) {
     }
 }
 
+// Compact staged data of one INT4 tile for one thread (the INT4 phase keeps kRing of
+// them in flight).  Each stage also carries the block id of the tile kRing further on,
+// so no load ever waits for a block id issued after other loads.
+struct Stage4 {
+    u4 k;         // K codes: token (t/4)%16 of block t/64, dims 32(t%4) .. +32
+    u4 v;         // V words (t%64)*4 .. +3 of block t/64
+    f4 vs;        // V scales of tokens 4g..4g+3, g = (t%64)/16
+    float ks;     // K scale of the K row
+    uint32_t kz;  // K zero point of the K row
+    uint32_t vz;  // V zero points of tokens 4g..4g+3 (bytes)
+    int valid;    // valid tokens of block t/64 (0 past the end)
+    int next_id;  // block id of this thread's block in tile + kRing
+};
+constexpr int kRing = 4;          // INT4 tiles in flight per thread
+
+// Block id of this thread's block (t/64) of INT4 tile x, clamped to the last block.
+__device__ __forceinline__ int block_id4(const PrefillParams& p, int nb, int b, int x) {
+    const int lb = min(x * 4 + (int)(threadIdx.x >> 6), nb - 1);
+    return p.bt[(int64_t)b * p.bt_stride + lb];
+}
+
+// Loads INT4 tile `tile` (past the end it re-reads the last block and carries no valid
+// token) from block id `id`, and the id of tile + kRing.
+__device__ __forceinline__ void load4(const PrefillParams& p, int n4, int len4, int b, int h, int tile, int id,
+                                      Stage4& s) {
+    const int t = threadIdx.x;
+    const int nb = (len4 + kBlockTokens - 1) / kBlockTokens;
+    int phys = id;
+    if (phys >= 0 ? (int64_t)phys >= p.pool_blocks : (int64_t)(~phys) >= p.staging_blocks) {
+        if (p.err) atomicOr(p.err, 1);
+        phys = p.fallback_id;
+    }
+    const int64_t rb = (int64_t)p.Hkv * kHeadPartBytes;
+    const uint8_t* part = (phys >= 0 ? p.pool + (int64_t)phys * rb : p.staging + (int64_t)(~phys) * rb) +
+                          RecordLayout::part(h);
+    const int rr = (t >> 2) & 15, pt = t & 3, g = (t & 63) >> 4;
+    const int lbt = tile * 4 + (t >> 6);
+    s.valid = (tile < n4 && lbt < nb) ? min(kBlockTokens, len4 - lbt * kBlockTokens) : 0;
+    s.k = *(const u4*)(part + kPartKc + rr * 64 + pt * 16);
+    s.ks = *(const float*)(part + kPartKs + rr * 4);
+    s.kz = part[kPartKz + rr];
+    s.v = *(const u4*)(part + kPartVc + (t & 63) * 16);
+    s.vs = *(const f4*)(part + kPartVs + g * 16);
+    s.vz = *(const uint32_t*)(part + kPartVz + g * 4);
+    s.next_id = block_id4(p, nb, b, min(tile + kRing, n4 - 1));
+}
+
+// Dequantizes a staged INT4 tile into LDS buffer `lds` (K rows + V^T), exactly as the
+// reference's fp16 dequantization; slots past the valid length become zeros.
+__device__ __forceinline__ void store4(const Stage4& s, uint8_t* lds) {
+    const int t = threadIdx.x;
+    const int blk = t >> 6, rr = (t >> 2) & 15, pt = t & 3;
+    const int tok = blk * 16 + rr;
+    const bool ok = rr < s.valid;
+    const float zf = (float)s.kz;
+    const uint32_t w4[4] = {s.k.x, s.k.y, s.k.z, s.k.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {          // word j: dims 32pt + 8j .. +8
+        uint32_t r[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t pr = (w4[j] >> (4 * i)) & 0x000F000Fu;
+            const float lo = ((float)(pr & 0xF) - zf) * s.ks;
+            const float hi = ((float)(pr >> 16) - zf) * s.ks;
+            r[i] = ok ? pack2(lo, hi) : 0u;
+        }
+        *(u4*)(lds + k_addr(tok, pt * 4 + j)) = u4{r[0], r[1], r[2], r[3]};
+    }
+    const int g = (t & 63) >> 4, c = t & 15;
+    float zf4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) zf4[i] = (float)((s.vz >> (8 * i)) & 0xFF);
+    const uint32_t v4[4] = {s.v.x, s.v.y, s.v.z, s.v.w};
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+        const uint32_t w = v4[mm];
+        // x_k at bit (k%2)*16 + (k/2)*4: x0..x3 = tokens 4g..4g+3 at dim c+32mm, x4..x7 at +16
+        float val[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int tk = k & 3;
+            const float code = (float)((w >> nib_shift(k)) & 0xFu);
+            val[k] = (4 * g + tk < s.valid) ? (code - zf4[tk]) * s.vs[tk] : 0.0f;
+        }
+        const int unit = blk * 4 + g;
+        const int d1 = c + 32 * mm, d2 = d1 + 16;
+        *(u2*)(lds + vt_addr(d1, unit)) = u2{pack2(val[0], val[1]), pack2(val[2], val[3])};
+        *(u2*)(lds + vt_addr(d2, unit)) = u2{pack2(val[4], val[5]), pack2(val[6], val[7])};
+    }
+}
+
+// One 64-token tile of attention for this wave's 32 query rows: S^T = K.Q^T, masked
+// online softmax, O^T += V^T.P^T.  `cur` holds the tile's K rows and V^T in LDS.
+__device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int causal_base, int n, int hh,
+                                            int qrow, const h8 (&qf)[8], float scale_log2, f16v (&acc)[4],
+                                            float& m, float& l) {
+    f16v S[2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) S[tb][r] = 0.f;
+        const int tok = tb * 32 + n;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const h8 a = __builtin_bit_cast(h8, *(const u4*)(cur + k_addr(tok, 2 * s + hh)));
+            S[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], S[tb], 0, 0, 0);
+        }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int tok = tb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+            bool ok = tok < tvalid;
+            if (causal_base >= 0) ok = ok && (causal_base + tok <= qrow);
+            const float sv = ok ? S[tb][r] * scale_log2 : -INFINITY;
+            S[tb][r] = sv;
+            mt = fmaxf(mt, sv);
+        }
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    if (__ballot(mt > m)) {
+        const float m_new = fmaxf(m, mt);
+        const float alpha = (m_new > m) ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+        l *= alpha;
+        m = m_new;
+    }
+    const float msafe = (m == -INFINITY) ? 0.f : m;
+    h8 P[2][2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * (2 * u + jj) + i;
+                    const float pv = __builtin_amdgcn_exp2f(S[tb][r] - msafe);
+                    l += pv;
+                    P[tb][u][jj * 4 + i] = (_Float16)pv;
+                }
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int unit0 = tb * 8 + 4 * u + hh;      // tokens tb*32 + 16u + 4hh (+8 for jj=1)
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const int dim = 32 * db + n;
+                const u2 lo = *(const u2*)(cur + vt_addr(dim, unit0));
+                const u2 hi = *(const u2*)(cur + vt_addr(dim, unit0 + 2));
+                const h8 a = __builtin_bit_cast(h8, u4{lo.x, lo.y, hi.x, hi.y});
+                acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, P[tb][u], acc[db], 0, 0, 0);
+            }
+        }
+}
+
 __global__ __launch_bounds__(kThreadsP) void prefill_attn_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     const int b = blockIdx.z;
@@ -302,110 +463,81 @@ __global__ __launch_bounds__(kThreadsP) void prefill_attn_kernel(PrefillParams p
         for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
     float m = -INFINITY, l = 0.f;
 
+    // ---- INT4 tiles: kRing staged tiles in flight; tile t is computed from LDS buffer
+    // t % 2 while tile t + 1 is dequantized into the other buffer.  The tile count is
+    // padded to a multiple of kRing (padding tiles carry no valid token) so the ring
+    // slots stay compile-time registers.
+    const int n4 = tm.n4;
+    const int n4p = n4 > 0 ? (n4 + kRing - 1) / kRing * kRing : 0;
+    if (n4 > 0) {
+        Stage4 ring[kRing];
+        const int nb4 = (tm.len4 + kBlockTokens - 1) / kBlockTokens;
+        int id0[kRing];
+#pragma unroll
+        for (int u = 0; u < kRing; ++u) id0[u] = block_id4(p, nb4, b, min(u, n4 - 1));
+#pragma unroll
+        for (int u = 0; u < kRing - 1; ++u) {
+            __builtin_amdgcn_sched_barrier(0);
+            load4(p, n4, tm.len4, b, h, u, id0[u], ring[u]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        ring[kRing - 1].next_id = id0[kRing - 1];
+        store4(ring[0], lds_raw);
+        __syncthreads();
+        for (int t0 = 0; t0 < n4p; t0 += kRing) {
+#pragma unroll
+            for (int u = 0; u < kRing; ++u) {
+                const int tile = t0 + u;
+                __builtin_amdgcn_sched_barrier(0);
+                Stage4& slot = ring[(u + kRing - 1) % kRing];
+                load4(p, n4, tm.len4, b, h, tile + kRing - 1, slot.next_id, slot);
+                __builtin_amdgcn_sched_barrier(0);
+                const int tvalid = min(kT, tm.len4 - tile * kT);
+                attend_tile(lds_raw + (tile & 1) * (2 * kTileBytes), tvalid, -1, n, hh, qrow, qf, p.scale_log2,
+                            acc, m, l);
+                store4(ring[(u + 1) % kRing], lds_raw + ((tile + 1) & 1) * (2 * kTileBytes));
+                __syncthreads();
+            }
+        }
+    }
+
+    // ---- fp16 zone tiles and the causal chunk: one staged tile in flight
     Stage st;
-    if (ntiles > 0) {
-        stage_load(p, tm, b, h, 0, st);
-        stage_store(st, lds_raw);
+    const int par0 = n4p;   // LDS buffer parity continues after the INT4 tiles
+    if (ntiles > n4) {
+        stage_load(p, tm, b, h, n4, st);
+        stage_store(st, lds_raw + (par0 & 1) * (2 * kTileBytes));
     }
     __syncthreads();
-    for (int tile = 0; tile < ntiles; ++tile) {
-        uint8_t* cur = lds_raw + (tile & 1) * (2 * kTileBytes);
-        uint8_t* nxt = lds_raw + ((tile + 1) & 1) * (2 * kTileBytes);
+    for (int tile = n4; tile < ntiles; ++tile) {
+        const int par = par0 + (tile - n4);
+        uint8_t* cur = lds_raw + (par & 1) * (2 * kTileBytes);
+        uint8_t* nxt = lds_raw + ((par + 1) & 1) * (2 * kTileBytes);
         if (tile + 1 < ntiles) stage_load(p, tm, b, h, tile + 1, st);
 
         // valid tokens of this tile and causal limit
         int tvalid = kT;
         int causal_base = -1;  // chunk position of token 0 of this tile, or -1
         {
-            int x = tile;
-            if (x < tm.n4) {
-                tvalid = min(kT, tm.len4 - x * kT);
-            } else {
-                x -= tm.n4;
-                bool found = false;
+            int x = tile - tm.n4;
+            bool found = false;
 #pragma unroll
-                for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
-                    if (!found && zi < p.nz) {
-                        if (x < tm.nz_t[zi]) {
-                            tvalid = min(kT, tm.lenz[zi] - x * kT);
-                            found = true;
-                        } else {
-                            x -= tm.nz_t[zi];
-                        }
+            for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
+                if (!found && zi < p.nz) {
+                    if (x < tm.nz_t[zi]) {
+                        tvalid = min(kT, tm.lenz[zi] - x * kT);
+                        found = true;
+                    } else {
+                        x -= tm.nz_t[zi];
                     }
                 }
-                if (!found) {
-                    tvalid = min(kT, p.Sq - x * kT);
-                    causal_base = x * kT;
-                }
+            }
+            if (!found) {
+                tvalid = min(kT, p.Sq - x * kT);
+                causal_base = x * kT;
             }
         }
-
-        // ---- S^T = K . Q^T for two 32-token blocks
-        f16v S[2];
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) S[tb][r] = 0.f;
-            const int tok = tb * 32 + n;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const h8 a = __builtin_bit_cast(h8, *(const u4*)(cur + k_addr(tok, 2 * s + hh)));
-                S[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], S[tb], 0, 0, 0);
-            }
-        }
-        // ---- scores, mask, online softmax (per query = per lane column n)
-        float mt = -INFINITY;
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int tok = tb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                bool ok = tok < tvalid;
-                if (causal_base >= 0) ok = ok && (causal_base + tok <= qrow);
-                const float sv = ok ? S[tb][r] * p.scale_log2 : -INFINITY;
-                S[tb][r] = sv;
-                mt = fmaxf(mt, sv);
-            }
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        if (__ballot(mt > m)) {
-            const float m_new = fmaxf(m, mt);
-            const float alpha = (m_new > m) ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-            l *= alpha;
-            m = m_new;
-        }
-        const float msafe = (m == -INFINITY) ? 0.f : m;
-        h8 P[2][2];
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-#pragma unroll
-                for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int r = 4 * (2 * u + jj) + i;
-                        const float pv = __builtin_amdgcn_exp2f(S[tb][r] - msafe);
-                        l += pv;
-                        P[tb][u][jj * 4 + i] = (_Float16)pv;
-                    }
-        // ---- O^T += V^T . P^T (4 dim blocks x 4 token steps)
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int unit0 = tb * 8 + 4 * u + hh;      // tokens tb*32 + 16u + 4hh (+8 for jj=1)
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const int dim = 32 * db + n;
-                    const u2 lo = *(const u2*)(cur + vt_addr(dim, unit0));
-                    const u2 hi = *(const u2*)(cur + vt_addr(dim, unit0 + 2));
-                    const h8 a = __builtin_bit_cast(h8, u4{lo.x, lo.y, hi.x, hi.y});
-                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, P[tb][u], acc[db], 0, 0, 0);
-                }
-            }
+        attend_tile(cur, tvalid, causal_base, n, hh, qrow, qf, p.scale_log2, acc, m, l);
         if (tile + 1 < ntiles) stage_store(st, nxt);
         __syncthreads();
     }
