@@ -118,10 +118,36 @@ __device__ __forceinline__ f4 ld_l2_f4(__amdgpu_buffer_rsrc_t r, int byte_off) {
 
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 
-// (w >> 4i) & 0x000F000F | 0x6400_6400  ->  fp16 pair (1024 + x_2i, 1024 + x_2i+1)
-__device__ __forceinline__ uint32_t nib_pair(uint32_t w, int i) {
-    return ((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+// (a & m) | c in one VALU instruction (the compiler splits it when m, c are literals).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "s"(c));   // one scalar operand per VOP3
+    return r;
 }
+
+// The eight codes x0..x7 of a packed word as exact fp16 (code - zero point) pairs.
+// (w & 0x000F000F) | 0x6400_6400 is the fp16 pair (1024 + x0, 1024 + x1); the pair at
+// bits 4..7 / 20..23 gives (1024 + 16 x2, 1024 + 16 x3), which one fma with 1/16 maps
+// to (64 + x2, 64 + x3); w >> 8 repeats this for x4..x7.  z1024 holds 1024 + zp of the
+// pairs (x0,x1) and (x4,x5), z64 holds 64 + zp of (x2,x3) and (x6,x7).  Every value is
+// an integer below 2048, so all of it is exact in fp16.
+struct NibPairs {
+    h2 p0, p1, p2, p3;   // (x0,x1), (x2,x3), (x4,x5), (x6,x7) minus their zero points
+};
+__device__ __forceinline__ NibPairs unpack_word(uint32_t w, h2 z1024, h2 z64) {
+    const uint32_t m0 = 0x000F000Fu, m1 = 0x00F000F0u, c = 0x64006400u;
+    const h2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const uint32_t w8 = w >> 8;
+    NibPairs r;
+    r.p0 = __builtin_bit_cast(h2, and_or(w, m0, c)) - z1024;
+    r.p1 = __builtin_elementwise_fma(__builtin_bit_cast(h2, and_or(w, m1, c)), s16, -z64);
+    r.p2 = __builtin_bit_cast(h2, and_or(w8, m0, c)) - z1024;
+    r.p3 = __builtin_elementwise_fma(__builtin_bit_cast(h2, and_or(w8, m1, c)), s16, -z64);
+    return r;
+}
+// fp16 pairs (1024 + a, 1024 + b) and (64 + a, 64 + b) of two zero points a, b <= 15
+__device__ __forceinline__ h2 zp1024(uint32_t a, uint32_t b) { return __builtin_bit_cast(h2, 0x64006400u | a | (b << 16)); }
+__device__ __forceinline__ h2 zp64(uint32_t a, uint32_t b) { return __builtin_bit_cast(h2, 0x54005400u | (a << 4) | (b << 20)); }
 
 struct Int4Blk {
     u4 k;         // K codes of token (lane%16), dims 32g..32g+31
@@ -206,12 +232,9 @@ __device__ __forceinline__ void softmax_update(const float (&s)[N], f4 (&acc)[8]
 }
 
 // K operand of one packed word (dims 8j..8j+7 of token lane%16): exact code - zp.
-__device__ __forceinline__ h8 k_operand(uint32_t w, h2 kz2) {
-    const h2 a0 = as_h2(nib_pair(w, 0)) - kz2;
-    const h2 a1 = as_h2(nib_pair(w, 1)) - kz2;
-    const h2 a2 = as_h2(nib_pair(w, 2)) - kz2;
-    const h2 a3 = as_h2(nib_pair(w, 3)) - kz2;
-    return h8{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+__device__ __forceinline__ h8 k_operand(uint32_t w, h2 kz1024, h2 kz64) {
+    const NibPairs a = unpack_word(w, kz1024, kz64);
+    return h8{a.p0[0], a.p0[1], a.p1[0], a.p1[1], a.p2[0], a.p2[1], a.p3[0], a.p3[1]};
 }
 
 // Two INT4 blocks (32 tokens) per step: the two QK chains interleave, and one
@@ -220,15 +243,15 @@ __device__ __forceinline__ h8 k_operand(uint32_t w, h2 kz2) {
 __device__ __forceinline__ void step_int4_pair(const Int4Blk& A, const Int4Blk& B, int nA, int nB, int g,
                                                const h8 (&qf)[4], float scale_log2, f4 (&acc)[8], float& m,
                                                float& l) {
-    const _Float16 kzA = (_Float16)(1024.0f + (float)A.kz), kzB = (_Float16)(1024.0f + (float)B.kz);
-    const h2 kA2 = {kzA, kzA}, kB2 = {kzB, kzB};
+    const h2 kA1024 = zp1024(A.kz, A.kz), kA64 = zp64(A.kz, A.kz);
+    const h2 kB1024 = zp1024(B.kz, B.kz), kB64 = zp64(B.kz, B.kz);
     const uint32_t kwA[4] = {A.k.x, A.k.y, A.k.z, A.k.w};
     const uint32_t kwB[4] = {B.k.x, B.k.y, B.k.z, B.k.w};
     f4 SA = {0.f, 0.f, 0.f, 0.f}, SB = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        SA = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand(kwA[j], kA2), qf[j], SA, 0, 0, 0);
-        SB = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand(kwB[j], kB2), qf[j], SB, 0, 0, 0);
+        SA = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand(kwA[j], kA1024, kA64), qf[j], SA, 0, 0, 0);
+        SB = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand(kwB[j], kB1024, kB64), qf[j], SB, 0, 0, 0);
     }
     float s[8];
     const bool full = nA >= kBlockTokens && nB >= kBlockTokens;
@@ -262,20 +285,18 @@ __device__ __forceinline__ void step_int4_pair(const Int4Blk& A, const Int4Blk& 
             P[4 + v] = (_Float16)((4 * g + v < nB) ? pr[4 + v] * B.vs[v] : 0.0f);
         }
     }
-    const h2 zA01 = {(_Float16)(1024.0f + (float)(A.vz & 0xff)), (_Float16)(1024.0f + (float)((A.vz >> 8) & 0xff))};
-    const h2 zA23 = {(_Float16)(1024.0f + (float)((A.vz >> 16) & 0xff)), (_Float16)(1024.0f + (float)(A.vz >> 24))};
-    const h2 zB01 = {(_Float16)(1024.0f + (float)(B.vz & 0xff)), (_Float16)(1024.0f + (float)((B.vz >> 8) & 0xff))};
-    const h2 zB23 = {(_Float16)(1024.0f + (float)((B.vz >> 16) & 0xff)), (_Float16)(1024.0f + (float)(B.vz >> 24))};
+    // V zero points of tokens 4g..4g+3: pairs (x0,x1), (x4,x5) are tokens 4g, 4g+1;
+    // pairs (x2,x3), (x6,x7) are tokens 4g+2, 4g+3
+    const h2 zA01 = zp1024(A.vz & 0xffu, (A.vz >> 8) & 0xffu), zA23 = zp64((A.vz >> 16) & 0xffu, A.vz >> 24);
+    const h2 zB01 = zp1024(B.vz & 0xffu, (B.vz >> 8) & 0xffu), zB23 = zp64((B.vz >> 16) & 0xffu, B.vz >> 24);
     const uint32_t vwA[4] = {A.v.x, A.v.y, A.v.z, A.v.w};
     const uint32_t vwB[4] = {B.v.x, B.v.y, B.v.z, B.v.w};
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
-        const h2 a0 = as_h2(nib_pair(vwA[mm], 0)) - zA01, a1 = as_h2(nib_pair(vwA[mm], 1)) - zA23;
-        const h2 a2 = as_h2(nib_pair(vwA[mm], 2)) - zA01, a3 = as_h2(nib_pair(vwA[mm], 3)) - zA23;
-        const h2 b0 = as_h2(nib_pair(vwB[mm], 0)) - zB01, b1 = as_h2(nib_pair(vwB[mm], 1)) - zB23;
-        const h2 b2 = as_h2(nib_pair(vwB[mm], 2)) - zB01, b3 = as_h2(nib_pair(vwB[mm], 3)) - zB23;
-        const h8 V0 = {a0[0], a0[1], a1[0], a1[1], b0[0], b0[1], b1[0], b1[1]};   // dims c + 32mm
-        const h8 V1 = {a2[0], a2[1], a3[0], a3[1], b2[0], b2[1], b3[0], b3[1]};   // dims c + 32mm + 16
+        const NibPairs a = unpack_word(vwA[mm], zA01, zA23);
+        const NibPairs bq = unpack_word(vwB[mm], zB01, zB23);
+        const h8 V0 = {a.p0[0], a.p0[1], a.p1[0], a.p1[1], bq.p0[0], bq.p0[1], bq.p1[0], bq.p1[1]};   // dims c + 32mm
+        const h8 V1 = {a.p2[0], a.p2[1], a.p3[0], a.p3[1], bq.p2[0], bq.p2[1], bq.p3[0], bq.p3[1]};   // dims c + 32mm + 16
         acc[2 * mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(V0, P, acc[2 * mm], 0, 0, 0);
         acc[2 * mm + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(V1, P, acc[2 * mm + 1], 0, 0, 0);
     }
