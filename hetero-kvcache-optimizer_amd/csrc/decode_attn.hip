@@ -253,6 +253,21 @@ __device__ __forceinline__ void step_int4_pair(const Int4Blk& A, const Int4Blk& 
         SA = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand(kwA[j], kA1024, kA64), qf[j], SA, 0, 0, 0);
         SB = __builtin_amdgcn_mfma_f32_16x16x32_f16(k_operand(kwB[j], kB1024, kB64), qf[j], SB, 0, 0, 0);
     }
+    // V operands are unpacked while the QK products are in flight (they do not depend
+    // on the scores).  V zero points of tokens 4g..4g+3: pairs (x0,x1), (x4,x5) are
+    // tokens 4g, 4g+1; pairs (x2,x3), (x6,x7) are tokens 4g+2, 4g+3.
+    const h2 zA01 = zp1024(A.vz & 0xffu, (A.vz >> 8) & 0xffu), zA23 = zp64((A.vz >> 16) & 0xffu, A.vz >> 24);
+    const h2 zB01 = zp1024(B.vz & 0xffu, (B.vz >> 8) & 0xffu), zB23 = zp64((B.vz >> 16) & 0xffu, B.vz >> 24);
+    const uint32_t vwA[4] = {A.v.x, A.v.y, A.v.z, A.v.w};
+    const uint32_t vwB[4] = {B.v.x, B.v.y, B.v.z, B.v.w};
+    h8 V0[4], V1[4];
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+        const NibPairs a = unpack_word(vwA[mm], zA01, zA23);
+        const NibPairs bq = unpack_word(vwB[mm], zB01, zB23);
+        V0[mm] = h8{a.p0[0], a.p0[1], a.p1[0], a.p1[1], bq.p0[0], bq.p0[1], bq.p1[0], bq.p1[1]};   // dims c + 32mm
+        V1[mm] = h8{a.p2[0], a.p2[1], a.p3[0], a.p3[1], bq.p2[0], bq.p2[1], bq.p3[0], bq.p3[1]};   // dims c + 32mm + 16
+    }
     float s[8];
     const bool full = nA >= kBlockTokens && nB >= kBlockTokens;
     if (full) {
@@ -285,20 +300,10 @@ __device__ __forceinline__ void step_int4_pair(const Int4Blk& A, const Int4Blk& 
             P[4 + v] = (_Float16)((4 * g + v < nB) ? pr[4 + v] * B.vs[v] : 0.0f);
         }
     }
-    // V zero points of tokens 4g..4g+3: pairs (x0,x1), (x4,x5) are tokens 4g, 4g+1;
-    // pairs (x2,x3), (x6,x7) are tokens 4g+2, 4g+3
-    const h2 zA01 = zp1024(A.vz & 0xffu, (A.vz >> 8) & 0xffu), zA23 = zp64((A.vz >> 16) & 0xffu, A.vz >> 24);
-    const h2 zB01 = zp1024(B.vz & 0xffu, (B.vz >> 8) & 0xffu), zB23 = zp64((B.vz >> 16) & 0xffu, B.vz >> 24);
-    const uint32_t vwA[4] = {A.v.x, A.v.y, A.v.z, A.v.w};
-    const uint32_t vwB[4] = {B.v.x, B.v.y, B.v.z, B.v.w};
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
-        const NibPairs a = unpack_word(vwA[mm], zA01, zA23);
-        const NibPairs bq = unpack_word(vwB[mm], zB01, zB23);
-        const h8 V0 = {a.p0[0], a.p0[1], a.p1[0], a.p1[1], bq.p0[0], bq.p0[1], bq.p1[0], bq.p1[1]};   // dims c + 32mm
-        const h8 V1 = {a.p2[0], a.p2[1], a.p3[0], a.p3[1], bq.p2[0], bq.p2[1], bq.p3[0], bq.p3[1]};   // dims c + 32mm + 16
-        acc[2 * mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(V0, P, acc[2 * mm], 0, 0, 0);
-        acc[2 * mm + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(V1, P, acc[2 * mm + 1], 0, 0, 0);
+        acc[2 * mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(V0[mm], P, acc[2 * mm], 0, 0, 0);
+        acc[2 * mm + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(V1[mm], P, acc[2 * mm + 1], 0, 0, 0);
     }
 }
 
