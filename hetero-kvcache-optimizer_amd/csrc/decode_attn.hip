@@ -517,7 +517,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
             const float mw = sm_m[w * 16 + hd];
-            const float e = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+            const float e = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
             O += sm_o[(w * nrep + hd) * kHeadDim + d] * e;
             L += sm_l[w * 16 + hd] * e;
         }
@@ -589,14 +589,23 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                     os[j] = f4{ld_agent(ps + d4), ld_agent(ps + d4 + 1), ld_agent(ps + d4 + 2), ld_agent(ps + d4 + 3)};
                 }
             }
+            // the eight states merge with independent terms against their common max
+            float Mc = ms[0];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                if (ms[j] == -INFINITY) continue;
-                const float Mn = fmaxf(M, ms[j]);
-                const float a = (M == -INFINITY) ? 0.f : exp2f(M - Mn);
-                const float e = exp2f(ms[j] - Mn);
-                O = O * a + os[j] * e;
-                L = L * a + ls[j] * e;
+            for (int j = 1; j < 8; ++j) Mc = fmaxf(Mc, ms[j]);
+            if (Mc > -INFINITY) {
+                const float Mn = fmaxf(M, Mc);
+                const float a = (M == -INFINITY) ? 0.f : fast_exp2(M - Mn);
+                f4 Oc = {0.f, 0.f, 0.f, 0.f};
+                float Lc = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float e = (ms[j] == -INFINITY) ? 0.f : fast_exp2(ms[j] - Mn);
+                    Oc += os[j] * e;
+                    Lc += ls[j] * e;
+                }
+                O = O * a + Oc;
+                L = L * a + Lc;
                 M = Mn;
             }
         }
@@ -619,7 +628,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         for (int k = 0; k < K; ++k) {
             const float* w = sm + (k * units + u) * 6;
             if (w[0] == -INFINITY) continue;
-            const float e = exp2f(w[0] - M);
+            const float e = fast_exp2(w[0] - M);
             L += w[1] * e;
             O += f4{w[2], w[3], w[4], w[5]} * e;
         }
