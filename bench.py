@@ -216,7 +216,8 @@ def bench_paged(torch, ops, args):
 
     def launch():
         ops.decode_attention(q, zones=[(sink, None, SINK), (rec, None, RECENT)], pool=pool, block_table=bt_d,
-                             int4_lens=lens, int4_max_len=max(mids), workspace=ws, out=out)
+                             int4_lens=lens, int4_max_len=max(mids), workspace=ws, out=out,
+                             deterministic=args.deterministic)
 
     for _ in range(max(args.warmup, 1)):
         launch()
@@ -243,7 +244,8 @@ def bench_paged(torch, ops, args):
                                "INT4 middle + 4096 fp16 recent), 32 q / 8 kv heads, head_dim 128, INT4 blocks via "
                                "a random-permutation block table; %d pool blocks; one pool (fits the 256 MB "
                                "Infinity Cache only partly)" % total,
-                   "contexts": ctx.tolist(), "bytes_per_step": step_bytes},
+                   "contexts": ctx.tolist(), "bytes_per_step": step_bytes,
+                   "schedule": "fixed (deterministic)" if args.deterministic else "on demand"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": None,
@@ -467,6 +469,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--deterministic", action="store_true",
+                    help="decode with the fixed block-to-wave schedule (bitwise reproducible)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged"], default="decode",
@@ -519,7 +523,7 @@ def main():
     def launch(i):
         c = copies[i % R]
         ops.decode_attention(q_dev, zones=c["zones"], pool=c["pool"], block_table=c["bt"],
-                             int4_max_len=MID, workspace=ws, out=out)
+                             int4_max_len=MID, workspace=ws, out=out, deterministic=args.deterministic)
 
     for i in range(max(R, 8)):
         launch(i)
@@ -599,6 +603,7 @@ def main():
                    "batch": B, "context": CTX, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
                    "int4_tokens": MID, "fp16_tokens": SINK + RECENT, "kv_copies_rotated": R,
                    "launch": "eager" if args.no_graph else "hip graph replay",
+                   "schedule": "fixed (deterministic)" if args.deterministic else "on demand",
                    "bytes_per_step": STEP_BYTES},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),

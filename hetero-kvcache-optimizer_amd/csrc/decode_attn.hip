@@ -55,10 +55,17 @@ constexpr int kPartStride = kHeadDim + 4;  // o[128], m, l, 2 pad (16-byte rows)
 #endif
 constexpr int kPrefetch = HKV_DECODE_PREFETCH;  // INT4 block pairs in flight per wave
 constexpr int kMaxSplits = 64;
+constexpr int kIdWindow = 1024;           // INT4 block ids staged in LDS at a time
+constexpr int kIdPerThread = kIdWindow / kThreads;
+static_assert(kIdWindow % kThreads == 0, "whole id entries per thread");
 constexpr float kLog2e = 1.4426950408889634f;
 // Bytes one kv head reads per item (the weights that balance the ranges).
 constexpr int64_t kInt4ItemBytes = kBlockTokens * (kHeadDim / 2 + 5) * 2;   // 2208
 constexpr int64_t kF16ItemBytes = kBlockTokens * kHeadDim * 2 * 2;           // 8192
+#ifndef HKV_INT4_COST
+#define HKV_INT4_COST 2560
+#endif
+constexpr int64_t kInt4Cost = HKV_INT4_COST;   // balance weight of an INT4 block against an fp16 tile
 
 struct ZoneP {
     const uint16_t* k;
@@ -154,7 +161,7 @@ struct Int4Blk {
     u4 v;         // V codes: tokens 4g..4g+3, dims c+16n (n=0..7)
     f4 ks;        // K scales of tokens 4g..4g+3
     f4 vs;        // V scales of tokens 4g..4g+3
-    uint32_t kz;  // K zero point of token (lane%16)
+    uint32_t kz;  // K zero points of tokens 4(c/4)..+3 (bytes); token c's is byte c%4
     uint32_t vz;  // V zero points of tokens 4g..4g+3 (bytes)
 };
 
@@ -163,41 +170,86 @@ struct F16Tile {
     u4 v[4];      // V^T tile: halves [n][i] for tokens 4g+i, dims c+16n
 };
 
+// Loads go through a buffer resource per block whose size is 0 for a slot with
+// nothing to read: such a load returns zeros without a memory access, so the
+// refills issued past the end of a range cost no traffic and no wait.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ u4 ld16(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t ld4(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
 // `phys` is the (already validated, wave-uniform) block id: >= 0 a pool record,
 // < 0 staging record ~phys.  Every load of a block is issued back to back so
 // several blocks stay in flight.
-__device__ __forceinline__ void load_int4(const DecodeParams& p, int h, int phys, int c, int g, Int4Blk& d) {
+__device__ __forceinline__ void load_int4(const DecodeParams& p, int h, int phys, bool valid, int c, int g,
+                                          Int4Blk& d) {
     const int64_t rb = (int64_t)p.Hkv * kHeadPartBytes;
     const uint8_t* part = (phys >= 0 ? p.pool + (int64_t)phys * rb : p.staging + (int64_t)(~phys) * rb) +
                           RecordLayout::part(h);
-    d.k = *(const u4*)(part + kPartKc + c * kCodeRowBytes + g * 16);
-    d.v = *(const u4*)(part + kPartVc + (g * 16 + c) * 16);
-    d.ks = *(const f4*)(part + kPartKs + g * 16);
-    d.vs = *(const f4*)(part + kPartVs + g * 16);
-    d.kz = part[kPartKz + c];
-    d.vz = *(const uint32_t*)(part + kPartVz + g * 4);
+    const __amdgpu_buffer_rsrc_t r = rsrc(part, valid ? kHeadPartBytes : 0);
+    d.k = ld16(r, kPartKc + c * kCodeRowBytes + g * 16);
+    d.v = ld16(r, kPartVc + (g * 16 + c) * 16);
+    d.ks = __builtin_bit_cast(f4, ld16(r, kPartKs + g * 16));
+    d.vs = __builtin_bit_cast(f4, ld16(r, kPartVs + g * 16));
+    d.kz = ld4(r, kPartKz + (c & ~3));   // a full word: no byte value lives across the loop
+    d.vz = ld4(r, kPartVz + g * 4);
 }
 
-// Block ids of logical blocks [lb0, lb0 + 64) of sequence b, one per lane, with
-// out-of-range ids replaced by a valid one and reported once through p.err.
-__device__ __forceinline__ int load_block_ids(const DecodeParams& p, int b, int lb0, int lb1, int lane) {
-    int id = p.fallback_id;
-    if (lb0 + lane < lb1) id = p.bt[(int64_t)b * p.bt_stride + lb0 + lane];
-    const bool bad = (lb0 + lane < lb1) &&
-                     (id >= 0 ? (int64_t)id >= p.pool_blocks : (int64_t)(~id) >= p.staging_blocks);
-    if (bad) id = p.fallback_id;
-    if (__ballot(bad) && lane == 0 && p.err) atomicOr(p.err, 1);
-    return id;
+// Block ids of logical blocks [lb0, lb0 + n) of sequence b, padded to an even
+// count by repeating the last one: thread t requests entries t, t + kThreads.
+__device__ __forceinline__ void fetch_block_ids(const DecodeParams& p, int b, int lb0, int n, int (&r)[kIdPerThread]) {
+    const int n2 = (n + 1) & ~1;
+#pragma unroll
+    for (int j = 0; j < kIdPerThread; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        r[j] = i < n2 ? p.bt[(int64_t)b * p.bt_stride + lb0 + min(i, n - 1)] : 0;
+    }
 }
 
-__device__ __forceinline__ void load_f16(const ZoneP& z, int64_t bh, int tile, int c, int g, F16Tile& d) {
-    const uint16_t* kp = z.k + ((bh * z.cap + (int64_t)tile * kBlockTokens + c) * kHeadDim) + 32 * g;
-    const uint16_t* vp = z.v + (bh * (z.cap / kBlockTokens) + tile) * (kBlockTokens * kHeadDim) +
-                         (g * 16 + c) * 32;
+// Writes the fetched ids to LDS, with out-of-range ids replaced by a valid one and
+// reported through p.err.
+__device__ __forceinline__ void commit_block_ids(const DecodeParams& p, int n, const int (&r)[kIdPerThread], int* sm) {
+    const int n2 = (n + 1) & ~1;
+    bool bad_any = false;
+#pragma unroll
+    for (int j = 0; j < kIdPerThread; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        if (i < n2) {
+            int id = r[j];
+            const bool bad = id >= 0 ? (int64_t)id >= p.pool_blocks : (int64_t)(~id) >= p.staging_blocks;
+            if (bad) {
+                id = p.fallback_id;
+                bad_any = true;
+            }
+            sm[i] = id;
+        }
+    }
+    if (__ballot(bad_any) && (threadIdx.x & 63) == 0 && p.err) atomicOr(p.err, 1);
+}
+
+// Next unit of a workgroup counter, wave-uniform.
+__device__ __forceinline__ int grab(int* ctr) {
+    int v = 0;
+    if ((threadIdx.x & 63) == 0) v = atomicAdd(ctr, 1);
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
+__device__ __forceinline__ u2 read_pair_ids(const int* sm, int pair) { return *(const u2*)(sm + 2 * pair); }
+
+__device__ __forceinline__ void load_f16(const ZoneP& z, int64_t bh, int tile, bool valid, int c, int g, F16Tile& d) {
+    constexpr int kTileBytes = kBlockTokens * kHeadDim * 2;   // 4 KB of K rows, 4 KB of V^T
+    const __amdgpu_buffer_rsrc_t rk = rsrc(z.k + (bh * z.cap + (int64_t)tile * kBlockTokens) * kHeadDim, valid ? kTileBytes : 0);
+    const __amdgpu_buffer_rsrc_t rv =
+        rsrc(z.v + (bh * (z.cap / kBlockTokens) + tile) * (kBlockTokens * kHeadDim), valid ? kTileBytes : 0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        d.k[j] = *(const u4*)(kp + 8 * j);
-        d.v[j] = *(const u4*)(vp + 8 * j);
+        d.k[j] = ld16(rk, (c * kHeadDim + 32 * g + 8 * j) * 2);
+        d.v[j] = ld16(rv, ((g * 16 + c) * 32 + 8 * j) * 2);
     }
 }
 
@@ -240,11 +292,12 @@ __device__ __forceinline__ h8 k_operand(uint32_t w, h2 kz1024, h2 kz64) {
 // Two INT4 blocks (32 tokens) per step: the two QK chains interleave, and one
 // 16x16x32 MFMA per 16 dims does PV for both blocks (k slots 0..3 = block A
 // tokens 4g..4g+3, slots 4..7 = block B tokens 4g..4g+3).
-__device__ __forceinline__ void step_int4_pair(const Int4Blk& A, const Int4Blk& B, int nA, int nB, int g,
+__device__ __forceinline__ void step_int4_pair(const Int4Blk& A, const Int4Blk& B, int nA, int nB, int g, int kzsh,
                                                const h8 (&qf)[4], float scale_log2, f4 (&acc)[8], float& m,
                                                float& l) {
-    const h2 kA1024 = zp1024(A.kz, A.kz), kA64 = zp64(A.kz, A.kz);
-    const h2 kB1024 = zp1024(B.kz, B.kz), kB64 = zp64(B.kz, B.kz);
+    const uint32_t kza = __builtin_amdgcn_ubfe(A.kz, kzsh, 8), kzb = __builtin_amdgcn_ubfe(B.kz, kzsh, 8);
+    const h2 kA1024 = zp1024(kza, kza), kA64 = zp64(kza, kza);
+    const h2 kB1024 = zp1024(kzb, kzb), kB64 = zp64(kzb, kzb);
     const uint32_t kwA[4] = {A.k.x, A.k.y, A.k.z, A.k.w};
     const uint32_t kwB[4] = {B.k.x, B.k.y, B.k.z, B.k.w};
     f4 SA = {0.f, 0.f, 0.f, 0.f}, SB = {0.f, 0.f, 0.f, 0.f};
@@ -341,44 +394,74 @@ __device__ __forceinline__ void step_f16(F16Tile& d, int nvalid, int g, const h8
     }
 }
 
-// Item layout of one (sequence, kv head): INT4 blocks [0, nb4), then the tiles
-// of zone 0, 1, 2.  first_item(x) = index of the first item whose byte offset
-// is >= x, so [first_item(a), first_item(b)) partitions the items.
-struct ItemMap {
-    int nb4;
+// Tile counts of the fp16 zones of one sequence; tiles are numbered over zones
+// 0, 1, 2 in order.
+struct ZoneTiles {
     int nt[HKV_MAX_F16_ZONES];
-    int nz;
-    __device__ int64_t total_bytes() const {
-        int64_t t = (int64_t)nb4 * kInt4ItemBytes;
-#pragma unroll
-        for (int z = 0; z < HKV_MAX_F16_ZONES; ++z) t += (int64_t)nt[z] * kF16ItemBytes;
-        return t;
-    }
-    __device__ int first_item(int64_t x) const {
-        const int64_t e4 = (int64_t)nb4 * kInt4ItemBytes;
-        if (x <= e4) return (int)((x + kInt4ItemBytes - 1) / kInt4ItemBytes);
-        int base = nb4;
-        int64_t off = e4;
-        int r = -1;
-#pragma unroll
-        for (int z = 0; z < HKV_MAX_F16_ZONES; ++z) {
-            const int64_t ez = off + (int64_t)nt[z] * kF16ItemBytes;
-            if (r < 0 && x <= ez) r = base + (int)((x - off + kF16ItemBytes - 1) / kF16ItemBytes);
-            base += nt[z];
-            off = ez;
-        }
-        return r < 0 ? base : r;
-    }
+    __device__ int total() const { return nt[0] + nt[1] + nt[2]; }
 };
 
+// Zone, valid length and tile of fp16 tile t counted over zones 0, 1, 2 in order.
+static_assert(HKV_MAX_F16_ZONES == 3, "locate_tile walks three zones");
+__device__ __forceinline__ void locate_tile(const DecodeParams& p, const ZoneTiles& im, const int (&lenz)[HKV_MAX_F16_ZONES],
+                                            int t, ZoneP& z, int& len, int& tile) {
+    z = p.z[0];
+    len = lenz[0];
+    if (t >= im.nt[0]) {
+        t -= im.nt[0];
+        z = p.z[1];
+        len = lenz[1];
+        if (t >= im.nt[1]) {
+            t -= im.nt[1];
+            z = p.z[2];
+            len = lenz[2];
+        }
+    }
+    tile = t;
+}
+
+// kDynamic: the workgroup's units are handed to its waves from LDS counters, so
+// every wave stays busy until the workgroup's share is done (the two waves sharing
+// a SIMD do not progress at the same rate: the older one wins issue).  The result
+// then depends on which wave took which unit, in the last bits.  Otherwise wave w
+// takes units w, w + kWaves, ... and the result is bitwise reproducible.
+template <bool kDynamic>
+__device__ __forceinline__ int next_unit(int* ctr, int& seq) {
+    if constexpr (kDynamic) {
+        return grab(ctr);
+    } else {
+        const int u = seq;
+        seq += kWaves;
+        return u;
+    }
+}
+
+// Splits that stream only INT4 blocks when a pair's ranges are made of one kind
+// each, or 0 when every range takes the same share of both kinds.  Ranges of one
+// kind avoid a second pipeline start inside a range; they are used when the
+// rounding of nsplit into two groups costs at most ~6% over an even share.  Costs:
+// an INT4 block counts kInt4Cost bytes (its 2208 bytes, plus the block-id
+// indirection and the nibble decode), an fp16 tile its 8192 bytes.
+__device__ __forceinline__ int int4_splits(int nb4, int ntf, int nsplit) {
+    if (nb4 == 0 || ntf == 0 || nsplit < 2) return 0;
+    const int64_t c4 = (int64_t)nb4 * kInt4Cost, cf = (int64_t)ntf * kF16ItemBytes, ct = c4 + cf;
+    int s4 = (int)((c4 * nsplit + ct / 2) / ct);
+    s4 = min(max(s4, 1), nsplit - 1);
+    const int64_t worst = max((c4 + s4 - 1) / s4, (cf + nsplit - s4 - 1) / (nsplit - s4));
+    return worst * 16 <= (ct + nsplit - 1) / nsplit * 17 ? s4 : 0;
+}
+
+template <bool kDynamic>
 __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const int BH = p.B * p.Hkv;
     const int bh = blockIdx.x % BH;
     const int split = blockIdx.x / BH;
     const int nsplit = p.max_splits;
     const int b = bh / p.Hkv, h = bh % p.Hkv;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: buffer resources stay scalar
     const int c = lane & 15, g = lane >> 4;
+    const int kzsh = 8 * (c & 3);
     const int nrep = p.nrep;
     if (p.xcc_local && p.nxcc > 1 && threadIdx.x == 0) {
         const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15;   // HW_REG_XCC_ID
@@ -387,20 +470,43 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
 
     const int len4 = p.int4_lens ? min(max(p.int4_lens[b], 0), p.int4_max_len) : p.int4_max_len;
     int lenz[HKV_MAX_F16_ZONES];
-    ItemMap im;
-    im.nb4 = (len4 + kBlockTokens - 1) / kBlockTokens;
-    im.nz = p.nz;
+    ZoneTiles zt;
 #pragma unroll
     for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
         lenz[zi] = 0;
         if (zi < p.nz)
             lenz[zi] = p.z[zi].lens ? min(max(p.z[zi].lens[b], 0), p.z[zi].max_len) : p.z[zi].max_len;
-        im.nt[zi] = (lenz[zi] + kBlockTokens - 1) / kBlockTokens;
+        zt.nt[zi] = (lenz[zi] + kBlockTokens - 1) / kBlockTokens;
     }
-    const int64_t total = im.total_bytes();
-    const int64_t r0 = total * split / nsplit, r1 = total * (split + 1) / nsplit;
-    const int64_t w0 = r0 + (r1 - r0) * wave / kWaves, w1 = r0 + (r1 - r0) * (wave + 1) / kWaves;
-    const int i0 = im.first_item(w0), i1 = im.first_item(w1);
+    // Range `split` of this (sequence, kv head): INT4 blocks [a0, a1) and fp16
+    // tiles [f0, f0 + nf).
+    const int nb4 = (len4 + kBlockTokens - 1) / kBlockTokens, ntf = zt.total();
+    int a0, a1, f0, nf;
+    {
+        const int s4 = int4_splits(nb4, ntf, nsplit);
+        if (s4 > 0 && s4 < nsplit) {
+            // splits [0, s4) stream INT4 blocks only, the others fp16 tiles only
+            const bool is4 = split < s4;
+            const int si = is4 ? split : split - s4, sn = is4 ? s4 : nsplit - s4, n = is4 ? nb4 : ntf;
+            const int u0 = (int)((int64_t)n * si / sn), u1 = (int)((int64_t)n * (si + 1) / sn);
+            a0 = is4 ? u0 : 0;
+            a1 = is4 ? u1 : 0;
+            f0 = is4 ? 0 : u0;
+            nf = is4 ? 0 : u1 - u0;
+        } else {
+            // every split takes the same share of both kinds
+            a0 = (int)((int64_t)nb4 * split / nsplit);
+            a1 = (int)((int64_t)nb4 * (split + 1) / nsplit);
+            f0 = (int)((int64_t)ntf * split / nsplit);
+            nf = (int)((int64_t)ntf * (split + 1) / nsplit) - f0;
+        }
+    }
+
+    // The block ids of the first INT4 window are requested before anything else;
+    // the fp16 tiles are streamed while they are on their way.
+    int idr[kIdPerThread];
+    fetch_block_ids(p, b, a0, min(kIdWindow, a1 - a0), idr);
+    __builtin_amdgcn_sched_barrier(0);
 
     // q fragments: lane (c, g) holds q[head c][32g + 8j .. +8] for step j.
     h8 qf[4];
@@ -419,69 +525,109 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     for (int n = 0; n < 8; ++n) acc[n] = f4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.0f;
 
-    // ---- INT4 blocks of this wave's piece, two per step.  Block ids come 64 at
-    // a time; the loop body is branch-free so the next kPrefetch pairs stay in
-    // flight: past the end it re-reads the last block (an in-bounds address) and
-    // runs with no valid token, which contributes nothing.
-    {
-        const int lb0 = i0, lb1 = min(i1, im.nb4);
-        for (int cb = lb0; cb < lb1; cb += 64) {
-            const int cn = min(64, lb1 - cb);
-            const int ids = load_block_ids(p, b, cb, cb + cn, lane);
-            Int4Blk bufA[kPrefetch], bufB[kPrefetch];
-            // sched_barrier keeps each slot's loads together and in slot order, in the
-            // prologue as in the loop, so the waits before a slot's use only cover that
-            // slot and the later slots stay in flight
+    __shared__ __align__(16) int sm_ids[kIdWindow + 2];
+    __shared__ int sm_ctr[2];   // next INT4 pair, next fp16 tile (kDynamic)
+    if (kDynamic && threadIdx.x == 0) {
+        sm_ctr[0] = kPrefetch * kWaves;   // the first round of each window is static
+        sm_ctr[1] = 2 * kWaves;
+    }
+
+    // ---- fp16 zone tiles f0 .. f0 + nf, depth 2.  Every slot of a round is
+    // consumed (an empty one with no valid token, which contributes nothing), and
+    // the only exit is at the back edge; units only grow, so an empty slot 0 means
+    // every later slot is empty too.  An exit from inside the round would add a path
+    // on which the later slots were not refilled, and the waits at the loop head
+    // would then drain every slot.
+    if (nf > 0) {
+        F16Tile buf[2];
+        int tq[2];
+        ZoneP zq[2];
+        int lq[2];
+        int seq = wave + 2 * kWaves;
 #pragma unroll
-            for (int k = 0; k < kPrefetch; ++k) {
-                __builtin_amdgcn_sched_barrier(0);
-                load_int4(p, h, __builtin_amdgcn_readlane(ids, min(2 * k, cn - 1)), c, g, bufA[k]);
-                load_int4(p, h, __builtin_amdgcn_readlane(ids, min(2 * k + 1, cn - 1)), c, g, bufB[k]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            for (int base = 0; base < cn; base += 2 * kPrefetch) {
+        for (int k = 0; k < 2; ++k) {
+            tq[k] = wave + k * kWaves;
+            int t;
+            locate_tile(p, zt, lenz, f0 + min(tq[k], nf - 1), zq[k], lq[k], t);
+            __builtin_amdgcn_sched_barrier(0);
+            load_f16(zq[k], bh, t, tq[k] < nf, c, g, buf[k]);
+            __builtin_amdgcn_sched_barrier(0);
+            lq[k] -= t * kBlockTokens;
+        }
+        // the first INT4 window's ids arrive with these tiles (they were requested
+        // first); they and the counters are published before the loop starts
+        if (a1 > a0) commit_block_ids(p, min(kIdWindow, a1 - a0), idr, sm_ids);
+        __syncthreads();
+        if (tq[0] < nf) {
+            do {
 #pragma unroll
-                for (int k = 0; k < kPrefetch; ++k) {
-                    const int i = base + 2 * k;
-                    const int nA = (i < cn ? min(kBlockTokens, len4 - (cb + i) * kBlockTokens) : 0);
-                    const int nB = (i + 1 < cn ? min(kBlockTokens, len4 - (cb + i + 1) * kBlockTokens) : 0);
-                    step_int4_pair(bufA[k], bufB[k], nA, nB, g, qf, p.scale_log2, acc, m, l);
+                for (int k = 0; k < 2; ++k) {
+                    step_f16(buf[k], tq[k] < nf ? min(kBlockTokens, lq[k]) : 0, g, qf, p.scale_log2, acc, m, l);
+                    tq[k] = next_unit<kDynamic>(&sm_ctr[1], seq);
+                    int t;
+                    locate_tile(p, zt, lenz, f0 + min(tq[k], nf - 1), zq[k], lq[k], t);
                     __builtin_amdgcn_sched_barrier(0);
-                    load_int4(p, h, __builtin_amdgcn_readlane(ids, min(i + 2 * kPrefetch, cn - 1)), c, g, bufA[k]);
-                    load_int4(p, h, __builtin_amdgcn_readlane(ids, min(i + 2 * kPrefetch + 1, cn - 1)), c, g, bufB[k]);
+                    load_f16(zq[k], bh, t, tq[k] < nf, c, g, buf[k]);
                     __builtin_amdgcn_sched_barrier(0);
+                    lq[k] -= t * kBlockTokens;
                 }
-            }
+            } while (tq[0] < nf);
         }
     }
-    // ---- fp16 zone tiles of this wave's piece (same pipelining, depth 2)
-    {
-        int zbase = im.nb4;
+
+    // ---- INT4 blocks a0 .. a1, two per step, in windows of kIdWindow block ids
+    // staged in LDS (same loop shape).  An empty slot re-reads the window's last
+    // pair, an in-bounds address.
+    if (nf <= 0 && a1 > a0) {
+        commit_block_ids(p, min(kIdWindow, a1 - a0), idr, sm_ids);
+        __syncthreads();
+    }
+    for (int wb = a0; wb < a1; wb += kIdWindow) {
+        const int wn = min(kIdWindow, a1 - wb);
+        if (wb != a0) {
+            fetch_block_ids(p, b, wb, wn, idr);
+            commit_block_ids(p, wn, idr, sm_ids);
+            __syncthreads();
+        }
+        const int npairs = (wn + 1) >> 1;
+        Int4Blk bufA[kPrefetch], bufB[kPrefetch];
+        int pk[kPrefetch];
+        int seq = wave + kPrefetch * kWaves;
+        // sched_barrier keeps each slot's loads together and in slot order, in the
+        // prologue as in the loop, so the waits before a slot's use only cover that
+        // slot and the later slots stay in flight
 #pragma unroll
-        for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
-            const int t0 = max(i0 - zbase, 0), t1 = min(i1 - zbase, im.nt[zi]);
-            if (zi < p.nz && t0 < t1) {
-                const ZoneP& z = p.z[zi];
-                const int len = lenz[zi];
-                F16Tile buf[2];
-                __builtin_amdgcn_sched_barrier(0);
-                load_f16(z, bh, t0, c, g, buf[0]);
-                __builtin_amdgcn_sched_barrier(0);
-                load_f16(z, bh, min(t0 + 1, t1 - 1), c, g, buf[1]);
-                __builtin_amdgcn_sched_barrier(0);
-                for (int base = t0; base < t1; base += 2) {
+        for (int k = 0; k < kPrefetch; ++k) {
+            pk[k] = wave + k * kWaves;
+            const u2 id = read_pair_ids(sm_ids, min(pk[k], npairs - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            load_int4(p, h, __builtin_amdgcn_readfirstlane((int)id.x), pk[k] < npairs, c, g, bufA[k]);
+            load_int4(p, h, __builtin_amdgcn_readfirstlane((int)id.y), 2 * pk[k] + 1 < wn, c, g, bufB[k]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        int nxt = next_unit<kDynamic>(&sm_ctr[0], seq);
+        u2 nid = read_pair_ids(sm_ids, min(nxt, npairs - 1));
+        if (pk[0] < npairs) {
+            do {
 #pragma unroll
-                    for (int k = 0; k < 2; ++k) {
-                        const int t = base + k;
-                        step_f16(buf[k], t < t1 ? min(kBlockTokens, len - t * kBlockTokens) : 0, g, qf,
-                                 p.scale_log2, acc, m, l);
-                        __builtin_amdgcn_sched_barrier(0);
-                        load_f16(z, bh, min(t + 2, t1 - 1), c, g, buf[k]);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
+                for (int k = 0; k < kPrefetch; ++k) {
+                    const int lb = wb + 2 * pk[k];
+                    const int nA = pk[k] < npairs ? min(kBlockTokens, len4 - lb * kBlockTokens) : 0;
+                    const int nB = (2 * pk[k] + 1 < wn) ? min(kBlockTokens, len4 - (lb + 1) * kBlockTokens) : 0;
+                    step_int4_pair(bufA[k], bufB[k], nA, nB, g, kzsh, qf, p.scale_log2, acc, m, l);
+                    pk[k] = nxt;
+                    __builtin_amdgcn_sched_barrier(0);
+                    load_int4(p, h, __builtin_amdgcn_readfirstlane((int)nid.x), nxt < npairs, c, g, bufA[k]);
+                    load_int4(p, h, __builtin_amdgcn_readfirstlane((int)nid.y), 2 * nxt + 1 < wn, c, g, bufB[k]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    nxt = next_unit<kDynamic>(&sm_ctr[0], seq);
+                    nid = read_pair_ids(sm_ids, min(nxt, npairs - 1));
                 }
-            }
-            zbase += im.nt[zi];
+            } while (pk[0] < npairs);
+        }
+        if (wb + kIdWindow < a1) {
+            __syncthreads();   // every wave is done with this window's ids and counter
+            if (kDynamic && threadIdx.x == 0) sm_ctr[0] = kPrefetch * kWaves;
         }
     }
 
@@ -736,6 +882,8 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     HKV_REQUIRE(nrep <= 16, HKV_ERR_UNSUPPORTED, "hkv_decode_attn: n_rep %d > 16", nrep);
     HKV_REQUIRE(a->num_f16_zones >= 0 && a->num_f16_zones <= HKV_MAX_F16_ZONES, HKV_ERR_ARG,
                 "hkv_decode_attn: num_f16_zones %d out of range", a->num_f16_zones);
+    HKV_REQUIRE((a->flags & ~HKV_DECODE_DETERMINISTIC) == 0, HKV_ERR_ARG, "hkv_decode_attn: unknown flags 0x%x",
+                (unsigned)a->flags);
     HKV_REQUIRE(a->q && a->out && a->workspace, HKV_ERR_ARG, "hkv_decode_attn: null q/out/workspace");
     HKV_REQUIRE((((uintptr_t)a->q) & 15) == 0 && (a->q_stride_b % 8) == 0 && (a->q_stride_h % 8) == 0,
                 HKV_ERR_ARG, "hkv_decode_attn: q must be 16-byte aligned with strides multiple of 8");
@@ -812,16 +960,19 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     p.xcc_local = (BH % p.nxcc) == 0 ? 1 : 0;
     p.max_splits = ms;
     const size_t lds = lds_bytes(nrep);
-    if (lds > 64 * 1024) {
-        static bool raised = false;
-        if (!raised) {
-            HKV_HIP_CHECK(hipFuncSetAttribute((const void*)decode_attn_kernel,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
-            raised = true;
-        }
+    const bool det = (a->flags & HKV_DECODE_DETERMINISTIC) != 0;
+    const void* fn = det ? (const void*)decode_attn_kernel<false> : (const void*)decode_attn_kernel<true>;
+    static bool raised[2] = {false, false};   // the merge area plus the static id window can exceed 64 KB
+    if (!raised[det]) {
+        HKV_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
+        raised[det] = true;
     }
-    hipLaunchKernelGGL(decode_attn_kernel, dim3((unsigned)(BH * ms)), dim3(kThreads), lds,
-                       (hipStream_t)stream, p);
+    if (det)
+        hipLaunchKernelGGL(decode_attn_kernel<false>, dim3((unsigned)(BH * ms)), dim3(kThreads), lds,
+                           (hipStream_t)stream, p);
+    else
+        hipLaunchKernelGGL(decode_attn_kernel<true>, dim3((unsigned)(BH * ms)), dim3(kThreads), lds,
+                           (hipStream_t)stream, p);
     HKV_LAUNCH_CHECK("decode_attn_kernel");
     return HKV_OK;
 }

@@ -13,9 +13,10 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libheterokv.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_U8 = 0, 1, 2, 3
 MAX_F16_ZONES = 3
+DECODE_DETERMINISTIC = 1   # HKV_DECODE_DETERMINISTIC
 BLOCK_TOKENS = 16
 HEAD_DIM = 128
 
@@ -75,7 +76,7 @@ class DecodeArgs(ctypes.Structure):
                 ("int4_lens", vp), ("int4_max_len", i32),
                 ("out", vp), ("out_stride_b", i64), ("out_stride_h", i64),
                 ("workspace", vp), ("workspace_bytes", ctypes.c_size_t), ("splits_hint", i32),
-                ("staging", vp), ("staging_blocks", i64)]
+                ("staging", vp), ("staging_blocks", i64), ("flags", i32)]
 
 
 class PrefillArgs(ctypes.Structure):

@@ -151,6 +151,9 @@ class HeteroKVManager:
         self._eviction_counter = 0
         self._queued_tokens = 0      # tokens the reference would leave in its competition queue
         self._workspace = None
+        # True: decode launches use the fixed block-to-wave schedule (bitwise
+        # reproducible); False: blocks go to waves on demand (faster)
+        self.deterministic_decode = False
         # host tier (offload_to_host) and its prefetch schedule
         self._pf: Optional[Prefetcher] = None
         self._staging: List[ops.Int4Pool] = []
@@ -681,7 +684,8 @@ class HeteroKVManager:
         out = ops.decode_attention(q16, zones=zones, pool=st.pool if n4 else None,
                                    block_table=bt if n4 else None, int4_max_len=n4,
                                    sm_scale=sm_scale, workspace=self._workspace,
-                                   staging=self._staging[buf] if staged else None)
+                                   staging=self._staging[buf] if staged else None,
+                                   deterministic=self.deterministic_decode)
         if staged:
             self._pf.mark(slot)
             self._pending.pop(layer_idx, None)

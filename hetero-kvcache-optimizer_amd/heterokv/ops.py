@@ -285,7 +285,7 @@ def _int4_source(pool, staging):
 
 
 def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
-                     sm_scale=None, workspace=None, out=None, splits=0, staging=None):
+                     sm_scale=None, workspace=None, out=None, splits=0, staging=None, deterministic=False):
     """Split-K decode attention over fp16 zones and the INT4 pool.
 
     q: [B, Hq, 128] or [B, Hq, 1, 128] fp16.
@@ -294,6 +294,9 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
     staging: Int4Pool whose record i a block-table entry ~i (negative) names.
     splits: ranges per (sequence, kv head); 0 lets the library choose (about one
     workgroup per CU).
+    deterministic: fixed block-to-wave assignment, bitwise reproducible output.  The
+    default hands blocks to waves on demand (faster); outputs can then differ from
+    run to run in the last bits.
     Returns fp16 [B, Hq, 128] (or [B, Hq, 1, 128] if q was 4-D).
     """
     _require_gpu(q)
@@ -355,6 +358,7 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
     ws = workspace.get(nbytes)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     a.splits_hint = int(splits)
+    a.flags = _lib.DECODE_DETERMINISTIC if deterministic else 0
     check(load().hkv_decode_attn(ctypes.byref(a), stream_ptr(dev)), "hkv_decode_attn")
     return out.unsqueeze(2) if squeeze else out
 

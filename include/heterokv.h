@@ -65,7 +65,7 @@
 extern "C" {
 #endif
 
-#define HKV_ABI_VERSION 2
+#define HKV_ABI_VERSION 3
 
 /* dtype codes */
 #define HKV_DTYPE_F16  0
@@ -246,7 +246,15 @@ typedef struct HkvDecodeArgs {
     int32_t splits_hint;           /* 0 = auto */
     const uint8_t* staging;        /* records addressed by negative block ids (may be NULL) */
     int64_t staging_blocks;
+    int32_t flags;                 /* HKV_DECODE_* bits */
 } HkvDecodeArgs;
+
+/* Decode flag: every wave of a range takes a fixed subset of the range's blocks, so
+ * the output is bitwise reproducible from run to run.  Without it the blocks are
+ * handed out to the waves on demand, which keeps all of them busy to the end (faster
+ * on long contexts and large batches) and changes the summation order, so outputs
+ * can differ in the last bits between runs. */
+#define HKV_DECODE_DETERMINISTIC 1
 
 size_t hkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                                   int32_t head_dim, int32_t int4_max_len,

@@ -69,12 +69,13 @@ class Case:
             self.zones.append((zr, lens if B > 1 else None, max(self.recents)))
         self.int4_lens = torch.tensor(self.mids, dtype=torch.int32) if B > 1 else None
 
-    def run(self, workspace=None, sm_scale=None):
+    def run(self, workspace=None, sm_scale=None, deterministic=False, splits=0):
         from heterokv import ops
         out = ops.decode_attention(self.q.to(DEV), zones=self.zones, pool=self.pool,
                                    block_table=self.bt.to(DEV),
                                    int4_lens=self.int4_lens.to(DEV) if self.int4_lens is not None else None,
-                                   int4_max_len=self.maxmid, sm_scale=sm_scale, workspace=workspace)
+                                   int4_max_len=self.maxmid, sm_scale=sm_scale, workspace=workspace,
+                                   deterministic=deterministic, splits=splits)
         torch.cuda.synchronize()
         return out.float().cpu().numpy()
 
@@ -99,12 +100,14 @@ class Case:
 
 
 def _check(case, **kw):
-    got = case.run(**kw)
+    """Both block schedules (on-demand and fixed) against the oracle."""
     ref = case.oracle(sm_scale=kw.get("sm_scale"))
-    err = np.abs(got - ref).max()
-    print("  max abs err %.3e" % err, flush=True)
-    assert np.all(np.isfinite(got))
-    assert err <= TOL
+    for det in (False, True):
+        got = case.run(deterministic=det, **kw)
+        err = np.abs(got - ref).max()
+        print("  deterministic=%s max abs err %.3e" % (det, err), flush=True)
+        assert np.all(np.isfinite(got))
+        assert err <= TOL
     return got
 
 
@@ -160,14 +163,23 @@ def test_garbage_beyond_length_is_ignored():
 
 
 def test_deterministic_bitwise():
-    print("case: run twice, same bits", flush=True)
+    print("case: deterministic schedule, run twice, same bits", flush=True)
     from heterokv import ops
     c = Case(10, 2, 32, 8, 64, [9000, 4000], [4096, 2000])
     ws = ops.DecodeWorkspace(DEV)
-    a = c.run(workspace=ws)
-    b = c.run(workspace=ws)
+    a = c.run(workspace=ws, deterministic=True)
+    b = c.run(workspace=ws, deterministic=True)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     assert ws.error_flag() == 0
+
+
+def test_schedules_agree_on_long_windows():
+    """Ranges longer than one block-id window (1024 INT4 blocks) restage the ids
+    between windows: one range per pair (splits=1) over 40000 INT4 tokens = 2500
+    blocks = 3 windows, against the oracle in both schedules."""
+    print("case: splits=1, 2500 INT4 blocks, B=2", flush=True)
+    c = Case(12, 2, 16, 2, 64, [40000, 17000], [300, 4096])
+    _check(c, splits=1)
 
 
 def test_reference_api_fused_dequant_attn_decode():

@@ -87,10 +87,11 @@ def test_decode_with_staging_is_bit_identical(frac):
     q = (torch.randn((B, HQ, 128), generator=g) / math.sqrt(128)).half().to(DEV)
     ws = ops.DecodeWorkspace(DEV)
     ref = ops.decode_attention(q, zones=[(zone, None, 64)], pool=pool, block_table=bt, int4_max_len=T,
-                               workspace=ws)
+                               workspace=ws, deterministic=True)
     staging, bt2 = _move_to_staging(pool, bt, frac, 4)
     got = ops.decode_attention(q, zones=[(zone, None, 64)], pool=None if frac == 1.0 else pool,
-                               block_table=bt2, int4_max_len=T, workspace=ws, staging=staging)
+                               block_table=bt2, int4_max_len=T, workspace=ws, staging=staging,
+                               deterministic=True)
     torch.cuda.synchronize()
     assert ws.error_flag() == 0
     assert torch.equal(got, ref)
@@ -177,6 +178,7 @@ def test_manager_offload_bit_identical_to_resident(prefetch):
     K, V = _kv(11, B, H, sum(chunks) + steps)
     a = HeteroKVManager(L, sink_tokens=64, hbm_budget_tokens=576, device=DEV, enable_prefetch=prefetch)
     b = HeteroKVManager(L, sink_tokens=64, hbm_budget_tokens=576, device=DEV)
+    a.deterministic_decode = b.deterministic_decode = True
     pos = _feed([a, b], K, V, L, chunks)
     key = list(a._dram_table.keys())[1]
     moved = a.offload_to_host(0.75, seed=3)
