@@ -15,6 +15,7 @@
 // the 8-token k-slices the P^T operand needs, so P never leaves registers.  LDS rows
 // are XOR-swizzled (16-byte chunks for K, 8-byte units for V^T) against bank conflicts.
 #include "hkv_internal.h"
+#include "nibble_decode.h"
 
 #include <math.h>
 
@@ -33,6 +34,12 @@ constexpr int kT = 64;            // tokens per tile
 constexpr int kWavesP = 4;
 constexpr int kThreadsP = 256;
 constexpr int kTileBytes = kT * kHeadDim * 2;     // 16 KB for K, 16 KB for V^T
+// One LDS tile buffer: K rows, V^T, then per token the K factor (K scale x sm_scale x
+// log2 e) and the V scale, fp32.  INT4 tiles hold exact (code - zero point) values and
+// the scales are applied to the scores and the probabilities; fp16 tiles hold K and V
+// with factors (sm_scale x log2 e, 1).
+constexpr int kSkOff = 2 * kTileBytes, kSvOff = kSkOff + kT * 4;
+constexpr int kBufBytes = kSvOff + kT * 4;
 constexpr float kLog2eP = 1.4426950408889634f;
 
 struct ZoneP {
@@ -77,15 +84,14 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 
 // Staged global data of one tile for one thread (all tile kinds).
 struct Stage {
-    u4 a[4];      // K part (INT4: a[0] = 16 B codes; fp16: 4 x 16 B row pieces)
-    u4 b[4];      // V part (INT4: b[0] = 16 B codes; fp16: 4 x 16 B)
-    float ks, vs[4];
-    uint32_t kz, vz;
-    int kind;     // 0 = INT4, 1 = zone tile, 2 = chunk rows, 3 = empty
+    u4 a[4];      // K: 4 x 16 B row pieces
+    u4 b[4];      // V: 4 x 16 B
+    int kind;     // 1 = zone tile, 2 = chunk rows, 3 = empty
     int valid;    // tokens valid in this thread's slice
 };
 
-// Tile enumeration: INT4 tiles, then each zone's tiles, then the causal chunk's tiles.
+// Tile enumeration: INT4 tiles, then each zone's tiles, then the causal chunk's tiles
+// (the generic staging below handles the last two kinds).
 struct TileMap {
     int n4, nz_t[HKV_MAX_F16_ZONES], nc;
     int len4, lenz[HKV_MAX_F16_ZONES];
@@ -97,43 +103,6 @@ __device__ __forceinline__ void stage_load(const PrefillParams& p, const TileMap
     s.kind = 3;
     s.valid = 0;
     int x = tile;
-    if (x < tm.n4) {
-        // INT4: 4 blocks of 16 tokens.  K: thread -> block t/64, token (t/4)%16, 32 dims (t%4).
-        const int lb0 = x * 4;
-        const int blk = t >> 6;
-        const int lb = lb0 + blk;
-        const int nb = (tm.len4 + kBlockTokens - 1) / kBlockTokens;
-        s.kind = 0;
-        int phys = p.fallback_id;
-        if (lb < nb) {
-            phys = p.bt[(int64_t)b * p.bt_stride + lb];
-            if (phys >= 0 ? (int64_t)phys >= p.pool_blocks : (int64_t)(~phys) >= p.staging_blocks) {
-                if (p.err) atomicOr(p.err, 1);
-                phys = p.fallback_id;
-            }
-        }
-        const int64_t rb = (int64_t)p.Hkv * kHeadPartBytes;
-        const uint8_t* part = (phys >= 0 ? p.pool + (int64_t)phys * rb : p.staging + (int64_t)(~phys) * rb) +
-                              RecordLayout::part(h);
-        const int rr = (t >> 2) & 15, pt = t & 3;
-        const int tok0 = lb * kBlockTokens;
-        s.valid = (lb < nb) ? min(kBlockTokens, tm.len4 - tok0) : 0;
-        if (lb < nb) {
-            s.a[0] = *(const u4*)(part + kPartKc + rr * 64 + pt * 16);
-            s.ks = *(const float*)(part + kPartKs + rr * 4);
-            s.kz = part[kPartKz + rr];
-            // V: words (t%64)*4 .. +3 of this block: tokens 4g..4g+3, g = (t%64)/16
-            const int g = (t & 63) >> 4;
-            s.b[0] = *(const u4*)(part + kPartVc + (t & 63) * 16);
-            const float4 vs4 = *(const float4*)(part + kPartVs + g * 16);
-            s.vs[0] = vs4.x;
-            s.vs[1] = vs4.y;
-            s.vs[2] = vs4.z;
-            s.vs[3] = vs4.w;
-            s.vz = *(const uint32_t*)(part + kPartVz + g * 4);
-        }
-        return;
-    }
     x -= tm.n4;
 #pragma unroll
     for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
@@ -177,50 +146,13 @@ __device__ __forceinline__ void stage_load(const PrefillParams& p, const TileMap
 
 // Writes the staged data of one tile into LDS buffer `lds` (K rows + V^T), zeros for
 // slots past the valid length so that masked probabilities multiply finite values.
-__device__ __forceinline__ void stage_store(const Stage& s, uint8_t* lds) {
+__device__ __forceinline__ void stage_store(const Stage& s, uint8_t* lds, float scale_log2) {
     const int t = threadIdx.x;
-    if (s.kind == 0) {
-        const int blk = t >> 6, rr = (t >> 2) & 15, pt = t & 3;
-        const int tok = blk * 16 + rr;
-        const bool ok = rr < s.valid;
-        const float zf = (float)s.kz;
-        const uint32_t w4[4] = {s.a[0].x, s.a[0].y, s.a[0].z, s.a[0].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {          // word j: dims 32pt + 8j .. +8
-            u4 o;
-            uint32_t r[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t pr = (w4[j] >> (4 * i)) & 0x000F000Fu;
-                const float lo = ((float)(pr & 0xF) - zf) * s.ks;
-                const float hi = ((float)(pr >> 16) - zf) * s.ks;
-                r[i] = ok ? pack2(lo, hi) : 0u;
-            }
-            o = u4{r[0], r[1], r[2], r[3]};
-            *(u4*)(lds + k_addr(tok, pt * 4 + j)) = o;
-        }
-        const int g = (t & 63) >> 4, c = t & 15;
-        float zf4[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) zf4[i] = (float)((s.vz >> (8 * i)) & 0xFF);
-        const uint32_t v4[4] = {s.b[0].x, s.b[0].y, s.b[0].z, s.b[0].w};
-#pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
-            const uint32_t w = v4[mm];
-            // x_k at bit (k%2)*16 + (k/2)*4: x0..x3 = tokens 4g..4g+3 at dim c+32mm, x4..x7 at +16
-            float val[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int tk = k & 3;
-                const float code = (float)((w >> nib_shift(k)) & 0xFu);
-                val[k] = (4 * g + tk < s.valid) ? (code - zf4[tk]) * s.vs[tk] : 0.0f;
-            }
-            const int unit = blk * 4 + g;
-            const int d1 = c + 32 * mm, d2 = d1 + 16;
-            *(u2*)(lds + vt_addr(d1, unit)) = u2{pack2(val[0], val[1]), pack2(val[2], val[3])};
-            *(u2*)(lds + vt_addr(d2, unit)) = u2{pack2(val[4], val[5]), pack2(val[6], val[7])};
-        }
-    } else if (s.kind == 1 || s.kind == 2 || s.kind == 3) {
+    if (t < kT) {
+        ((float*)(lds + kSkOff))[t] = scale_log2;
+        ((float*)(lds + kSvOff))[t] = 1.0f;
+    }
+    {
         const int tok = t >> 2, pt = t & 3;
         const bool okk = s.kind != 3 && tok < s.valid;
 #pragma unroll
@@ -264,7 +196,7 @@ struct Stage4 {
     u4 v;         // V words (t%64)*4 .. +3 of block t/64
     f4 vs;        // V scales of tokens 4g..4g+3, g = (t%64)/16
     float ks;     // K scale of the K row
-    uint32_t kz;  // K zero point of the K row
+    uint32_t kz;  // K zero point of the K row (low byte)
     uint32_t vz;  // V zero points of tokens 4g..4g+3 (bytes)
     int valid;    // valid tokens of block t/64 (0 past the end)
     int next_id;  // block id of this thread's block in tile + kRing
@@ -296,62 +228,51 @@ __device__ __forceinline__ void load4(const PrefillParams& p, int n4, int len4, 
     s.valid = (tile < n4 && lbt < nb) ? min(kBlockTokens, len4 - lbt * kBlockTokens) : 0;
     s.k = *(const u4*)(part + kPartKc + rr * 64 + pt * 16);
     s.ks = *(const float*)(part + kPartKs + rr * 4);
-    s.kz = part[kPartKz + rr];
+    s.kz = *(const uint32_t*)(part + kPartKz + (rr & ~3)) >> (8 * (rr & 3));   // a word load, no byte value
     s.v = *(const u4*)(part + kPartVc + (t & 63) * 16);
     s.vs = *(const f4*)(part + kPartVs + g * 16);
     s.vz = *(const uint32_t*)(part + kPartVz + g * 4);
     s.next_id = block_id4(p, nb, b, min(tile + kRing, n4 - 1));
 }
 
-// Dequantizes a staged INT4 tile into LDS buffer `lds` (K rows + V^T), exactly as the
-// reference's fp16 dequantization; slots past the valid length become zeros.
-__device__ __forceinline__ void store4(const Stage4& s, uint8_t* lds) {
+// Writes a staged INT4 tile into LDS buffer `lds`: K rows and V^T as exact fp16
+// (code - zero point) values, and the per-token factors.  Tokens past the valid
+// length hold finite values (their block is a valid record) and are masked in the
+// scores.
+__device__ __forceinline__ void store4(const Stage4& s, uint8_t* lds, float scale_log2) {
     const int t = threadIdx.x;
     const int blk = t >> 6, rr = (t >> 2) & 15, pt = t & 3;
     const int tok = blk * 16 + rr;
-    const bool ok = rr < s.valid;
-    const float zf = (float)s.kz;
+    const uint32_t kz = s.kz & 0xFFu;
+    const h2 kz1024 = zp1024(kz, kz), kz64 = zp64(kz, kz);
     const uint32_t w4[4] = {s.k.x, s.k.y, s.k.z, s.k.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {          // word j: dims 32pt + 8j .. +8
-        uint32_t r[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t pr = (w4[j] >> (4 * i)) & 0x000F000Fu;
-            const float lo = ((float)(pr & 0xF) - zf) * s.ks;
-            const float hi = ((float)(pr >> 16) - zf) * s.ks;
-            r[i] = ok ? pack2(lo, hi) : 0u;
-        }
-        *(u4*)(lds + k_addr(tok, pt * 4 + j)) = u4{r[0], r[1], r[2], r[3]};
+        const NibPairs a = unpack_word(w4[j], kz1024, kz64);
+        *(u4*)(lds + k_addr(tok, pt * 4 + j)) =
+            u4{__builtin_bit_cast(uint32_t, a.p0), __builtin_bit_cast(uint32_t, a.p1),
+               __builtin_bit_cast(uint32_t, a.p2), __builtin_bit_cast(uint32_t, a.p3)};
     }
+    if (pt == 0) ((float*)(lds + kSkOff))[tok] = s.ks * scale_log2;
+    // V word (t%64)*4 + mm: x0..x3 = tokens 4g..4g+3 at dim c+32mm, x4..x7 at +16
     const int g = (t & 63) >> 4, c = t & 15;
-    float zf4[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) zf4[i] = (float)((s.vz >> (8 * i)) & 0xFF);
+    const h2 z01 = zp1024(s.vz & 0xFFu, (s.vz >> 8) & 0xFFu), z23 = zp64((s.vz >> 16) & 0xFFu, s.vz >> 24);
     const uint32_t v4[4] = {s.v.x, s.v.y, s.v.z, s.v.w};
+    const int unit = blk * 4 + g;
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
-        const uint32_t w = v4[mm];
-        // x_k at bit (k%2)*16 + (k/2)*4: x0..x3 = tokens 4g..4g+3 at dim c+32mm, x4..x7 at +16
-        float val[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int tk = k & 3;
-            const float code = (float)((w >> nib_shift(k)) & 0xFu);
-            val[k] = (4 * g + tk < s.valid) ? (code - zf4[tk]) * s.vs[tk] : 0.0f;
-        }
-        const int unit = blk * 4 + g;
+        const NibPairs a = unpack_word(v4[mm], z01, z23);
         const int d1 = c + 32 * mm, d2 = d1 + 16;
-        *(u2*)(lds + vt_addr(d1, unit)) = u2{pack2(val[0], val[1]), pack2(val[2], val[3])};
-        *(u2*)(lds + vt_addr(d2, unit)) = u2{pack2(val[4], val[5]), pack2(val[6], val[7])};
+        *(u2*)(lds + vt_addr(d1, unit)) = u2{__builtin_bit_cast(uint32_t, a.p0), __builtin_bit_cast(uint32_t, a.p1)};
+        *(u2*)(lds + vt_addr(d2, unit)) = u2{__builtin_bit_cast(uint32_t, a.p2), __builtin_bit_cast(uint32_t, a.p3)};
     }
+    if (c == 0) *(f4*)(lds + kSvOff + (blk * 16 + 4 * g) * 4) = s.vs;
 }
 
 // One 64-token tile of attention for this wave's 32 query rows: S^T = K.Q^T, masked
 // online softmax, O^T += V^T.P^T.  `cur` holds the tile's K rows and V^T in LDS.
 __device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int causal_base, int n, int hh,
-                                            int qrow, const h8 (&qf)[8], float scale_log2, f16v (&acc)[4],
-                                            float& m, float& l) {
+                                            int qrow, const h8 (&qf)[8], f16v (&acc)[4], float& m, float& l) {
     f16v S[2];
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
@@ -364,6 +285,16 @@ __device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int 
             S[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], S[tb], 0, 0, 0);
         }
     }
+    // lane (n, hh) holds tokens tb*32 + 8j + 4hh + i for r = 4j + i: four consecutive
+    // tokens per j, whose factors are one 16-byte LDS read
+    f4 fk[2][4], fv[2][4];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            fk[tb][j] = *(const f4*)(cur + kSkOff + (tb * 32 + 8 * j + 4 * hh) * 4);
+            fv[tb][j] = *(const f4*)(cur + kSvOff + (tb * 32 + 8 * j + 4 * hh) * 4);
+        }
     float mt = -INFINITY;
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb)
@@ -372,7 +303,7 @@ __device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int 
             const int tok = tb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
             bool ok = tok < tvalid;
             if (causal_base >= 0) ok = ok && (causal_base + tok <= qrow);
-            const float sv = ok ? S[tb][r] * scale_log2 : -INFINITY;
+            const float sv = ok ? S[tb][r] * fk[tb][r >> 2][r & 3] : -INFINITY;
             S[tb][r] = sv;
             mt = fmaxf(mt, sv);
         }
@@ -398,7 +329,7 @@ __device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int 
                     const int r = 4 * (2 * u + jj) + i;
                     const float pv = __builtin_amdgcn_exp2f(S[tb][r] - msafe);
                     l += pv;
-                    P[tb][u][jj * 4 + i] = (_Float16)pv;
+                    P[tb][u][jj * 4 + i] = (_Float16)(pv * fv[tb][r >> 2][r & 3]);
                 }
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb)
@@ -482,7 +413,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_attn_kernel(PrefillParams p
             __builtin_amdgcn_sched_barrier(0);
         }
         ring[kRing - 1].next_id = id0[kRing - 1];
-        store4(ring[0], lds_raw);
+        store4(ring[0], lds_raw, p.scale_log2);
         __syncthreads();
         for (int t0 = 0; t0 < n4p; t0 += kRing) {
 #pragma unroll
@@ -493,9 +424,8 @@ __global__ __launch_bounds__(kThreadsP) void prefill_attn_kernel(PrefillParams p
                 load4(p, n4, tm.len4, b, h, tile + kRing - 1, slot.next_id, slot);
                 __builtin_amdgcn_sched_barrier(0);
                 const int tvalid = min(kT, tm.len4 - tile * kT);
-                attend_tile(lds_raw + (tile & 1) * (2 * kTileBytes), tvalid, -1, n, hh, qrow, qf, p.scale_log2,
-                            acc, m, l);
-                store4(ring[(u + 1) % kRing], lds_raw + ((tile + 1) & 1) * (2 * kTileBytes));
+                attend_tile(lds_raw + (tile & 1) * kBufBytes, tvalid, -1, n, hh, qrow, qf, acc, m, l);
+                store4(ring[(u + 1) % kRing], lds_raw + ((tile + 1) & 1) * kBufBytes, p.scale_log2);
                 __syncthreads();
             }
         }
@@ -506,13 +436,13 @@ __global__ __launch_bounds__(kThreadsP) void prefill_attn_kernel(PrefillParams p
     const int par0 = n4p;   // LDS buffer parity continues after the INT4 tiles
     if (ntiles > n4) {
         stage_load(p, tm, b, h, n4, st);
-        stage_store(st, lds_raw + (par0 & 1) * (2 * kTileBytes));
+        stage_store(st, lds_raw + (par0 & 1) * kBufBytes, p.scale_log2);
     }
     __syncthreads();
     for (int tile = n4; tile < ntiles; ++tile) {
         const int par = par0 + (tile - n4);
-        uint8_t* cur = lds_raw + (par & 1) * (2 * kTileBytes);
-        uint8_t* nxt = lds_raw + ((par + 1) & 1) * (2 * kTileBytes);
+        uint8_t* cur = lds_raw + (par & 1) * kBufBytes;
+        uint8_t* nxt = lds_raw + ((par + 1) & 1) * kBufBytes;
         if (tile + 1 < ntiles) stage_load(p, tm, b, h, tile + 1, st);
 
         // valid tokens of this tile and causal limit
@@ -537,8 +467,8 @@ __global__ __launch_bounds__(kThreadsP) void prefill_attn_kernel(PrefillParams p
                 causal_base = x * kT;
             }
         }
-        attend_tile(cur, tvalid, causal_base, n, hh, qrow, qf, p.scale_log2, acc, m, l);
-        if (tile + 1 < ntiles) stage_store(st, nxt);
+        attend_tile(cur, tvalid, causal_base, n, hh, qrow, qf, acc, m, l);
+        if (tile + 1 < ntiles) stage_store(st, nxt, p.scale_log2);
         __syncthreads();
     }
     (void)first_chunk_tile;
@@ -649,7 +579,13 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
     p.o_st = a->out_stride_t;
     p.err = a->err_flag;
     const dim3 grid((a->num_queries + kQ - 1) / kQ, a->num_kv_heads * ngrp, a->batch);
-    hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kThreadsP), 4 * kTileBytes, (hipStream_t)stream, p);
+    static bool raised = false;   // two tile buffers are a little over 64 KB
+    if (!raised) {
+        HKV_HIP_CHECK(hipFuncSetAttribute((const void*)prefill_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          2 * kBufBytes));
+        raised = true;
+    }
+    hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kThreadsP), 2 * kBufBytes, (hipStream_t)stream, p);
     HKV_LAUNCH_CHECK("prefill_attn_kernel");
     return HKV_OK;
 }
