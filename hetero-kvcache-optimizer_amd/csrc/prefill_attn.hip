@@ -201,7 +201,7 @@ struct Stage4 {
     int valid;    // valid tokens of block t/64 (0 past the end)
     int next_id;  // block id of this thread's block in tile + kRing
 };
-constexpr int kRing = 4;          // INT4 tiles in flight per thread
+constexpr int kRing = 2;          // INT4 tiles in flight per thread (4 measured slower: register pressure)
 
 // Block id of this thread's block (t/64) of INT4 tile x, clamped to the last block.
 __device__ __forceinline__ int block_id4(const PrefillParams& p, int nb, int b, int x) {
