@@ -273,40 +273,39 @@ __device__ __forceinline__ void store4(const Stage4& s, uint8_t* lds, float scal
 // online softmax, O^T += V^T.P^T.  `cur` holds the tile's K rows and V^T in LDS.
 __device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int causal_base, int n, int hh,
                                             int qrow, const h8 (&qf)[8], f16v (&acc)[4], float& m, float& l) {
+    // Phases are kept apart (sched_barrier) so that at most one token block's operands
+    // are live at a time: the kernel then fits two waves per SIMD.
     f16v S[2];
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) S[tb][r] = 0.f;
         const int tok = tb * 32 + n;
+        h8 a[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const h8 a = __builtin_bit_cast(h8, *(const u4*)(cur + k_addr(tok, 2 * s + hh)));
-            S[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], S[tb], 0, 0, 0);
-        }
+        for (int s = 0; s < 8; ++s) a[s] = __builtin_bit_cast(h8, *(const u4*)(cur + k_addr(tok, 2 * s + hh)));
+#pragma unroll
+        for (int s = 0; s < 8; ++s) S[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[s], qf[s], S[tb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
     }
     // lane (n, hh) holds tokens tb*32 + 8j + 4hh + i for r = 4j + i: four consecutive
     // tokens per j, whose factors are one 16-byte LDS read
-    f4 fk[2][4], fv[2][4];
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            fk[tb][j] = *(const f4*)(cur + kSkOff + (tb * 32 + 8 * j + 4 * hh) * 4);
-            fv[tb][j] = *(const f4*)(cur + kSvOff + (tb * 32 + 8 * j + 4 * hh) * 4);
-        }
     float mt = -INFINITY;
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
+    for (int tb = 0; tb < 2; ++tb) {
+        f4 fk[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fk[j] = *(const f4*)(cur + kSkOff + (tb * 32 + 8 * j + 4 * hh) * 4);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int tok = tb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
             bool ok = tok < tvalid;
             if (causal_base >= 0) ok = ok && (causal_base + tok <= qrow);
-            const float sv = ok ? S[tb][r] * fk[tb][r >> 2][r & 3] : -INFINITY;
+            const float sv = ok ? S[tb][r] * fk[r >> 2][r & 3] : -INFINITY;
             S[tb][r] = sv;
             mt = fmaxf(mt, sv);
         }
+    }
     mt = fmaxf(mt, __shfl_xor(mt, 32));
     if (__ballot(mt > m)) {
         const float m_new = fmaxf(m, mt);
@@ -317,9 +316,13 @@ __device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int 
         m = m_new;
     }
     const float msafe = (m == -INFINITY) ? 0.f : m;
-    h8 P[2][2];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
+    for (int tb = 0; tb < 2; ++tb) {
+        f4 fv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fv[j] = *(const f4*)(cur + kSvOff + (tb * 32 + 8 * j + 4 * hh) * 4);
+        h8 P[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -329,25 +332,30 @@ __device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int 
                     const int r = 4 * (2 * u + jj) + i;
                     const float pv = __builtin_amdgcn_exp2f(S[tb][r] - msafe);
                     l += pv;
-                    P[tb][u][jj * 4 + i] = (_Float16)(pv * fv[tb][r >> 2][r & 3]);
+                    P[u][jj * 4 + i] = (_Float16)(pv * fv[r >> 2][r & 3]);
                 }
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int unit0 = tb * 8 + 4 * u + hh;      // tokens tb*32 + 16u + 4hh (+8 for jj=1)
+            h8 a[4];
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
                 const int dim = 32 * db + n;
                 const u2 lo = *(const u2*)(cur + vt_addr(dim, unit0));
                 const u2 hi = *(const u2*)(cur + vt_addr(dim, unit0 + 2));
-                const h8 a = __builtin_bit_cast(h8, u4{lo.x, lo.y, hi.x, hi.y});
-                acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, P[tb][u], acc[db], 0, 0, 0);
+                a[db] = __builtin_bit_cast(h8, u4{lo.x, lo.y, hi.x, hi.y});
             }
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[db], P[u], acc[db], 0, 0, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
-__global__ __launch_bounds__(kThreadsP) void prefill_attn_kernel(PrefillParams p) {
+// Two workgroups per CU (two waves per SIMD): one wave's MFMA chains overlap the
+// other's dequantization and softmax.  This caps a wave at 256 registers; the few
+// values spilled are kernel-wide addresses read outside the INT4 tile loop.
+__global__ __launch_bounds__(kThreadsP, 2) void prefill_attn_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     const int b = blockIdx.z;
     const int ngrp = (p.nrep + kWavesP - 1) / kWavesP;
