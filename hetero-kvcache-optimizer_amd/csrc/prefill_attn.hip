@@ -38,8 +38,9 @@ constexpr int kTileBytes = kT * kHeadDim * 2;     // 16 KB for K, 16 KB for V^T
 // log2 e) and the V scale, fp32.  INT4 tiles hold exact (code - zero point) values and
 // the scales are applied to the scores and the probabilities; fp16 tiles hold K and V
 // with factors (sm_scale x log2 e, 1).
-constexpr int kSkOff = 2 * kTileBytes, kSvOff = kSkOff + kT * 4;
-constexpr int kBufBytes = kSvOff + kT * 4;
+// A third per-token array holds the score bias: 0, or -inf past the valid length.
+constexpr int kSkOff = 2 * kTileBytes, kSvOff = kSkOff + kT * 4, kSbOff = kSvOff + kT * 4;
+constexpr int kBufBytes = kSbOff + kT * 4;
 constexpr float kLog2eP = 1.4426950408889634f;
 
 struct ZoneP {
@@ -151,6 +152,7 @@ __device__ __forceinline__ void stage_store(const Stage& s, uint8_t* lds, float 
     if (t < kT) {
         ((float*)(lds + kSkOff))[t] = scale_log2;
         ((float*)(lds + kSvOff))[t] = 1.0f;
+        ((float*)(lds + kSbOff))[t] = s.kind != 3 && t < s.valid ? 0.0f : -INFINITY;
     }
     {
         const int tok = t >> 2, pt = t & 3;
@@ -253,7 +255,10 @@ __device__ __forceinline__ void store4(const Stage4& s, uint8_t* lds, float scal
             u4{__builtin_bit_cast(uint32_t, a.p0), __builtin_bit_cast(uint32_t, a.p1),
                __builtin_bit_cast(uint32_t, a.p2), __builtin_bit_cast(uint32_t, a.p3)};
     }
-    if (pt == 0) ((float*)(lds + kSkOff))[tok] = s.ks * scale_log2;
+    if (pt == 0) {
+        ((float*)(lds + kSkOff))[tok] = s.ks * scale_log2;
+        ((float*)(lds + kSbOff))[tok] = rr < s.valid ? 0.0f : -INFINITY;
+    }
     // V word (t%64)*4 + mm: x0..x3 = tokens 4g..4g+3 at dim c+32mm, x4..x7 at +16
     const int g = (t & 63) >> 4, c = t & 15;
     const h2 z01 = zp1024(s.vz & 0xFFu, (s.vz >> 8) & 0xFFu), z23 = zp64((s.vz >> 16) & 0xFFu, s.vz >> 24);
@@ -271,6 +276,10 @@ __device__ __forceinline__ void store4(const Stage4& s, uint8_t* lds, float scal
 
 // One 64-token tile of attention for this wave's 32 query rows: S^T = K.Q^T, masked
 // online softmax, O^T += V^T.P^T.  `cur` holds the tile's K rows and V^T in LDS.
+// kCausal: the tile is a piece of the causal chunk starting at chunk position
+// causal_base; token t is visible to query row qrow when t < tvalid and
+// causal_base + t <= qrow.  Otherwise the tile's bias array masks it.
+template <bool kCausal>
 __device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int causal_base, int n, int hh,
                                             int qrow, const h8 (&qf)[8], f16v (&acc)[4], float& m, float& l) {
     // Phases are kept apart (sched_barrier) so that at most one token block's operands
@@ -296,14 +305,23 @@ __device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int 
         f4 fk[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) fk[j] = *(const f4*)(cur + kSkOff + (tb * 32 + 8 * j + 4 * hh) * 4);
+        if constexpr (kCausal) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int tok = tb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-            bool ok = tok < tvalid;
-            if (causal_base >= 0) ok = ok && (causal_base + tok <= qrow);
-            const float sv = ok ? S[tb][r] * fk[r >> 2][r & 3] : -INFINITY;
-            S[tb][r] = sv;
-            mt = fmaxf(mt, sv);
+            for (int r = 0; r < 16; ++r) {
+                const int tok = tb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                const bool ok = tok < tvalid && causal_base + tok <= qrow;
+                S[tb][r] = ok ? S[tb][r] * fk[r >> 2][r & 3] : -INFINITY;
+                mt = fmaxf(mt, S[tb][r]);
+            }
+        } else {
+            f4 fb[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fb[j] = *(const f4*)(cur + kSbOff + (tb * 32 + 8 * j + 4 * hh) * 4);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                S[tb][r] = __builtin_fmaf(S[tb][r], fk[r >> 2][r & 3], fb[r >> 2][r & 3]);
+                mt = fmaxf(mt, S[tb][r]);
+            }
         }
     }
     mt = fmaxf(mt, __shfl_xor(mt, 32));
@@ -432,7 +450,7 @@ __global__ __launch_bounds__(kThreadsP, 2) void prefill_attn_kernel(PrefillParam
                 load4(p, n4, tm.len4, b, h, tile + kRing - 1, slot.next_id, slot);
                 __builtin_amdgcn_sched_barrier(0);
                 const int tvalid = min(kT, tm.len4 - tile * kT);
-                attend_tile(lds_raw + (tile & 1) * kBufBytes, tvalid, -1, n, hh, qrow, qf, acc, m, l);
+                attend_tile<false>(lds_raw + (tile & 1) * kBufBytes, tvalid, -1, n, hh, qrow, qf, acc, m, l);
                 store4(ring[(u + 1) % kRing], lds_raw + ((tile + 1) & 1) * kBufBytes, p.scale_log2);
                 __syncthreads();
             }
@@ -475,7 +493,10 @@ __global__ __launch_bounds__(kThreadsP, 2) void prefill_attn_kernel(PrefillParam
                 causal_base = x * kT;
             }
         }
-        attend_tile(cur, tvalid, causal_base, n, hh, qrow, qf, acc, m, l);
+        if (causal_base >= 0)
+            attend_tile<true>(cur, tvalid, causal_base, n, hh, qrow, qf, acc, m, l);
+        else
+            attend_tile<false>(cur, tvalid, causal_base, n, hh, qrow, qf, acc, m, l);
         if (tile + 1 < ntiles) stage_store(st, nxt, p.scale_log2);
         __syncthreads();
     }
