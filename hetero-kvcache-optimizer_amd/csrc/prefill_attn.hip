@@ -77,7 +77,20 @@ struct PrefillParams {
 
 // LDS addresses (bytes) of the swizzled tiles.
 __device__ __forceinline__ int k_addr(int tok, int chunk) { return tok * 256 + ((chunk ^ (tok & 15)) << 4); }
-__device__ __forceinline__ int vt_addr(int dim, int unit) { return kTileBytes + dim * 128 + ((unit ^ (dim & 15)) << 3); }
+// V^T rows hold the tile's 64 tokens in 8-byte units of 4 tokens.  Within each
+// 16-token group the units are stored in the order 0, 2, 1, 3, so that the 8 tokens
+// one lane feeds to a P.V product (tokens 4hh..4hh+3 and 8+4hh..8+4hh+3 of a group)
+// are one 16-byte read; the 16-byte pairs are XOR-swizzled by row against bank
+// conflicts.  vt_addr takes the natural unit index (token / 4).
+__device__ __forceinline__ int vt_unit(int unit) { return (unit & ~3) | ((unit & 1) << 1) | ((unit >> 1) & 1); }
+__device__ __forceinline__ int vt_addr(int dim, int unit) {
+    const int su = vt_unit(unit);
+    return kTileBytes + dim * 128 + ((((su >> 1) ^ (dim & 7)) << 4) | ((su & 1) << 3));
+}
+// The 16 bytes holding natural units 4gr + hh and 4gr + 2 + hh (gr = 16-token group).
+__device__ __forceinline__ int vt_pair_addr(int dim, int gr, int hh) {
+    return kTileBytes + dim * 128 + (((2 * gr + hh) ^ (dim & 7)) << 4);
+}
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return (uint32_t)f2h_rn(a) | ((uint32_t)f2h_rn(b) << 16);
@@ -354,15 +367,11 @@ __device__ __forceinline__ void attend_tile(const uint8_t* cur, int tvalid, int 
                 }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int unit0 = tb * 8 + 4 * u + hh;      // tokens tb*32 + 16u + 4hh (+8 for jj=1)
+            // tokens tb*32 + 16u + 4hh .. +3 and +8 .. +11: 16-token group 2tb + u
             h8 a[4];
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const int dim = 32 * db + n;
-                const u2 lo = *(const u2*)(cur + vt_addr(dim, unit0));
-                const u2 hi = *(const u2*)(cur + vt_addr(dim, unit0 + 2));
-                a[db] = __builtin_bit_cast(h8, u4{lo.x, lo.y, hi.x, hi.y});
-            }
+            for (int db = 0; db < 4; ++db)
+                a[db] = __builtin_bit_cast(h8, *(const u4*)(cur + vt_pair_addr(32 * db + n, 2 * tb + u, hh)));
 #pragma unroll
             for (int db = 0; db < 4; ++db) acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[db], P[u], acc[db], 0, 0, 0);
         }
