@@ -101,6 +101,12 @@ struct DecodeParams {
     int64_t part_pair_stride;  // floats between the partial blocks of consecutive pairs (256-byte multiple)
     int xcc_local;             // 1: all ranges of a pair run on one XCD (see above)
     int nxcc;                  // XCDs the dispatcher round-robins over
+    // optional score output (kScores): row (b, q head) holds the log2-domain score of
+    // every item [INT4 tokens | zone 0 | zone 1 | zone 2]; zone z starts at sc_zone[z]
+    float* scores;
+    int64_t sc_sb, sc_sh;
+    int sc_zone[HKV_MAX_F16_ZONES];
+    float* stats;              // [B][Hq][2]: the softmax max and sum of each row
 };
 
 // Partial states cross workgroups (and XCDs) through agent-scope relaxed atomic
@@ -261,9 +267,13 @@ __device__ __forceinline__ h8 k_operand(uint32_t w, h2 kz1024, h2 kz64) {
 // Two INT4 blocks (32 tokens) per step: the two QK chains interleave, and one
 // 16x16x32 MFMA per 16 dims does PV for both blocks (k slots 0..3 = block A
 // tokens 4g..4g+3, slots 4..7 = block B tokens 4g..4g+3).
+// With kScores, lanes of a valid head store the pair's eight scores (4 consecutive
+// tokens of each block) at sA / sB.
+template <bool kScores = false>
 __device__ __forceinline__ void step_int4_pair(const Int4Blk& A, const Int4Blk& B, int nA, int nB, int g, int kzsh,
                                                const h8 (&qf)[4], float scale_log2, f4 (&acc)[8], float& m,
-                                               float& l) {
+                                               float& l, bool store = false, float* sA = nullptr,
+                                               float* sB = nullptr) {
     const uint32_t kza = __builtin_amdgcn_ubfe(A.kz, kzsh, 8), kzb = __builtin_amdgcn_ubfe(B.kz, kzsh, 8);
     const h2 kA1024 = zp1024(kza, kza), kA64 = zp64(kza, kza);
     const h2 kB1024 = zp1024(kzb, kzb), kB64 = zp64(kzb, kzb);
@@ -305,6 +315,15 @@ __device__ __forceinline__ void step_int4_pair(const Int4Blk& A, const Int4Blk& 
             s[4 + v] = (4 * g + v < nB) ? SB[v] * (B.ks[v] * scale_log2) : -INFINITY;
         }
     }
+    if constexpr (kScores) {
+        if (store) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                if (4 * g + v < nA) sA[v] = s[v];
+                if (4 * g + v < nB) sB[v] = s[4 + v];
+            }
+        }
+    }
     float pr[8];
     softmax_update<8>(s, acc, m, l, pr);
     h8 P;
@@ -329,14 +348,23 @@ __device__ __forceinline__ void step_int4_pair(const Int4Blk& A, const Int4Blk& 
     }
 }
 
+template <bool kScores = false>
 __device__ __forceinline__ void step_f16(F16Tile& d, int nvalid, int g, const h8 (&qf)[4],
-                                         float scale_log2, f4 (&acc)[8], float& m, float& l) {
+                                         float scale_log2, f4 (&acc)[8], float& m, float& l, bool store = false,
+                                         float* sp = nullptr) {
     f4 S = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) S = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, d.k[j]), qf[j], S, 0, 0, 0);
     float s[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) s[v] = (4 * g + v < nvalid) ? S[v] * scale_log2 : -INFINITY;
+    if constexpr (kScores) {
+        if (store) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (4 * g + v < nvalid) sp[v] = s[v];
+        }
+    }
     float pr[4];
     softmax_update<4>(s, acc, m, l, pr);
     h4 P;
@@ -394,6 +422,20 @@ __device__ __forceinline__ void locate_tile(const DecodeParams& p, const ZoneTil
 // a SIMD do not progress at the same rate: the older one wins issue).  The result
 // then depends on which wave took which unit, in the last bits.  Otherwise wave w
 // takes units w, w + kWaves, ... and the result is bitwise reproducible.
+// Zone and tile of fp16 tile t counted over zones 0, 1, 2 in order.
+__device__ __forceinline__ void locate_zone(const ZoneTiles& im, int t, int& zi, int& tile) {
+    zi = 0;
+    if (t >= im.nt[0]) {
+        t -= im.nt[0];
+        zi = 1;
+        if (t >= im.nt[1]) {
+            t -= im.nt[1];
+            zi = 2;
+        }
+    }
+    tile = t;
+}
+
 template <bool kDynamic>
 __device__ __forceinline__ int next_unit(int* ctr, int& seq) {
     if constexpr (kDynamic) {
@@ -420,7 +462,7 @@ __device__ __forceinline__ int int4_splits(int nb4, int ntf, int nsplit) {
     return worst * 16 <= (ct + nsplit - 1) / nsplit * 17 ? s4 : 0;
 }
 
-template <bool kDynamic>
+template <bool kDynamic, bool kScores>
 __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const int BH = p.B * p.Hkv;
     const int bh = blockIdx.x % BH;
@@ -493,6 +535,8 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
 #pragma unroll
     for (int n = 0; n < 8; ++n) acc[n] = f4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.0f;
+    float* srow = nullptr;   // this lane's score row (kScores)
+    if constexpr (kScores) srow = p.scores + (int64_t)b * p.sc_sb + (int64_t)(h * nrep + min(c, nrep - 1)) * p.sc_sh;
 
     __shared__ __align__(16) int sm_ids[kIdWindow + 2];
     __shared__ int sm_ctr[2];   // next INT4 pair, next fp16 tile (kDynamic)
@@ -531,7 +575,16 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             do {
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
-                    step_f16(buf[k], tq[k] < nf ? min(kBlockTokens, lq[k]) : 0, g, qf, p.scale_log2, acc, m, l);
+                    if constexpr (kScores) {
+                        int zi, t;
+                        locate_zone(zt, f0 + min(tq[k], nf - 1), zi, t);
+                        float* sp = srow + (zi == 0 ? p.sc_zone[0] : zi == 1 ? p.sc_zone[1] : p.sc_zone[2]) +
+                                    t * kBlockTokens + 4 * g;
+                        step_f16<true>(buf[k], tq[k] < nf ? min(kBlockTokens, lq[k]) : 0, g, qf, p.scale_log2, acc,
+                                       m, l, c < nrep, sp);
+                    } else {
+                        step_f16(buf[k], tq[k] < nf ? min(kBlockTokens, lq[k]) : 0, g, qf, p.scale_log2, acc, m, l);
+                    }
                     tq[k] = next_unit<kDynamic>(&sm_ctr[1], seq);
                     int t;
                     locate_tile(p, zt, lenz, f0 + min(tq[k], nf - 1), zq[k], lq[k], t);
@@ -583,7 +636,12 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                     const int lb = wb + 2 * pk[k];
                     const int nA = pk[k] < npairs ? min(kBlockTokens, len4 - lb * kBlockTokens) : 0;
                     const int nB = (2 * pk[k] + 1 < wn) ? min(kBlockTokens, len4 - (lb + 1) * kBlockTokens) : 0;
-                    step_int4_pair(bufA[k], bufB[k], nA, nB, g, kzsh, qf, p.scale_log2, acc, m, l);
+                    if constexpr (kScores)
+                        step_int4_pair<true>(bufA[k], bufB[k], nA, nB, g, kzsh, qf, p.scale_log2, acc, m, l, c < nrep,
+                                             srow + lb * kBlockTokens + 4 * g,
+                                             srow + (lb + 1) * kBlockTokens + 4 * g);
+                    else
+                        step_int4_pair(bufA[k], bufB[k], nA, nB, g, kzsh, qf, p.scale_log2, acc, m, l);
                     pk[k] = nxt;
                     __builtin_amdgcn_sched_barrier(0);
                     load_int4(p, h, __builtin_amdgcn_readfirstlane((int)nid.x), nxt < npairs, c, g, bufA[k]);
@@ -638,6 +696,11 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         }
         if (nsplit == 1) {
             p.out[(int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d] = f2h_rn(L > 0.f ? O / L : 0.f);
+            if (kScores && d == 0) {
+                float* st = p.stats + ((int64_t)b * p.Hkv * nrep + h * nrep + hd) * 2;
+                st[0] = M;
+                st[1] = L;
+            }
         } else if (p.xcc_local) {
             part[hd * kPartStride + d] = O;
             if (d == 0) {
@@ -751,6 +814,11 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         uint16_t* op = p.out + (int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d4;
 #pragma unroll
         for (int v = 0; v < 4; ++v) op[v] = f2h_rn(O[v] * inv);
+        if (kScores && d4 == 0) {
+            float* st = p.stats + ((int64_t)b * p.Hkv * nrep + h * nrep + hd) * 2;
+            st[0] = M;
+            st[1] = L;
+        }
     }
     if (threadIdx.x == 0) {
         if (p.xcc_local)
@@ -853,6 +921,13 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
                 "hkv_decode_attn: num_f16_zones %d out of range", a->num_f16_zones);
     HKV_REQUIRE((a->flags & ~HKV_DECODE_DETERMINISTIC) == 0, HKV_ERR_ARG, "hkv_decode_attn: unknown flags 0x%x",
                 (unsigned)a->flags);
+    if (a->scores) {
+        HKV_REQUIRE(a->score_stats != nullptr, HKV_ERR_ARG, "hkv_decode_attn: scores without score_stats");
+        int64_t row = a->int4_max_len;
+        for (int i = 0; i < a->num_f16_zones; ++i) row += a->f16[i].max_len;
+        HKV_REQUIRE(a->scores_stride_h >= row && a->scores_stride_b >= (int64_t)a->num_q_heads * a->scores_stride_h,
+                    HKV_ERR_ARG, "hkv_decode_attn: score strides too small for %lld items per row", (long long)row);
+    }
     HKV_REQUIRE(a->q && a->out && a->workspace, HKV_ERR_ARG, "hkv_decode_attn: null q/out/workspace");
     HKV_REQUIRE((((uintptr_t)a->q) & 15) == 0 && (a->q_stride_b % 8) == 0 && (a->q_stride_h % 8) == 0,
                 HKV_ERR_ARG, "hkv_decode_attn: q must be 16-byte aligned with strides multiple of 8");
@@ -928,20 +1003,37 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     p.nxcc = num_xcc();
     p.xcc_local = (BH % p.nxcc) == 0 ? 1 : 0;
     p.max_splits = ms;
+    p.scores = a->scores;
+    p.sc_sb = a->scores_stride_b;
+    p.sc_sh = a->scores_stride_h;
+    p.stats = a->score_stats;
+    {
+        int base = a->int4_max_len;
+        for (int i = 0; i < HKV_MAX_F16_ZONES; ++i) {
+            p.sc_zone[i] = base;
+            if (i < a->num_f16_zones) base += a->f16[i].max_len;
+        }
+    }
     const size_t lds = lds_bytes(nrep);
     const bool det = (a->flags & HKV_DECODE_DETERMINISTIC) != 0;
-    const void* fn = det ? (const void*)decode_attn_kernel<false> : (const void*)decode_attn_kernel<true>;
-    static bool raised[2] = {false, false};   // the merge area plus the static id window can exceed 64 KB
-    if (!raised[det]) {
-        HKV_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
-        raised[det] = true;
+    const bool sc = a->scores != nullptr;
+    const int var = (det ? 0 : 1) + (sc ? 2 : 0);
+    static const void* const fns[4] = {(const void*)decode_attn_kernel<false, false>,
+                                       (const void*)decode_attn_kernel<true, false>,
+                                       (const void*)decode_attn_kernel<false, true>,
+                                       (const void*)decode_attn_kernel<true, true>};
+    static bool raised[4] = {false, false, false, false};   // the merge area plus the static id window can exceed 64 KB
+    if (!raised[var]) {
+        HKV_HIP_CHECK(hipFuncSetAttribute(fns[var], hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
+        raised[var] = true;
     }
-    if (det)
-        hipLaunchKernelGGL(decode_attn_kernel<false>, dim3((unsigned)(BH * ms)), dim3(kThreads), lds,
-                           (hipStream_t)stream, p);
-    else
-        hipLaunchKernelGGL(decode_attn_kernel<true>, dim3((unsigned)(BH * ms)), dim3(kThreads), lds,
-                           (hipStream_t)stream, p);
+    const dim3 grid((unsigned)(BH * ms)), block(kThreads);
+    switch (var) {
+        case 0: hipLaunchKernelGGL((decode_attn_kernel<false, false>), grid, block, lds, (hipStream_t)stream, p); break;
+        case 1: hipLaunchKernelGGL((decode_attn_kernel<true, false>), grid, block, lds, (hipStream_t)stream, p); break;
+        case 2: hipLaunchKernelGGL((decode_attn_kernel<false, true>), grid, block, lds, (hipStream_t)stream, p); break;
+        default: hipLaunchKernelGGL((decode_attn_kernel<true, true>), grid, block, lds, (hipStream_t)stream, p); break;
+    }
     HKV_LAUNCH_CHECK("decode_attn_kernel");
     return HKV_OK;
 }

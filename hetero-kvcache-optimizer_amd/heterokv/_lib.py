@@ -13,7 +13,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libheterokv.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_U8 = 0, 1, 2, 3
 MAX_F16_ZONES = 3
 DECODE_DETERMINISTIC = 1   # HKV_DECODE_DETERMINISTIC
@@ -76,7 +76,8 @@ class DecodeArgs(ctypes.Structure):
                 ("int4_lens", vp), ("int4_max_len", i32),
                 ("out", vp), ("out_stride_b", i64), ("out_stride_h", i64),
                 ("workspace", vp), ("workspace_bytes", ctypes.c_size_t), ("splits_hint", i32),
-                ("staging", vp), ("staging_blocks", i64), ("flags", i32)]
+                ("staging", vp), ("staging_blocks", i64), ("flags", i32),
+                ("scores", vp), ("scores_stride_b", i64), ("scores_stride_h", i64), ("score_stats", vp)]
 
 
 class PrefillArgs(ctypes.Structure):
@@ -130,6 +131,11 @@ SYMBOLS = [
     ("hkv_pf_stats", ctypes.c_int, [vp, ctypes.POINTER(PfStats)]),
     ("hkv_pf_synchronize", ctypes.c_int, [vp]),
     ("hkv_gather_blocks", ctypes.c_int, [vp, i64, vp, i64, vp, i64, i64, vp, vp, vp]),
+    ("hkv_attn_weights", ctypes.c_int, [vp, i64, i64, vp, i32, i32, i64, vp, vp, i64, i32, vp]),
+    ("hkv_block_scores", ctypes.c_int, [vp, i64, i32, vp, vp]),
+    ("hkv_eviction_workspace_bytes", ctypes.c_size_t, [i64, i32, i32, i32, i32]),
+    ("hkv_eviction_candidates", ctypes.c_int, [vp, i64, i32, i32, i32, i32, vp, ctypes.POINTER(i32), vp,
+                                                ctypes.c_size_t, vp]),
 ]
 
 _lock = threading.Lock()

@@ -44,7 +44,7 @@ class FusedHeteroCache(DynamicCache):
                  enable_quant: bool = True, enable_prefetch: bool = True, enable_triton: bool = True,
                  bandwidth_limiter=None, self_healing: bool = True, adaptive_self_healing: bool = False,
                  enable_method_d: bool = False, method_d_alpha: float = 1.0, fused_decode: bool = True,
-                 fused_prefill: bool = False):
+                 fused_prefill: bool = False, track_attention: bool = False):
         super().__init__()
         if adaptive_self_healing and not fused_decode:
             raise HeteroKVError(-4, "windowed retrieval (adaptive_self_healing) runs on the fused decode path; "
@@ -64,6 +64,9 @@ class FusedHeteroCache(DynamicCache):
         self.method_d_alpha = method_d_alpha
         self.fused_decode = fused_decode
         self.fused_prefill = fused_prefill
+        # feed the heavy-hitter oracle with the last layer's decode attention weights
+        # (engine_wrapper.py:165-180 intends this; the reference's patch never sets them)
+        self.track_attention = track_attention
         self._prefill_zone = None
         self._num_layers = num_layers
         self._manager: Optional[HeteroKVManager] = None
@@ -244,7 +247,9 @@ def heterokv_attention_forward(module, query, key, value, attention_mask, scalin
     route = getattr(key, "_hkv_route", None)
     if route is not None and query.shape[2] == 1:
         cache, layer_idx, include_dram = route
-        out = cache._manager.attend_decode(layer_idx, query, sm_scale=scaling, include_dram=include_dram)
+        feed = cache.track_attention and cache._num_layers is not None and layer_idx == cache._num_layers - 1
+        out = cache._manager.attend_decode(layer_idx, query, sm_scale=scaling, include_dram=include_dram,
+                                           feed_oracle=feed)
         return out.transpose(1, 2).contiguous(), None
     pre = getattr(key, "_hkv_prefill", None)
     if pre is not None and query.shape[2] == key.shape[2] - pre[1]:

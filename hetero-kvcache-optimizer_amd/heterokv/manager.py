@@ -31,6 +31,7 @@ import torch
 
 from . import ops
 from ._lib import BLOCK_TOKENS, HEAD_DIM, HeteroKVError
+from .heavy_hitter import HeavyHitterOracle
 from .kv_compressor import KVCompressor
 from .prefetcher import AdaptivePrefetchController, Prefetcher
 
@@ -173,6 +174,9 @@ class HeteroKVManager:
         self.retrieval_window: Any = None
         self._adaptive_controller = AdaptivePrefetchController()
         self._last_attention_weights: Optional[torch.Tensor] = None
+        # cumulative attention scores (manager.py:102-106); fed by update_attention_scores
+        # or attend_decode(feed_oracle=True)
+        self._oracle = HeavyHitterOracle(block_size=16, sink_tokens=sink_tokens, local_window=hbm_budget_tokens)
 
     # ---------------------------------------------------------------- helpers
     @property
@@ -312,7 +316,13 @@ class HeteroKVManager:
             st.int4_pos.extend(first_pos)
         st.int4_len += n
         self._chunk_eviction_order.append(key)
-        self._chunk_attention_scores[key] = 1.0 / (self._eviction_counter + 1)
+        scores = self._oracle.token_scores
+        if scores is not None:
+            # manager.py:1262-1268: the mean oracle score of tokens [counter * n, +n)
+            part = scores[self._eviction_counter * n:(self._eviction_counter + 1) * n]
+            self._chunk_attention_scores[key] = float(part.mean().item()) if part.numel() > 0 else 0.0
+        else:
+            self._chunk_attention_scores[key] = 1.0 / (self._eviction_counter + 1)
         if layer == 0:
             self._eviction_counter += 1
 
@@ -643,7 +653,7 @@ class HeteroKVManager:
 
     # ---------------------------------------------------------------- fused decode
     def attend_decode(self, layer_idx: int, query_states: torch.Tensor, sm_scale: Optional[float] = None,
-                      include_dram: bool = True) -> torch.Tensor:
+                      include_dram: bool = True, feed_oracle: bool = False) -> torch.Tensor:
         """softmax(q K^T * sm_scale) V over [INT4 middle (if include_dram) | sink | tail |
         heavy hitters] of the layer, in one split-K launch (hkv_decode_attn).  With a host
         tier, the layer's host records are copied into a staging buffer on the prefetcher's
@@ -681,17 +691,54 @@ class HeteroKVManager:
         if staged:
             self._pf.wait(slot)
         q16 = _as16(query_states)
+        scores = stats = None
+        if feed_oracle:
+            n_items = n4 + sum(z[2] for z in zones)
+            scores = torch.full((q16.shape[0], q16.shape[1], max(n_items, 1)), float("-inf"),
+                                dtype=torch.float32, device=q16.device)
+            stats = torch.empty((q16.shape[0], q16.shape[1], 2), dtype=torch.float32, device=q16.device)
         out = ops.decode_attention(q16, zones=zones, pool=st.pool if n4 else None,
                                    block_table=bt if n4 else None, int4_max_len=n4,
                                    sm_scale=sm_scale, workspace=self._workspace,
                                    staging=self._staging[buf] if staged else None,
-                                   deterministic=self.deterministic_decode)
+                                   deterministic=self.deterministic_decode, scores=scores, score_stats=stats)
+        if feed_oracle:
+            w = ops.attn_weights(scores[:1], stats[:1], order=self._score_order(st, n4))
+            self.update_attention_scores(w[0])
         if staged:
             self._pf.mark(slot)
             self._pending.pop(layer_idx, None)
             self._waited.append(slot)
         self._selection_of.pop(layer_idx, None)
         return out.to(query_states.dtype)
+
+    # ---------------------------------------------------------------- heavy-hitter scores
+    def update_attention_scores(self, attention_weights: torch.Tensor) -> None:
+        """manager.py:319-329: feed the newest token's attention weights to the oracle and
+        keep them for the adaptive window controller."""
+        self._oracle.update(attention_weights)
+        self._last_attention_weights = attention_weights.detach().clone()
+
+    def get_oracle_scores(self) -> Optional[torch.Tensor]:
+        """manager.py:331-333: the oracle's cumulative per-token scores."""
+        return self._oracle.token_scores
+
+    def _score_order(self, st: "_LayerState", n4: int) -> torch.Tensor:
+        """Decode score items in the order the reference concatenates the attended tokens:
+        the INT4 tokens (eviction order), the sink, the recent window oldest first, the
+        heavy hitters.  Items are indexed as attend_decode lays them out: INT4 tokens,
+        then the sink, tail-ring and heavy-hitter slots."""
+        parts = [torch.arange(n4, dtype=torch.int64)]
+        base = n4
+        if st.sink_len:
+            parts.append(base + torch.arange(st.sink_len, dtype=torch.int64))
+            base += st.sink_len
+        if st.tail_len:
+            parts.append(base + (st.tail_head + torch.arange(st.tail_len, dtype=torch.int64)) % st.ring)
+            base += st.tail_len
+        if st.hh_len:
+            parts.append(base + torch.arange(st.hh_len, dtype=torch.int64))
+        return torch.cat(parts).to(self.device)
 
     # ---------------------------------------------------------------- summaries
     def memory_summary(self) -> Dict[str, Any]:

@@ -285,7 +285,8 @@ def _int4_source(pool, staging):
 
 
 def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
-                     sm_scale=None, workspace=None, out=None, splits=0, staging=None, deterministic=False):
+                     sm_scale=None, workspace=None, out=None, splits=0, staging=None, deterministic=False,
+                     scores=None, score_stats=None):
     """Split-K decode attention over fp16 zones and the INT4 pool.
 
     q: [B, Hq, 128] or [B, Hq, 1, 128] fp16.
@@ -297,6 +298,10 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
     deterministic: fixed block-to-wave assignment, bitwise reproducible output.  The
     default hands blocks to waves on demand (faster); outputs can then differ from
     run to run in the last bits.
+    scores / score_stats: optional fp32 outputs [B, Hq, n_items] (n_items >= int4_max_len
+    plus the zones' max lengths; item order INT4 tokens, then each zone's slots) and
+    [B, Hq, 2]: the log2-domain score of every item and each row's softmax max and sum
+    (feeds attn_weights).  Items past a sequence's lengths are left untouched.
     Returns fp16 [B, Hq, 128] (or [B, Hq, 1, 128] if q was 4-D).
     """
     _require_gpu(q)
@@ -359,6 +364,16 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     a.splits_hint = int(splits)
     a.flags = _lib.DECODE_DETERMINISTIC if deterministic else 0
+    if scores is not None:
+        _require_gpu(scores, score_stats)
+        if score_stats is None or scores.dtype != torch.float32 or score_stats.dtype != torch.float32:
+            raise HeteroKVError(-1, "decode_attention: scores and score_stats must be fp32 tensors")
+        if scores.dim() != 3 or tuple(scores.shape[:2]) != (B, Hq) or scores.stride(2) != 1 or \
+                tuple(score_stats.shape) != (B, Hq, 2) or not score_stats.is_contiguous():
+            raise HeteroKVError(-1, "decode_attention: scores [B, Hq, n] (unit item stride) and "
+                                    "score_stats [B, Hq, 2] expected")
+        a.scores, a.scores_stride_b, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
+        a.score_stats = score_stats.data_ptr()
     check(load().hkv_decode_attn(ctypes.byref(a), stream_ptr(dev)), "hkv_decode_attn")
     return out.unsqueeze(2) if squeeze else out
 
@@ -388,6 +403,62 @@ def gather_blocks(src, ids, dst, staging=None, dst_offset=0):
                                    ids.data_ptr(), n, rb, dst.data[dst_offset].data_ptr(), dst.err.data_ptr(),
                                    stream_ptr(dev)), "hkv_gather_blocks")
     return dst
+
+
+# ----------------------------------------------------------------------- heavy-hitter scoring
+def attn_weights(scores, score_stats, order=None, out=None, accumulate=False):
+    """Attention weights of the newest token averaged over heads (hkv_attn_weights).
+
+    scores [B, H, n] / score_stats [B, H, 2]: a decode launch's score outputs.  order:
+    optional int64 [m] item indices (negative: weight 0).  Returns fp32 [B, m] (or adds
+    into out when accumulate)."""
+    _require_gpu(scores, score_stats)
+    B, H, n = scores.shape
+    dev = scores.device
+    if order is not None:
+        order = order.to(device=dev, dtype=torch.int64).contiguous().reshape(-1)
+        m = order.numel()
+    else:
+        m = n
+    if out is None:
+        out = torch.empty((B, m), dtype=torch.float32, device=dev)
+        accumulate = False
+    if out.dtype != torch.float32 or out.dim() != 2 or out.shape[0] != B or out.shape[1] < m or out.stride(1) != 1:
+        raise HeteroKVError(-1, "attn_weights: out must be fp32 [B, >= %d] with unit stride" % m)
+    check(load().hkv_attn_weights(scores.data_ptr(), scores.stride(0), scores.stride(1), score_stats.data_ptr(),
+                                  B, H, m, order.data_ptr() if order is not None else None, out.data_ptr(),
+                                  out.stride(0), 1 if accumulate else 0, stream_ptr(dev)), "hkv_attn_weights")
+    return out
+
+
+def block_scores(token_scores, seq_len, block_size):
+    """Mean score of each block of block_size tokens (hkv_block_scores): fp32 [ceil(seq_len / bs)]."""
+    _require_gpu(token_scores)
+    ts = token_scores.contiguous()
+    if ts.dtype != torch.float32 or ts.numel() < seq_len:
+        raise HeteroKVError(-1, "block_scores: fp32 token scores with at least seq_len entries expected")
+    nb = (seq_len + block_size - 1) // block_size
+    out = torch.empty(nb, dtype=torch.float32, device=ts.device)
+    check(load().hkv_block_scores(ts.data_ptr(), seq_len, block_size, out.data_ptr(), stream_ptr(ts.device)),
+          "hkv_block_scores")
+    return out
+
+
+def eviction_candidates(token_scores, seq_len, block_size, sink_tokens, local_window, max_blocks):
+    """Lowest-mean unprotected blocks, ascending (hkv_eviction_candidates): int64 [k]."""
+    _require_gpu(token_scores)
+    ts = token_scores.contiguous()
+    if ts.dtype != torch.float32 or ts.numel() < seq_len:
+        raise HeteroKVError(-1, "eviction_candidates: fp32 token scores with at least seq_len entries expected")
+    lib = load()
+    wsb = lib.hkv_eviction_workspace_bytes(seq_len, block_size, sink_tokens, local_window, max_blocks)
+    ws = torch.empty(max(wsb, 8), dtype=torch.uint8, device=ts.device)
+    out = torch.empty(max(max_blocks, 1), dtype=torch.int64, device=ts.device)
+    k = _lib.i32(0)
+    check(lib.hkv_eviction_candidates(ts.data_ptr(), seq_len, block_size, sink_tokens, local_window, max_blocks,
+                                      out.data_ptr(), ctypes.byref(k), ws.data_ptr(), ws.numel(),
+                                      stream_ptr(ts.device)), "hkv_eviction_candidates")
+    return out[:k.value]
 
 
 # ----------------------------------------------------------------------- prefill attention

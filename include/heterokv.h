@@ -65,7 +65,7 @@
 extern "C" {
 #endif
 
-#define HKV_ABI_VERSION 3
+#define HKV_ABI_VERSION 4
 
 /* dtype codes */
 #define HKV_DTYPE_F16  0
@@ -247,6 +247,15 @@ typedef struct HkvDecodeArgs {
     const uint8_t* staging;        /* records addressed by negative block ids (may be NULL) */
     int64_t staging_blocks;
     int32_t flags;                 /* HKV_DECODE_* bits */
+    /* Optional score output (NULL: none).  Row (b, q head) at scores + b * scores_stride_b
+     * + head * scores_stride_h receives the log2-domain score (q.k * sm_scale * log2 e) of
+     * every item: INT4 tokens [0, int4_max_len), then each fp16 zone's slots
+     * [0, f16[i].max_len) in zone order.  Items past a sequence's lengths are not written.
+     * score_stats [batch][num_q_heads][2] receives each row's softmax max and sum, so that
+     * exp2(score - max) / sum is the attention probability.  Feeds hkv_attn_weights. */
+    float* scores;
+    int64_t scores_stride_b, scores_stride_h;
+    float* score_stats;
 } HkvDecodeArgs;
 
 /* Decode flag: every wave of a range takes a fixed subset of the range's blocks, so
@@ -358,6 +367,38 @@ int hkv_pf_synchronize(HkvPrefetcher* pf);
 int hkv_gather_blocks(const uint8_t* src_pool, int64_t src_blocks, const uint8_t* src_staging,
                       int64_t staging_blocks, const int32_t* ids, int64_t n, int64_t record_bytes,
                       uint8_t* dst, int32_t* err_flag, void* stream);
+
+/*
+ * Heavy-hitter scoring (src/policy/heavy_hitter.py:26-101, src/kernels/oracle_triton.py:16-79).
+ *
+ * hkv_attn_weights: the attention weights of the newest token, averaged over heads,
+ * from a decode launch's scores and score_stats (HkvDecodeArgs):
+ *   out[b][t] (+)= (1/num_heads) sum_h exp2(scores[b][h][order[t]] - max[b][h]) / sum[b][h]
+ * for t < n_items (order NULL: the identity; order[t] < 0: weight 0).  With
+ * accumulate != 0 the weights are added to out (HeavyHitterOracle.update); otherwise
+ * they replace it.  This is the [seq_len] vector the reference's attention patch hands
+ * to the oracle (fused_attention_patch.py:104-107), one row per sequence.
+ */
+int hkv_attn_weights(const float* scores, int64_t scores_stride_b, int64_t scores_stride_h,
+                     const float* score_stats, int32_t batch, int32_t num_heads, int64_t n_items,
+                     const int64_t* order, float* out, int64_t out_stride_b, int32_t accumulate,
+                     void* stream);
+
+/* compute_block_scores: out[i] = mean of token_scores over block i of block_size tokens
+ * (the last block may be partial); ceil(seq_len / block_size) outputs. */
+int hkv_block_scores(const float* token_scores, int64_t seq_len, int32_t block_size, float* out, void* stream);
+
+/* HeavyHitterOracle.get_eviction_candidates with scores present: the max_blocks blocks
+ * with the lowest mean score, ascending (equal means: lower index first), never one of
+ * the first ceil(sink_tokens / block_size) or last ceil(local_window / block_size)
+ * blocks.  *num_out (set on the host, no sync) = min(max_blocks, unprotected blocks),
+ * 0 when seq_len <= sink_tokens + local_window; out receives that many int64 block
+ * indices.  The workspace is hkv_eviction_workspace_bytes(...) bytes, 8-byte aligned. */
+size_t hkv_eviction_workspace_bytes(int64_t seq_len, int32_t block_size, int32_t sink_tokens,
+                                    int32_t local_window, int32_t max_blocks);
+int hkv_eviction_candidates(const float* token_scores, int64_t seq_len, int32_t block_size,
+                            int32_t sink_tokens, int32_t local_window, int32_t max_blocks, int64_t* out,
+                            int32_t* num_out, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }
