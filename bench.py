@@ -253,6 +253,72 @@ def bench_paged(torch, ops, args):
     print(json.dumps(line), flush=True)
 
 
+def bench_scoring(torch, ops, args):
+    """Heavy-hitter scoring on the 32K decode workload: the decode launch with score
+    outputs against the plain one, the head-averaged weights of the newest token
+    (hkv_attn_weights, 32 heads x 32768 items) and the eviction candidates of a 131072-token
+    score board (8192 blocks of 16, sink 64, local 4096, 64 candidates)."""
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    q, K, V = make_inputs(torch)
+    R = args.copies
+    copies = [build_copy(torch, ops, q, K, V, dev) for _ in range(R)]
+    q_dev = q.to(dev)
+    out = torch.empty((B, HQ, D), dtype=torch.float16, device=dev)
+    ws = ops.DecodeWorkspace(dev)
+    n_items = MID + SINK + RECENT
+    scores = torch.full((B, HQ, n_items), float("-inf"), dtype=torch.float32, device=dev)
+    stats = torch.empty((B, HQ, 2), dtype=torch.float32, device=dev)
+    board = torch.zeros(131072, dtype=torch.float32, device=dev)
+    board += torch.rand(131072, device=dev, generator=torch.Generator(device=dev).manual_seed(3))
+    wts = torch.zeros((1, n_items), dtype=torch.float32, device=dev)
+
+    def dec(i, with_scores):
+        c = copies[i % R]
+        ops.decode_attention(q_dev, zones=c["zones"], pool=c["pool"], block_table=c["bt"], int4_max_len=MID,
+                             workspace=ws, out=out, scores=scores if with_scores else None,
+                             score_stats=stats if with_scores else None)
+
+    def timed(fn, n):
+        for i in range(max(args.warmup, 2)):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            fn(i)
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+
+    n = max(args.steps, 16)
+    us_plain = timed(lambda i: dec(i, False), n)
+    us_scores = timed(lambda i: dec(i, True), n)
+    us_weights = timed(lambda i: ops.attn_weights(scores, stats, out=wts, accumulate=True), n)
+    us_cand = timed(lambda i: ops.eviction_candidates(board, 131072, 16, 64, 4096, 64), max(n // 8, 8))
+    got = ops.eviction_candidates(board, 131072, 16, 64, 4096, 64).cpu().tolist()
+    blk = board.view(8192, 16).double().mean(1).cpu().numpy()
+    blk[:4] = float("inf")
+    blk[8192 - 256:] = float("inf")
+    want = sorted(range(8192), key=lambda i: (blk[i], i))[:64]
+    line = {
+        "metric": "heavy-hitter scoring cost per decode step at 32K ctx (us)",
+        "value": round(us_scores - us_plain + us_weights, 3), "unit": "us", "n_gpus": 1, "steps": n,
+        "warmup": args.warmup, "ms_per_step": round((us_scores + us_weights) * 1e-3, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (the 32K decode workload's seeded K/V; uniform random score board)",
+        "config": {"workload": "decode with score outputs (32 q / 8 kv heads, ctx 32768) + head-averaged weights "
+                               "of the newest token + 64 eviction candidates over 131072 scored tokens",
+                   "decode_us": round(us_plain, 3), "decode_with_scores_us": round(us_scores, 3),
+                   "attn_weights_us": round(us_weights, 3), "eviction_candidates_us": round(us_cand, 3),
+                   "score_bytes_written": B * HQ * n_items * 4,
+                   "candidates_match_float64_means": got == want},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 T_LAYERS, T_HQ, T_HKV, T_HIDDEN, T_INTER, T_VOCAB = 28, 28, 4, 3584, 18944, 152064
 T_CTX, T_CHUNK, T_SINK, T_KEEP, T_HOST_FRAC = 131072, 2048, 64, 4160, 0.75
 
@@ -473,7 +539,7 @@ def main():
                     help="decode with the fixed block-to-wave schedule (bitwise reproducible)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged", "scoring"], default="decode",
                     help="decode: the headline single-layer decode (default); prefill: the chunked-prefill "
                          "kernel on a 2048-token chunk over 64 + 131072 INT4 + 4096 tokens (MFMA bound); "
                          "tiered: end-to-end 28-layer decode at 131072 tokens with 75%% of the INT4 KV in "
@@ -510,6 +576,8 @@ def main():
         return bench_tiered(torch, args)
     if args.workload == "paged":
         return bench_paged(torch, ops, args)
+    if args.workload == "scoring":
+        return bench_scoring(torch, ops, args)
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

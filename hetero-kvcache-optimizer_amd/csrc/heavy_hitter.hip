@@ -30,21 +30,32 @@ struct WeightsParams {
     int accumulate;
 };
 
+constexpr int kMaxWeightHeads = 256;
+
 __global__ __launch_bounds__(256) void attn_weights_kernel(WeightsParams p) {
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    // each row's max and 1 / sum, once per workgroup
+    __shared__ float sm_m[kMaxWeightHeads], sm_inv[kMaxWeightHeads];
     const int b = blockIdx.y;
+    for (int h = threadIdx.x; h < p.H; h += 256) {
+        const float* st = p.stats + ((int64_t)b * p.H + h) * 2;
+        const float L = st[1];
+        sm_m[h] = st[0];
+        sm_inv[h] = L > 0.f ? 1.0f / L : 0.f;
+    }
+    __syncthreads();
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= p.n) return;
     const int64_t item = p.order ? p.order[t] : t;
     float w = 0.f;
     if (item >= 0) {
-        const float* st = p.stats + (int64_t)b * p.H * 2;
         const float* s = p.scores + (int64_t)b * p.sb + item;
+#pragma unroll 8
         for (int h = 0; h < p.H; ++h) {
             const float x = s[(int64_t)h * p.sh];
-            const float L = st[2 * h + 1];
-            if (x != -INFINITY && L > 0.f) w += exp2f(x - st[2 * h]) / L;
+            // exp2(-inf) = 0: masked items add nothing
+            w += __builtin_amdgcn_exp2f(x - sm_m[h]) * sm_inv[h];
         }
-        w /= (float)p.H;
+        w *= 1.0f / (float)p.H;
     }
     float* o = p.out + (int64_t)b * p.ob + t;
     *o = p.accumulate ? *o + w : w;
@@ -128,10 +139,14 @@ int pow2_at_least(int64_t x) {
     return p;
 }
 
-// Candidate count and protected range, as get_eviction_candidates decides them.
+// Candidate count and protected range, as get_eviction_candidates decides them, and
+// the sort layout: chunks of `chunk` keys sorted by one workgroup each; with more than
+// one chunk, each keeps its first k keys and one more workgroup sorts those.
 struct EvictPlan {
     int64_t nblocks, prot_lo, prot_hi;
     int k;
+    int chunk;
+    int64_t nchunks;
 };
 
 EvictPlan plan_eviction(int64_t seq_len, int bs, int sink, int local, int k) {
@@ -143,13 +158,19 @@ EvictPlan plan_eviction(int64_t seq_len, int bs, int sink, int local, int k) {
     e.prot_hi = e.nblocks - lb > 0 ? e.nblocks - lb : 0;
     const int64_t unsafe = e.nblocks - sb - lb > 0 ? e.nblocks - sb - lb : 0;
     e.k = (int)(k < unsafe ? k : unsafe);
+    // small chunks sort in parallel; a chunk holds at least 8k keys so that the merge
+    // pass stays small
+    int c = 512;
+    while (c < kSortMax && c < 8ll * e.k) c <<= 1;
+    while (c < kSortMax && ((e.nblocks + c - 1) / c) * (int64_t)e.k > kSortMax) c <<= 1;
+    e.chunk = c;
+    e.nchunks = e.k > 0 ? (e.nblocks + c - 1) / c : 0;
     return e;
 }
 
 size_t evict_workspace(const EvictPlan& e) {
     if (e.k <= 0) return 0;
-    const int64_t nchunks = (e.nblocks + kSortMax - 1) / kSortMax;
-    return (size_t)e.nblocks * 8 + (nchunks > 1 ? (size_t)nchunks * e.k * 8 : 0);
+    return (size_t)e.nblocks * 8 + (e.nchunks > 1 ? (size_t)e.nchunks * e.k * 8 : 0);
 }
 
 bool sort_lds_raised = false;
@@ -170,6 +191,8 @@ extern "C" int hkv_attn_weights(const float* scores, int64_t scores_stride_b, in
     HKV_REQUIRE(out_stride_b >= n_items, HKV_ERR_ARG, "hkv_attn_weights: out stride %lld < %lld items",
                 (long long)out_stride_b, (long long)n_items);
     HKV_REQUIRE(batch < 65536, HKV_ERR_ARG, "hkv_attn_weights: batch too large");
+    HKV_REQUIRE(num_heads <= kMaxWeightHeads, HKV_ERR_UNSUPPORTED, "hkv_attn_weights: more than %d heads",
+                kMaxWeightHeads);
     WeightsParams p{scores, scores_stride_b, scores_stride_h, score_stats, batch, num_heads, n_items,
                     order, out, out_stride_b, accumulate ? 1 : 0};
     hipLaunchKernelGGL(attn_weights_kernel, dim3((unsigned)((n_items + 255) / 256), (unsigned)batch), dim3(256), 0,
@@ -213,7 +236,7 @@ extern "C" int hkv_eviction_candidates(const float* token_scores, int64_t seq_le
                 HKV_ERR_CAPACITY, "hkv_eviction_candidates: workspace %zu bytes, need %zu (8-byte aligned)",
                 workspace_bytes, evict_workspace(e));
     HKV_REQUIRE(e.nblocks < (1ll << 32), HKV_ERR_UNSUPPORTED, "hkv_eviction_candidates: too many blocks");
-    const int64_t nchunks = (e.nblocks + kSortMax - 1) / kSortMax;
+    const int64_t nchunks = e.nchunks;
     HKV_REQUIRE(nchunks == 1 || nchunks * e.k <= kSortMax, HKV_ERR_UNSUPPORTED,
                 "hkv_eviction_candidates: %lld blocks with %d candidates exceed one merge pass",
                 (long long)e.nblocks, e.k);
@@ -230,13 +253,13 @@ extern "C" int hkv_eviction_candidates(const float* token_scores, int64_t seq_le
     if (nchunks == 1) {
         const int pw = pow2_at_least(e.nblocks);
         hipLaunchKernelGGL(sort_take_kernel, dim3(1), dim3(kSortThreads), (size_t)pw * 8, (hipStream_t)stream, keys,
-                           e.nblocks, kSortMax, pw, e.k, (uint64_t*)nullptr, out);
+                           e.nblocks, e.chunk, pw, e.k, (uint64_t*)nullptr, out);
         HKV_LAUNCH_CHECK("sort_take_kernel");
         return HKV_OK;
     }
     uint64_t* cand = keys + e.nblocks;
-    hipLaunchKernelGGL(sort_take_kernel, dim3((unsigned)nchunks), dim3(kSortThreads), (size_t)kSortMax * 8,
-                       (hipStream_t)stream, keys, e.nblocks, kSortMax, kSortMax, e.k, cand, (int64_t*)nullptr);
+    hipLaunchKernelGGL(sort_take_kernel, dim3((unsigned)nchunks), dim3(kSortThreads), (size_t)e.chunk * 8,
+                       (hipStream_t)stream, keys, e.nblocks, e.chunk, e.chunk, e.k, cand, (int64_t*)nullptr);
     HKV_LAUNCH_CHECK("sort_take_kernel");
     const int64_t nc = nchunks * e.k;
     const int pw = pow2_at_least(nc);
