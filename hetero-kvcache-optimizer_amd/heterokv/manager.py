@@ -728,17 +728,19 @@ class HeteroKVManager:
         the INT4 tokens (eviction order), the sink, the recent window oldest first, the
         heavy hitters.  Items are indexed as attend_decode lays them out: INT4 tokens,
         then the sink, tail-ring and heavy-hitter slots."""
-        parts = [torch.arange(n4, dtype=torch.int64)]
+        dev = self.device   # built on the device: no host-to-device copy per step
+        parts = [torch.arange(n4, dtype=torch.int64, device=dev)]
         base = n4
         if st.sink_len:
-            parts.append(base + torch.arange(st.sink_len, dtype=torch.int64))
+            parts.append(torch.arange(base, base + st.sink_len, dtype=torch.int64, device=dev))
             base += st.sink_len
         if st.tail_len:
-            parts.append(base + (st.tail_head + torch.arange(st.tail_len, dtype=torch.int64)) % st.ring)
+            parts.append(base + (torch.arange(st.tail_head, st.tail_head + st.tail_len, dtype=torch.int64,
+                                              device=dev) % st.ring))
             base += st.tail_len
         if st.hh_len:
-            parts.append(base + torch.arange(st.hh_len, dtype=torch.int64))
-        return torch.cat(parts).to(self.device)
+            parts.append(torch.arange(base, base + st.hh_len, dtype=torch.int64, device=dev))
+        return torch.cat(parts)
 
     # ---------------------------------------------------------------- summaries
     def memory_summary(self) -> Dict[str, Any]:
