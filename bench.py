@@ -359,6 +359,19 @@ def _decode_tokens(torch, model, cache, tok, pos, n, dev):
     return tok, pos, times, stats
 
 
+def _decode_tokens_graph(torch, runner, tok, pos, n, dev):
+    """_decode_tokens through a DecodeGraph (one captured decode step replayed per token)."""
+    times = []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        logits = runner.step(tok, torch.tensor([[pos]], device=dev))
+        tok = logits[:, -1:].argmax(-1)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        pos += 1
+    return tok, pos, times, []
+
+
 def _summ(times, stats):
     import statistics
     t = statistics.median(times)
@@ -431,7 +444,7 @@ def bench_tiered(torch, args):
     """End-to-end tiered decode at 131072 tokens: chunked prefill (2048-token chunks, fused
     prefill kernel), then 75% of every layer's INT4 block records moved to pinned host memory;
     decode with each layer's host records copied on the side stream one layer ahead."""
-    from heterokv.engine_wrapper import ChunkedPrefillEngine, FusedHeteroCache
+    from heterokv.engine_wrapper import ChunkedPrefillEngine, DecodeGraph, FusedHeteroCache
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     t0 = time.perf_counter()
@@ -461,6 +474,15 @@ def bench_tiered(torch, args):
         tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, args.steps, dev)
         out["resident"] = _summ(tm, st)
         print("[tiered] resident: %s" % out["resident"], file=sys.stderr, flush=True)
+        # the same with each decode step captured once in a HIP graph and replayed
+        # (device-stepped zones: no per-token host work besides bookkeeping)
+        runner = DecodeGraph(model, cache)
+        tok, pos, _, _ = _decode_tokens_graph(torch, runner, tok, pos, max(args.warmup, 3), dev)
+        tok, pos, tm, st = _decode_tokens_graph(torch, runner, tok, pos, args.steps, dev)
+        out["resident_graph"] = _summ(tm, st)
+        runner.close()
+        del runner
+        print("[tiered] resident, graph replay: %s" % out["resident_graph"], file=sys.stderr, flush=True)
         moved = cache.offload_to_host(T_HOST_FRAC, seed=0)
         torch.cuda.synchronize()
         host_bytes = mgr.memory_summary()["host_bytes"]

@@ -26,12 +26,14 @@
 // (atomic ticket after a release fence) merges the S partial states with
 // independent loads and writes the output, so the whole op is one launch.
 // Workgroup ids interleave the pairs so that all ranges of a pair land on one
-// XCD (dispatch is round-robin over XCDs by workgroup id).  When every range of
-// a pair shares an XCD (pairs a multiple of the XCD count), the hand-off stays
-// in that XCD's L2: plain stores, an L2 atomic ticket and L1-bypassing loads.
-// Otherwise it goes through memory with agent-scope (sc1) accesses.  Each
-// workgroup checks its XCD id against the assumed placement and reports a
-// mismatch in the error word (bit 2).
+// XCD: dispatch is round-robin over XCDs by workgroup id (the XCD that takes
+// workgroup 0 rotates from launch to launch, so only the id modulo the XCD count
+// is fixed).  When every range of a pair shares an XCD (pairs a multiple of the
+// XCD count), the hand-off stays in that XCD's L2: plain stores, an L2 atomic
+// ticket and L1-bypassing loads.  Otherwise it goes through memory with
+// agent-scope (sc1) accesses.  Each range tags its L2 partial state with its XCD
+// id; the merging workgroup reports a tag that is not its own in the error word
+// (bit 2) and clears the tags.
 #include "hkv_internal.h"
 #include "nibble_decode.h"
 
@@ -462,6 +464,30 @@ __device__ __forceinline__ int int4_splits(int nb4, int ntf, int nsplit) {
     return worst * 16 <= (ct + nsplit - 1) / nsplit * 17 ? s4 : 0;
 }
 
+// Partial states s0 + j K (j < 8) of head hd for the final merge: m, l and
+// float4 d4 of o.  Splits past the end read the last split again and get
+// m = -inf, so that every load is issued unconditionally.  kL2: XCD-local
+// hand-off (L1-bypassing buffer loads), else agent-scope loads.
+template <bool kL2>
+__device__ __forceinline__ void load_partials(__amdgpu_buffer_rsrc_t prs, const float* parts, int s0, int K,
+                                              int nsplit, int nrep, int hd, int d4, float* ms, float* ls, f4* os) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int sj = s0 + j * K;
+        const int off = min(sj, nsplit - 1) * (nrep * kPartStride) + hd * kPartStride;
+        if constexpr (kL2) {
+            ms[j] = sj < nsplit ? ld_l2(prs, (off + kHeadDim) * 4) : -INFINITY;
+            ls[j] = ld_l2(prs, (off + kHeadDim + 1) * 4);
+            os[j] = ld_l2_f4(prs, (off + d4) * 4);
+        } else {
+            const float* ps = parts + off;
+            ms[j] = sj < nsplit ? ld_agent(ps + kHeadDim) : -INFINITY;
+            ls[j] = ld_agent(ps + kHeadDim + 1);
+            os[j] = f4{ld_agent(ps + d4), ld_agent(ps + d4 + 1), ld_agent(ps + d4 + 2), ld_agent(ps + d4 + 3)};
+        }
+    }
+}
+
 template <bool kDynamic, bool kScores>
 __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const int BH = p.B * p.Hkv;
@@ -474,10 +500,8 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const int c = lane & 15, g = lane >> 4;
     const int kzsh = 8 * (c & 3);
     const int nrep = p.nrep;
-    if (p.xcc_local && p.nxcc > 1 && threadIdx.x == 0) {
-        const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15;   // HW_REG_XCC_ID
-        if (xcc % p.nxcc != (int)(blockIdx.x % p.nxcc) && p.err) atomicOr(p.err, 4);
-    }
+    // this workgroup's XCD (HW_REG_XCC_ID); tags its partial state in the L2 hand-off
+    const int xcc_tag = p.xcc_local ? (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15) + 1 : 0;
 
     const int len4 = p.int4_lens ? min(max(p.int4_lens[b], 0), p.int4_max_len) : p.int4_max_len;
     int lenz[HKV_MAX_F16_ZONES];
@@ -706,6 +730,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             if (d == 0) {
                 part[hd * kPartStride + kHeadDim] = M;
                 part[hd * kPartStride + kHeadDim + 1] = L;
+                if (hd == 0) reinterpret_cast<int*>(part)[kHeadDim + 2] = xcc_tag;
             }
         } else {
             st_agent(part + hd * kPartStride + d, O);
@@ -741,6 +766,13 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const float* parts = p.partials + (int64_t)bh * p.part_pair_stride;
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)parts, 0, (int)(nsplit * nrep * kPartStride * sizeof(float)), 0x00020000);
+    // Placement check: a range that ran on another XCD left its state and tag in that
+    // XCD's L2, and this L2 still holds the tag the last merge cleared.  Thread s
+    // reads range s's tag (head 0's row) ahead of the merge loads and checks and
+    // clears it at the end.
+    int tag = xcc_tag;
+    if (p.xcc_local && (int)threadIdx.x < nsplit)
+        tag = __float_as_int(ld_l2(prs, ((int)threadIdx.x * (nrep * kPartStride) + kHeadDim + 2) * 4));
     const int units = nrep * (kHeadDim / 4);
     const int K = kThreads / units;                  // >= 1 because nrep <= 16
     float* sm = smem;                                // [K][units][6] = (M, L, O[4])
@@ -752,21 +784,10 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         for (int s0 = k; s0 < nsplit; s0 += 8 * K) {
             float ms[8], ls[8];
             f4 os[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int sj = s0 + j * K;
-                const int off = min(sj, nsplit - 1) * (nrep * kPartStride) + hd * kPartStride;
-                if (p.xcc_local) {
-                    ms[j] = sj < nsplit ? ld_l2(prs, (off + kHeadDim) * 4) : -INFINITY;
-                    ls[j] = ld_l2(prs, (off + kHeadDim + 1) * 4);
-                    os[j] = ld_l2_f4(prs, (off + d4) * 4);
-                } else {
-                    const float* ps = parts + off;
-                    ms[j] = sj < nsplit ? ld_agent(ps + kHeadDim) : -INFINITY;
-                    ls[j] = ld_agent(ps + kHeadDim + 1);
-                    os[j] = f4{ld_agent(ps + d4), ld_agent(ps + d4 + 1), ld_agent(ps + d4 + 2), ld_agent(ps + d4 + 3)};
-                }
-            }
+            if (p.xcc_local)
+                load_partials<true>(prs, parts, s0, K, nsplit, nrep, hd, d4, ms, ls, os);
+            else
+                load_partials<false>(prs, parts, s0, K, nsplit, nrep, hd, d4, ms, ls, os);
             // the eight states merge with independent terms against their common max
             float Mc = ms[0];
 #pragma unroll
@@ -825,6 +846,12 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             __hip_atomic_store(&p.counters_l2[bh * 64], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         else
             __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // last in the kernel, so that no barrier waits for these stores
+    if (p.xcc_local && (int)threadIdx.x < nsplit) {
+        if (tag != xcc_tag && p.err) atomicOr(p.err, 4);
+        // the clear is ordered after the tag load by its use of the loaded value
+        if (tag != -1) reinterpret_cast<int*>(const_cast<float*>(parts))[threadIdx.x * (nrep * kPartStride) + kHeadDim + 2] = 0;
     }
 }
 

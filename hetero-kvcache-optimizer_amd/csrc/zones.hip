@@ -82,10 +82,122 @@ __global__ __launch_bounds__(128) void zone_read_kernel(const uint16_t* __restri
     }
 }
 
+// ---- device-stepped decode update: the decision of the manager's decode step
+// (manager.py:588-674 as this build keeps it) taken on the GPU from `state`, so the
+// step can be replayed from a captured graph.
+struct ZoneStepParams {
+    const uint16_t* k;
+    const uint16_t* v;
+    int64_t sb, sh;
+    int H;
+    uint16_t* tk;
+    uint16_t* tv;
+    int tcap, ring;
+    uint16_t* hk;
+    uint16_t* hv;
+    int hcap, hbudget;
+    int* state;   // tail_head, tail_len, hh_len, dropped
+    int* tail_lens;
+    int* hh_lens;
+    int B;
+};
+
+__device__ __forceinline__ int64_t vtile_index(int64_t bh, int cap, int slot, int d) {
+    return (bh * (cap / kBlockTokens) + slot / kBlockTokens) * (kBlockTokens * kHeadDim) + vtile_off(slot & 15, d);
+}
+
+__device__ inline bool state_ok(const ZoneStepParams& p, int head, int len, int hh) {
+    return head >= 0 && head < p.ring && len >= 0 && len <= p.ring && hh >= 0 && hh <= p.hbudget;
+}
+
+// One workgroup of 128 lanes (lane = dim) per (kv head, sequence): when the ring is
+// full its oldest token moves to the heavy-hitter zone (while it has room) before
+// the new token takes its slot.  Every lane reads and writes only its own dim.
+__global__ __launch_bounds__(128) void zone_step_kernel(ZoneStepParams p) {
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const int head = p.state[0], len = p.state[1], hh = p.state[2];
+    if (!state_ok(p, head, len, hh)) return;   // a state no step produced: write nothing
+    const int64_t bh = (int64_t)b * p.H + h;
+    int slot = head;
+    if (len < p.ring) {
+        slot = (head + len) % p.ring;
+    } else if (hh < p.hbudget) {
+        p.hk[(bh * p.hcap + hh) * kHeadDim + d] = p.tk[(bh * p.tcap + head) * kHeadDim + d];
+        p.hv[vtile_index(bh, p.hcap, hh, d)] = p.tv[vtile_index(bh, p.tcap, head, d)];
+    }
+    const int64_t src = (int64_t)b * p.sb + (int64_t)h * p.sh + d;
+    p.tk[(bh * p.tcap + slot) * kHeadDim + d] = p.k[src];
+    p.tv[vtile_index(bh, p.tcap, slot, d)] = p.v[src];
+}
+
+// Advances the state after the step and publishes the zone lengths per sequence.
+__global__ __launch_bounds__(256) void zone_advance_kernel(ZoneStepParams p) {
+    int head = p.state[0], len = p.state[1], hh = p.state[2], dropped = p.state[3];
+    if (!state_ok(p, head, len, hh)) return;
+    if (len < p.ring) {
+        ++len;
+    } else {
+        if (hh < p.hbudget)
+            ++hh;
+        else
+            ++dropped;
+        head = (head + 1) % p.ring;
+    }
+    for (int b = threadIdx.x; b < p.B; b += 256) {
+        if (p.tail_lens) p.tail_lens[b] = len;
+        if (p.hh_lens) p.hh_lens[b] = hh;
+    }
+    __syncthreads();   // every lane has read the old state
+    if (threadIdx.x == 0) {
+        p.state[0] = head;
+        p.state[1] = len;
+        p.state[2] = hh;
+        p.state[3] = dropped;
+    }
+}
+
 }  // namespace
 }  // namespace hkv
 
 using namespace hkv;
+
+extern "C" int hkv_zone_step(const HkvZoneStepArgs* a, void* stream) {
+    clear_error();
+    HKV_REQUIRE(a != nullptr, HKV_ERR_ARG, "hkv_zone_step: null args");
+    HKV_REQUIRE(a->head_dim == kHeadDim, HKV_ERR_UNSUPPORTED, "hkv_zone_step: head_dim %d != 128", a->head_dim);
+    HKV_REQUIRE(a->batch > 0 && a->batch <= 65535 && a->num_kv_heads > 0 && a->num_kv_heads <= 65535, HKV_ERR_ARG,
+                "hkv_zone_step: bad sizes");
+    HKV_REQUIRE(a->k && a->v && a->tail_k && a->tail_v && a->state, HKV_ERR_ARG, "hkv_zone_step: null pointer");
+    HKV_REQUIRE(a->tail_capacity > 0 && a->tail_capacity % kBlockTokens == 0 && a->tail_ring > 0 &&
+                    a->tail_ring <= a->tail_capacity,
+                HKV_ERR_ARG, "hkv_zone_step: tail ring %d / capacity %d", a->tail_ring, a->tail_capacity);
+    HKV_REQUIRE(a->hh_budget >= 0 && (a->hh_budget == 0 || (a->hh_k && a->hh_v && a->hh_capacity >= a->hh_budget &&
+                                                              a->hh_capacity % kBlockTokens == 0)),
+                HKV_ERR_ARG, "hkv_zone_step: heavy-hitter budget %d / capacity %d", a->hh_budget, a->hh_capacity);
+    ZoneStepParams p;
+    p.k = a->k;
+    p.v = a->v;
+    p.sb = a->src_stride_b;
+    p.sh = a->src_stride_h;
+    p.H = a->num_kv_heads;
+    p.tk = a->tail_k;
+    p.tv = a->tail_v;
+    p.tcap = a->tail_capacity;
+    p.ring = a->tail_ring;
+    p.hk = a->hh_k;
+    p.hv = a->hh_v;
+    p.hcap = a->hh_capacity;
+    p.hbudget = a->hh_budget;
+    p.state = a->state;
+    p.tail_lens = a->tail_lens;
+    p.hh_lens = a->hh_lens;
+    p.B = a->batch;
+    hipLaunchKernelGGL(zone_step_kernel, dim3(a->num_kv_heads, a->batch), dim3(128), 0, (hipStream_t)stream, p);
+    HKV_LAUNCH_CHECK("zone_step_kernel");
+    hipLaunchKernelGGL(zone_advance_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, p);
+    HKV_LAUNCH_CHECK("zone_advance_kernel");
+    return HKV_OK;
+}
 
 extern "C" int hkv_abi_version(void) { return HKV_ABI_VERSION; }
 

@@ -20,9 +20,9 @@ from .prefetcher import (Prefetcher, DRAMStorageManager, AsyncPrefetcher,  # noq
                          AdaptivePrefetchController)
 from .heavy_hitter import HeavyHitterOracle, compute_block_scores  # noqa: F401
 from .manager import HeteroKVManager  # noqa: F401
-from .engine_wrapper import (FusedHeteroCache, ChunkedPrefillEngine, build_fused_cache,  # noqa: F401
+from .engine_wrapper import (FusedHeteroCache, ChunkedPrefillEngine, DecodeGraph, build_fused_cache,  # noqa: F401
                              register_attention)
 
 __all__ = ["HeavyHitterOracle", "compute_block_scores", "HeteroKVError", "KVCompressor", "fused_dequant_attn_decode", "fused_dequant_attn_forward", "ops", "load", "HeteroKVManager",
-           "FusedHeteroCache", "ChunkedPrefillEngine", "build_fused_cache", "register_attention",
+           "FusedHeteroCache", "ChunkedPrefillEngine", "DecodeGraph", "build_fused_cache", "register_attention",
            "Prefetcher", "DRAMStorageManager", "AsyncPrefetcher", "AdaptivePrefetchController"]

@@ -13,7 +13,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libheterokv.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_U8 = 0, 1, 2, 3
 MAX_F16_ZONES = 3
 DECODE_DETERMINISTIC = 1   # HKV_DECODE_DETERMINISTIC
@@ -61,6 +61,14 @@ class ZoneWriteArgs(ctypes.Structure):
                 ("batch", i32), ("num_kv_heads", i32), ("head_dim", i32), ("num_tokens", i32),
                 ("slot_start", vp), ("capacity", i32), ("ring", i32),
                 ("zone_k", vp), ("zone_v", vp), ("slot_base", i32)]
+
+
+class ZoneStepArgs(ctypes.Structure):
+    _fields_ = [("k", vp), ("v", vp), ("src_stride_b", i64), ("src_stride_h", i64),
+                ("batch", i32), ("num_kv_heads", i32), ("head_dim", i32),
+                ("tail_k", vp), ("tail_v", vp), ("tail_capacity", i32), ("tail_ring", i32),
+                ("hh_k", vp), ("hh_v", vp), ("hh_capacity", i32), ("hh_budget", i32),
+                ("state", vp), ("tail_lens", vp), ("hh_lens", vp)]
 
 
 class F16Zone(ctypes.Structure):
@@ -115,6 +123,7 @@ SYMBOLS = [
     ("hkv_zone_write", ctypes.c_int, [ctypes.POINTER(ZoneWriteArgs), vp]),
     ("hkv_zone_read", ctypes.c_int, [vp, vp, i32, i32, i32, i32, i32, vp, vp, vp]),
     ("hkv_zone_copy", ctypes.c_int, [vp, vp, i32, i32, vp, vp, i32, i32, i32, i32, i32, i32, vp]),
+    ("hkv_zone_step", ctypes.c_int, [ctypes.POINTER(ZoneStepArgs), vp]),
     ("hkv_decode_workspace_bytes", ctypes.c_size_t, [i32, i32, i32, i32, i32, vp, i32]),
     ("hkv_decode_attn", ctypes.c_int, [ctypes.POINTER(DecodeArgs), vp]),
     ("hkv_prefill_attn", ctypes.c_int, [ctypes.POINTER(PrefillArgs), vp]),

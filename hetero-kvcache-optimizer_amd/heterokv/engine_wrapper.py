@@ -312,6 +312,98 @@ class ChunkedPrefillEngine:
         return last
 
 
+class DecodeGraph:
+    """One decode step of `model` over a FusedHeteroCache, captured in a HIP graph and
+    replayed for every later token.
+
+    The cache's manager switches to device-stepped decode (enable_device_decode): the
+    zone decision of each step and the zone lengths decode attention reads live on the
+    GPU, so no kernel argument of a step depends on host state.  The first step runs
+    eagerly (it also sizes the decode workspace and settles the DRAM-tier gate, which
+    layer 0 refreshes after its own update); the second is captured and replayed; from
+    then on a step copies the token ids and positions into the graph's input buffers,
+    advances the host copies of the zone bookkeeping exactly as an eager step would and
+    replays.  The returned logits live in the graph's memory pool and are overwritten
+    by the next step.
+
+    Not for caches whose decode step does host work that has no graph form: a host
+    tier (records copied in on a side stream), a retrieval window, attention tracking.
+    The INT4 tier may not change while the graph lives (decode never adds to it)."""
+
+    def __init__(self, model, cache: FusedHeteroCache):
+        if not cache.fused_decode:
+            raise HeteroKVError(-4, "DecodeGraph needs fused_decode=True")
+        if cache.adaptive_self_healing or cache.track_attention:
+            raise HeteroKVError(-4, "DecodeGraph: adaptive retrieval and attention tracking run host logic per step")
+        self.model = model
+        self.cache = cache
+        self.graph = None
+        self.steps = 0
+        self._ids = self._pos = self._logits = None
+        self._int4 = None
+
+    def _check(self):
+        mgr = self.cache._manager
+        if mgr is None:
+            raise HeteroKVError(-1, "DecodeGraph: prefill the cache before decoding")
+        if mgr.retrieval_window is not None:
+            raise HeteroKVError(-4, "DecodeGraph: a retrieval window selects chunks on the host per step")
+        if any(st is not None and st.n_host > 0 for st in mgr._layers):
+            raise HeteroKVError(-4, "DecodeGraph: a host tier copies records in on a side stream per step")
+        int4 = [0 if st is None else st.int4_len for st in mgr._layers]
+        if self._int4 is not None and int4 != self._int4:
+            raise HeteroKVError(-1, "DecodeGraph: the INT4 tier changed since the graph was captured")
+        self._int4 = int4
+        return mgr
+
+    def _forward(self, ids, pos):
+        return self.model(input_ids=ids, position_ids=pos, past_key_values=self.cache, use_cache=True).logits
+
+    def _advance_host(self, mgr):
+        """What FusedHeteroCache.update does on the host for one decode token, layer by layer."""
+        cache = self.cache
+        for li in range(mgr.num_layers):
+            mgr.advance_decode_host(li, cache.real_seq_len)
+            if li == 0:
+                cache.real_seq_len += 1
+                if cache.self_healing:
+                    cache._refresh_swap_count()
+
+    @torch.inference_mode()
+    def step(self, input_ids: torch.Tensor, position_ids: torch.Tensor) -> torch.Tensor:
+        """input_ids, position_ids: [B, 1] on the cache's device; returns logits [B, 1, vocab]."""
+        mgr = self._check()
+        if self.steps == 0:
+            mgr.enable_device_decode(True)
+            out = self._forward(input_ids, position_ids)
+        elif self.graph is None:
+            self._ids = input_ids.clone()
+            self._pos = position_ids.clone()
+            g = torch.cuda.CUDAGraph()
+            # capturing runs the step's host logic once (the host state advances here);
+            # its kernels run at the first replay
+            with torch.cuda.graph(g):
+                self._logits = self._forward(self._ids, self._pos)
+            g.replay()
+            self.graph = g
+            out = self._logits
+        else:
+            self._ids.copy_(input_ids)
+            self._pos.copy_(position_ids)
+            self._advance_host(mgr)
+            self.graph.replay()
+            out = self._logits
+        self.steps += 1
+        return out
+
+    def close(self) -> None:
+        """Drop the graph and return the manager to host-stepped decode."""
+        self.graph = None
+        self._logits = None
+        if self.cache._manager is not None:
+            self.cache._manager.enable_device_decode(False)
+
+
 def build_fused_cache(num_layers: Optional[int] = None, device: str = "cuda:0", sink_tokens: int = 64,
                       keep_tail: int = 8192, chunk_size: int = 2048, group_size: int = 128,
                       enable_quant: bool = True, enable_prefetch: bool = True, enable_triton: bool = True,

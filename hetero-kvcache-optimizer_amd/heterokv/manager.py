@@ -56,6 +56,11 @@ class _LayerState:
         self.hh_len = 0
         self.hh_pos: List[int] = []
         self.hh_started = False
+        # device copies of (tail_head, tail_len, hh_len, dropped) and the per-sequence zone
+        # lengths, used by device-stepped decode (None: not in sync with the host values)
+        self.dev_state: Optional[torch.Tensor] = None
+        self.dev_tail_lens: Optional[torch.Tensor] = None
+        self.dev_hh_lens: Optional[torch.Tensor] = None
         self.pool: Optional[ops.Int4Pool] = None
         self.pool_used = 0                         # pool records in use
         self.bt: Optional[torch.Tensor] = None     # device int32 [B, cap]: logical block -> record id
@@ -119,6 +124,7 @@ class _LayerState:
         if n:
             self.tail.write(_as16(k), _as16(v), [0] * self.B)
         self.tail_head, self.tail_len = 0, n
+        self.dev_state = None
 
 
 class HeteroKVManager:
@@ -174,6 +180,8 @@ class HeteroKVManager:
         self.retrieval_window: Any = None
         self._adaptive_controller = AdaptivePrefetchController()
         self._last_attention_weights: Optional[torch.Tensor] = None
+        # device-stepped decode (enable_device_decode): zone decisions and lengths on the GPU
+        self.device_decode = False
         # cumulative attention scores (manager.py:102-106); fed by update_attention_scores
         # or attend_decode(feed_oracle=True)
         self._oracle = HeavyHitterOracle(block_size=16, sink_tokens=sink_tokens, local_window=hbm_budget_tokens)
@@ -225,6 +233,7 @@ class HeteroKVManager:
         self._check_input(key_states, value_states)
         st = self._state(layer_idx, key_states)
         if mode == "prefill":
+            st.dev_state = None
             if st.prefilled:
                 return self._incremental_prefill(layer_idx, st, key_states, value_states, seq_offset)
             return self._first_prefill(layer_idx, st, key_states, value_states, seq_offset)
@@ -275,10 +284,25 @@ class HeteroKVManager:
     def _decode(self, layer, st, k, v, seq_offset, materialize):
         if k.shape[2] != 1:
             raise HeteroKVError(-1, "decode expects one new token, got %d" % k.shape[2])
-        pos = seq_offset
         k16, v16 = _as16(k), _as16(v)
+        if self.device_decode:
+            if st.dev_state is None:
+                self._sync_device_state(st)
+            st.tail.step(st.hh, k16, v16, st.ring, self._heavyhitter_budget, st.dev_state, st.dev_tail_lens,
+                         st.dev_hh_lens)
+        self._decode_host(st, seq_offset, k16, v16, launch=not self.device_decode)
+        if not materialize:
+            return None, None
+        kk, vv = self.get_hbm_kv(layer)
+        return kk.to(k.dtype), vv.to(v.dtype)
+
+    def _decode_host(self, st, seq_offset, k16, v16, launch):
+        """The decode step's zone decision (manager.py:588-674 as this build keeps it), with
+        its kernels when `launch` (device-stepped decode takes the same decision on the GPU)."""
+        pos = seq_offset
         if st.tail_len < self.tail_budget:
-            st.tail.write(k16, v16, [st.tail_head + st.tail_len] * st.B, ring=st.ring)
+            if launch:
+                st.tail.write(k16, v16, [st.tail_head + st.tail_len] * st.B, ring=st.ring)
             st.tail_len += 1
             st.tail_pos.append(pos)
         else:
@@ -287,21 +311,47 @@ class HeteroKVManager:
             # attended again
             old = st.tail_pos.popleft()
             if st.hh_len < self._heavyhitter_budget:
-                st.tail.copy_to(st.hh, st.tail_head, st.hh_len, 1)
+                if launch:
+                    st.tail.copy_to(st.hh, st.tail_head, st.hh_len, 1)
                 st.hh_len += 1
                 st.hh_pos.append(old)
             else:
                 self._queued_tokens += 1
-            st.tail.write(k16, v16, [st.tail_head] * st.B, ring=st.ring)
+            if launch:
+                st.tail.write(k16, v16, [st.tail_head] * st.B, ring=st.ring)
             st.tail_head = (st.tail_head + 1) % st.ring
             st.tail_pos.append(pos)
         st.tail_started = True
         st.hh_started = True
         st.seq_offset = seq_offset + 1
-        if not materialize:
-            return None, None
-        kk, vv = self.get_hbm_kv(layer)
-        return kk.to(k.dtype), vv.to(v.dtype)
+
+    # ---------------------------------------------------------------- device-stepped decode
+    def enable_device_decode(self, on: bool = True) -> None:
+        """Take each decode step's zone decision on the GPU (hkv_zone_step) and let decode
+        attention read the recent-window and heavy-hitter lengths from device counters.  A
+        decode step then has no kernel argument that depends on host state, so it can be
+        captured once in a HIP graph and replayed (DecodeGraph).  The host copies of the
+        lengths and positions keep following the same rules."""
+        if on and self.tail_budget < 1:
+            raise HeteroKVError(-4, "device-stepped decode needs a recent window of at least one token")
+        self.device_decode = bool(on)
+        for st in self._layers:
+            if st is not None:
+                st.dev_state = None
+
+    def _sync_device_state(self, st) -> None:
+        dev = self.device
+        st.dev_state = torch.tensor([st.tail_head, st.tail_len, st.hh_len, 0], dtype=torch.int32, device=dev)
+        st.dev_tail_lens = torch.full((st.B,), st.tail_len, dtype=torch.int32, device=dev)
+        st.dev_hh_lens = torch.full((st.B,), st.hh_len, dtype=torch.int32, device=dev)
+
+    def advance_decode_host(self, layer_idx: int, seq_offset: int) -> None:
+        """The host half of one decode step of a layer, without kernels: what a replayed
+        decode graph did on the GPU."""
+        st = self._layers[layer_idx]
+        if st is None:
+            raise RuntimeError("Layer %d has not been allocated yet." % layer_idx)
+        self._decode_host(st, seq_offset, None, None, launch=False)
 
     def _evict(self, layer, st, k, v, first_pos):
         """manager.py:1231-1299: quantize + pack into the layer's INT4 blocks, record the chunk."""
@@ -343,6 +393,7 @@ class HeteroKVManager:
         # the reference keeps only the sink as its concatenated cache; all zones after it empty
         st.tail_head, st.tail_len, st.tail_pos = 0, 0, deque()
         st.hh_len, st.hh_pos = 0, []
+        st.dev_state = None
         if st.sink_len > self.sink_tokens:
             st.sink_len = self.sink_tokens
         return total - self.sink_tokens
@@ -665,13 +716,24 @@ class HeteroKVManager:
             raise RuntimeError("Layer %d has not been allocated yet." % layer_idx)
         if self._workspace is None:
             self._workspace = ops.DecodeWorkspace(self.device)
+        if feed_oracle and self.device_decode:
+            raise HeteroKVError(-1, "attend_decode: feed_oracle needs host-stepped decode")
         zones = []
         if st.sink_len:
             zones.append((st.sink, None, st.sink_len))
-        if st.tail_len:
-            zones.append((st.tail, None, st.tail_len))
-        if st.hh_len:
-            zones.append((st.hh, None, st.hh_len))
+        if self.device_decode:
+            # lengths from the device counters, bounds by value: the same launch serves
+            # every step
+            if st.dev_state is None:
+                self._sync_device_state(st)
+            zones.append((st.tail, st.dev_tail_lens, st.ring))
+            if self._heavyhitter_budget > 0:
+                zones.append((st.hh, st.dev_hh_lens, self._heavyhitter_budget))
+        else:
+            if st.tail_len:
+                zones.append((st.tail, None, st.tail_len))
+            if st.hh_len:
+                zones.append((st.hh, None, st.hh_len))
         n4 = st.int4_len if include_dram else 0
         bt = st.bt
         sel = None

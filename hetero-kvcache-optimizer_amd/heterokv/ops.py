@@ -238,6 +238,25 @@ class F16Zone:
                                    dst.capacity, dst_slot, self.batch, self.num_kv_heads, HEAD_DIM, n,
                                    stream_ptr(self.device)), "hkv_zone_copy")
 
+    def step(self, hh, k, v, ring, hh_budget, state, tail_lens=None, hh_lens=None):
+        """Device-stepped decode update (hkv_zone_step) of this ring zone and the heavy-hitter
+        zone hh: k, v [B, H, 1, 128] fp16; state int32 [4] (ring head, ring length,
+        heavy-hitter length, dropped) is read and advanced on the GPU; tail_lens / hh_lens
+        (int32 [B]) receive the new lengths."""
+        _require_gpu(k, v, state)
+        if k.dtype != torch.float16 or v.dtype != torch.float16 or k.shape != v.shape or k.shape[2] != 1:
+            raise HeteroKVError(-1, "F16Zone.step: k/v must be fp16 [B, H, 1, 128]")
+        if k.stride() != v.stride() or k.stride(-1) != 1:
+            k, v = k.contiguous(), v.contiguous()
+        a = _lib.ZoneStepArgs(k=k.data_ptr(), v=v.data_ptr(), src_stride_b=k.stride(0), src_stride_h=k.stride(1),
+                              batch=self.batch, num_kv_heads=self.num_kv_heads, head_dim=HEAD_DIM,
+                              tail_k=_p(self.k), tail_v=_p(self.v), tail_capacity=self.capacity, tail_ring=int(ring),
+                              hh_k=_p(hh.k) if hh is not None else None, hh_v=_p(hh.v) if hh is not None else None,
+                              hh_capacity=hh.capacity if hh is not None else 0, hh_budget=int(hh_budget),
+                              state=state.data_ptr(), tail_lens=_p(tail_lens) if tail_lens is not None else None,
+                              hh_lens=_p(hh_lens) if hh_lens is not None else None)
+        check(load().hkv_zone_step(ctypes.byref(a), stream_ptr(k.device)), "hkv_zone_step")
+
     def read(self, n):
         """Slots [0, n) as row-major (K, V) [B, H, n, 128]."""
         ok = torch.empty((self.batch, self.num_kv_heads, n, HEAD_DIM), dtype=torch.float16, device=self.device)

@@ -65,7 +65,7 @@
 extern "C" {
 #endif
 
-#define HKV_ABI_VERSION 4
+#define HKV_ABI_VERSION 5
 
 /* dtype codes */
 #define HKV_DTYPE_F16  0
@@ -210,6 +210,35 @@ int hkv_zone_read(const uint16_t* zone_k, const uint16_t* zone_v, int32_t batch,
 int hkv_zone_copy(const uint16_t* src_k, const uint16_t* src_v, int32_t src_capacity, int32_t src_slot,
                   uint16_t* dst_k, uint16_t* dst_v, int32_t dst_capacity, int32_t dst_slot,
                   int32_t batch, int32_t num_kv_heads, int32_t head_dim, int32_t n, void* stream);
+
+/*
+ * Device-stepped decode update of the recent-window ring and the heavy-hitter zone:
+ * the manager's decode step (src/memory/manager.py:588-674 as this build keeps it)
+ * with its decision taken on the GPU from `state`, so that a captured graph can
+ * replay it.  state = device int32 [4]: ring head, ring length, heavy-hitter length,
+ * dropped tokens.  If the ring is not full the new token goes to slot
+ * (head + length) % ring; otherwise the token at `head` moves to heavy-hitter slot
+ * hh_len while hh_len < hh_budget (else it is dropped), the new token takes `head`
+ * and head advances.  tail_lens / hh_lens (device int32 [batch], may be NULL)
+ * receive the new lengths, as zone lengths for hkv_decode_attn.
+ */
+typedef struct HkvZoneStepArgs {
+    const uint16_t* k;             /* new token [batch][num_kv_heads][1][128] fp16 */
+    const uint16_t* v;
+    int64_t src_stride_b, src_stride_h;
+    int32_t batch, num_kv_heads, head_dim;
+    uint16_t* tail_k;
+    uint16_t* tail_v;
+    int32_t tail_capacity, tail_ring;
+    uint16_t* hh_k;
+    uint16_t* hh_v;
+    int32_t hh_capacity, hh_budget;
+    int32_t* state;
+    int32_t* tail_lens;
+    int32_t* hh_lens;
+} HkvZoneStepArgs;
+
+int hkv_zone_step(const HkvZoneStepArgs* args, void* stream);
 
 /*
  * Split-K decode attention over [fp16 zones || INT4 pool] for one query token per

@@ -32,7 +32,7 @@ def test_header_symbols_exported(lib):
 
 
 def test_version_and_record_size(lib):
-    assert lib.hkv_abi_version() == 4
+    assert lib.hkv_abi_version() == 5
     assert lib.hkv_block_bytes(8, 128) == 17664
     assert lib.hkv_block_bytes(4, 128) == 8832
     assert lib.hkv_block_bytes(8, 64) == -1
@@ -48,7 +48,7 @@ def test_struct_layouts_match_c_compiler(tmp_path):
     structs = {"HkvPackArgs": _lib.PackArgs, "HkvRepackArgs": _lib.RepackArgs,
                "HkvZoneWriteArgs": _lib.ZoneWriteArgs, "HkvF16Zone": _lib.F16Zone,
                "HkvDecodeArgs": _lib.DecodeArgs, "HkvPrefillArgs": _lib.PrefillArgs,
-               "HkvCopyDesc": _lib.CopyDesc, "HkvPfStats": _lib.PfStats}
+               "HkvCopyDesc": _lib.CopyDesc, "HkvPfStats": _lib.PfStats, "HkvZoneStepArgs": _lib.ZoneStepArgs}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "%s"' % HEADER, "int main(void){"]
     for cname, py in structs.items():
         lines.append('printf("%s size %%zu\\n", sizeof(%s));' % (cname, cname))
