@@ -57,6 +57,9 @@ constexpr int kPartStride = kHeadDim + 4;  // o[128], m, l, 2 pad (16-byte rows)
 #endif
 constexpr int kPrefetch = HKV_DECODE_PREFETCH;  // INT4 block pairs in flight per wave
 constexpr int kMaxSplits = 64;
+// INT4 tokens, and fp16 tokens over all zones, per sequence: 2^22 items of 16 tokens
+// keep the range arithmetic in 32 bits.
+constexpr int kMaxZoneTokens = 1 << 26;
 constexpr int kIdWindow = 1024;           // INT4 block ids staged in LDS at a time
 constexpr int kIdPerThread = kIdWindow / kThreads;
 static_assert(kIdWindow % kThreads == 0, "whole id entries per thread");
@@ -455,13 +458,22 @@ __device__ __forceinline__ int next_unit(int* ctr, int& seq) {
 // rounding of nsplit into two groups costs at most ~6% over an even share.  Costs:
 // an INT4 block counts kInt4Cost bytes (its 2208 bytes, plus the block-id
 // indirection and the nibble decode), an fp16 tile its 8192 bytes.
+//
+// Every workgroup computes the plan before its first load, so it uses float costs
+// and 32-bit range bounds: a 64-bit division expands to ~130 instructions.
 __device__ __forceinline__ int int4_splits(int nb4, int ntf, int nsplit) {
     if (nb4 == 0 || ntf == 0 || nsplit < 2) return 0;
-    const int64_t c4 = (int64_t)nb4 * kInt4Cost, cf = (int64_t)ntf * kF16ItemBytes, ct = c4 + cf;
-    int s4 = (int)((c4 * nsplit + ct / 2) / ct);
+    const float c4 = (float)nb4 * (float)kInt4Cost, cf = (float)ntf * (float)kF16ItemBytes, ct = c4 + cf;
+    int s4 = (int)(c4 * (float)nsplit / ct + 0.5f);
     s4 = min(max(s4, 1), nsplit - 1);
-    const int64_t worst = max((c4 + s4 - 1) / s4, (cf + nsplit - s4 - 1) / (nsplit - s4));
-    return worst * 16 <= (ct + nsplit - 1) / nsplit * 17 ? s4 : 0;
+    const float worst = fmaxf(c4 / (float)s4, cf / (float)(nsplit - s4));
+    return worst * 16.0f <= ct / (float)nsplit * 17.0f ? s4 : 0;
+}
+
+// floor(n i / d) for the range bounds: n < 2^22 items (host-checked), i <= d <= 64,
+// so the product fits 32 bits and the division is exact.
+__device__ __forceinline__ int part_point(int n, int i, int d) {
+    return (int)(((uint32_t)n * (uint32_t)i) / (uint32_t)d);
 }
 
 // Partial states s0 + j K (j < 8) of head hd for the final merge: m, l and
@@ -523,17 +535,17 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             // splits [0, s4) stream INT4 blocks only, the others fp16 tiles only
             const bool is4 = split < s4;
             const int si = is4 ? split : split - s4, sn = is4 ? s4 : nsplit - s4, n = is4 ? nb4 : ntf;
-            const int u0 = (int)((int64_t)n * si / sn), u1 = (int)((int64_t)n * (si + 1) / sn);
+            const int u0 = part_point(n, si, sn), u1 = part_point(n, si + 1, sn);
             a0 = is4 ? u0 : 0;
             a1 = is4 ? u1 : 0;
             f0 = is4 ? 0 : u0;
             nf = is4 ? 0 : u1 - u0;
         } else {
             // every split takes the same share of both kinds
-            a0 = (int)((int64_t)nb4 * split / nsplit);
-            a1 = (int)((int64_t)nb4 * (split + 1) / nsplit);
-            f0 = (int)((int64_t)ntf * split / nsplit);
-            nf = (int)((int64_t)ntf * (split + 1) / nsplit) - f0;
+            a0 = part_point(nb4, split, nsplit);
+            a1 = part_point(nb4, split + 1, nsplit);
+            f0 = part_point(ntf, split, nsplit);
+            nf = part_point(ntf, split + 1, nsplit) - f0;
         }
     }
 
@@ -958,7 +970,8 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     HKV_REQUIRE(a->q && a->out && a->workspace, HKV_ERR_ARG, "hkv_decode_attn: null q/out/workspace");
     HKV_REQUIRE((((uintptr_t)a->q) & 15) == 0 && (a->q_stride_b % 8) == 0 && (a->q_stride_h % 8) == 0,
                 HKV_ERR_ARG, "hkv_decode_attn: q must be 16-byte aligned with strides multiple of 8");
-    HKV_REQUIRE(a->int4_max_len >= 0, HKV_ERR_ARG, "hkv_decode_attn: int4_max_len < 0");
+    HKV_REQUIRE(a->int4_max_len >= 0 && a->int4_max_len <= kMaxZoneTokens, HKV_ERR_ARG,
+                "hkv_decode_attn: int4_max_len %d outside [0, %d]", a->int4_max_len, kMaxZoneTokens);
     if (a->int4_max_len > 0) {
         HKV_REQUIRE(a->block_table && ((a->pool && a->pool_blocks > 0) || (a->staging && a->staging_blocks > 0)),
                     HKV_ERR_ARG, "hkv_decode_attn: INT4 zone without pool/staging records or block table");
@@ -984,6 +997,8 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
         }
         zl[i] = z.max_len;
     }
+    HKV_REQUIRE((int64_t)zl[0] + zl[1] + zl[2] <= kMaxZoneTokens, HKV_ERR_ARG,
+                "hkv_decode_attn: fp16 zones hold more than %d tokens", kMaxZoneTokens);
     const int64_t BH = (int64_t)a->batch * a->num_kv_heads;
     HKV_REQUIRE(BH < 65536, HKV_ERR_ARG, "hkv_decode_attn: batch x kv heads too large");
     const int ms = choose_splits((int)BH, a->int4_max_len, zl, a->num_f16_zones, a->splits_hint);

@@ -101,6 +101,11 @@ def test_decode_argument_errors(lib):
     assert b"workspace" in lib.hkv_last_error()
     a.f16[0] = _lib.F16Zone(k=4096, v=4096, capacity=64, max_len=80, lens=None)
     assert lib.hkv_decode_attn(ctypes.byref(a), None) == -1
+    # range bounds are 32-bit: at most 2^26 INT4 tokens per sequence
+    a.f16[0] = _lib.F16Zone(k=4096, v=4096, capacity=64, max_len=64, lens=None)
+    a.int4_max_len = (1 << 26) + 1
+    assert lib.hkv_decode_attn(ctypes.byref(a), None) == -1
+    assert b"int4_max_len" in lib.hkv_last_error()
 
 
 def test_workspace_size(lib):
