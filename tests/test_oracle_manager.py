@@ -58,6 +58,37 @@ def test_decode_slides_tail_into_heavy_hitters_fifo_then_drops():
     assert len(m.hh[0]) == 2048 and len(m.queue) == 1
 
 
+def test_competition_queue_top_k_is_fifo_for_any_scores():
+    """manager.py:686-715 with attention_competition_queue.py:34-107: the shared queue is
+    sorted by score before up to (budget - |hh|) tokens are taken.  With layers updated in
+    lockstep the queue holds at most the one token just evicted while a layer has room,
+    so whatever the scores, every heavy-hitter zone is the first `budget` tokens its tail
+    evicted, in order, and later ones stay queued (never attended).  This is the rule the
+    device-side decode step (hkv_zone_step) applies."""
+    import random
+
+    class Scored(ManagerOracle):
+        def _enqueue(self, layer, position, score):
+            super()._enqueue(layer, position, rng.random())
+
+    rng = random.Random(11)
+    L, budget = 3, 5
+    m = Scored(L, sink_tokens=4, hbm_budget_tokens=12)
+    m.hh_budget = budget
+    for layer in range(L):
+        m.update(layer, range(20), "prefill")
+    evicted = [[] for _ in range(L)]
+    for p in range(20, 50):
+        for layer in range(L):
+            if len(m.tail[layer]) == m.tail_budget:
+                evicted[layer].append(m.tail[layer][0])
+            m.update(layer, [p], "decode", seq_offset=p)
+    for layer in range(L):
+        assert m.hh[layer] == evicted[layer][:budget], layer
+    assert sorted(pos for _, pos, _ in m.queue.values()) == sorted(
+        pos for layer in range(L) for pos in evicted[layer][budget:])
+
+
 def test_decode_before_prefill_and_growing_tail():
     m = ManagerOracle(1, sink_tokens=4, hbm_budget_tokens=8)
     assert m.update(0, [0], "decode") == [0]
