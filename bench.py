@@ -253,6 +253,105 @@ def bench_paged(torch, ops, args):
     print(json.dumps(line), flush=True)
 
 
+C1_BYTES = 2 * 8 * 4096 * 128 * 2 + 2 * (8 * 4096 * 64 + 8 * 4096 * 4 + 8 * 4096)   # 21,299,200
+
+
+def bench_quant(torch, ops, args):
+    """Quantize+pack round trip on K, V [1, 8, 4096, 128] fp16 (group 128 = one token row,
+    4 outlier K channels x8): hkv_pack_tokens writes the INT4 block records (codes packed two
+    per byte, fp32 scale and u8 zero point per row); back to fp16 through the Path C route
+    (hkv_unpack_tokens + hkv_dequantize_groups).  Both read or write 21,299,200 algorithmic
+    bytes per K+V call; 16 rotated copies keep the inputs out of the 256 MB Infinity Cache."""
+    from heterokv.kv_compressor import KVCompressor
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator().manual_seed(0)
+    K = torch.randn((1, 8, 4096, 128), generator=g)
+    K[..., OUTLIERS] *= 8
+    V = torch.randn((1, 8, 4096, 128), generator=g)
+    K16, V16 = K.half(), V.half()
+    R = 16
+    ks = [K16.to(dev) for _ in range(R)]
+    vs = [V16.to(dev) for _ in range(R)]
+    pools = [ops.Int4Pool(256, 8, dev) for _ in range(R)]
+    bt = torch.arange(256, dtype=torch.int32, device=dev)[None]
+    start = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def quant(i):
+        ops.pack_tokens(pools[i % R], ks[i % R], vs[i % R], start, bt)
+
+    def roundtrip(i):
+        for which in (0, 1):
+            c, s, z = ops.unpack_tokens(pools[i % R], bt[0], 4096, which)
+            ops.dequantize_groups(c, s, z)
+
+    def timed(fn, n):
+        for i in range(max(args.warmup, 2 * R)):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            fn(i)
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+
+    n = max(args.steps, 64)
+    us_q = timed(quant, n)
+    us_rt = timed(roundtrip, max(n // 4, 16))
+    for p_ in pools:
+        p_.check_errors()
+    comp = KVCompressor(group_size=128, bits=4)
+    rel = {}
+    got = {}
+    for which, name, x in ((0, "k", K16), (1, "v", V16)):
+        c, s, z = ops.unpack_tokens(pools[0], bt[0], 4096, which)
+        got[name] = (c.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy())
+        rel[name] = round(comp.relative_error(x.to(dev), c.view(1, 8, 4096, 128), s, z), 4)
+    gbs = C1_BYTES / (us_q * 1e-6) / 1e9
+    cpu = None if args.no_cpu_baseline else cpu_baseline_quant(K16, V16, got, args.cpu_budget)
+    line = {
+        "metric": "INT4 quantize+pack GB/s on the C1 round-trip tensors (K, V [1, 8, 4096, 128] fp16)",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": n, "warmup": args.warmup,
+        "ms_per_step": round(us_q * 1e-3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16->int4", "data": "synthetic (seeded N(0,1) K/V, K channels 7, 31, 64, 100 x8)",
+        "config": {"workload": "quantize+pack K and V [1, 8, 4096, 128] fp16 into 256 INT4 block records of 8 kv "
+                               "heads (group 128), then back to fp16 by the Path C route",
+                   "algorithmic_bytes": C1_BYTES, "roundtrip_us": round(us_rt, 3),
+                   "roundtrip_gbs": round(C1_BYTES / (us_rt * 1e-6) / 1e9, 2),
+                   "relative_error_pct": rel},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_quant(K16, V16, got, budget_s):
+    """The oracle's compress (kv_compressor.py:50-98 restated in C, one thread) on the same
+    K and V, timed on the host; also the number of codes / scales / zero points that differ
+    from the GPU's (reported, expected 0)."""
+    import numpy as np
+    from oracle import compressor as oc
+    t0 = time.perf_counter()
+    reps = 0
+    mism = 0
+    while True:
+        for name, x in (("k", K16), ("v", V16)):
+            c, s, z = oc.compress(x[0].numpy(), 128)
+            if reps == 0:
+                gc, gs, gz = got[name]
+                mism += int((c != gc).sum() + (s.view(np.uint32) != gs.view(np.uint32)).sum() + (z != gz).sum())
+        reps += 1
+        if time.perf_counter() - t0 >= min(budget_s, 5.0) or reps >= 50:
+            break
+    per = (time.perf_counter() - t0) / reps
+    return {"value": round(C1_BYTES / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "%d full K+V compress pass(es), %.1f ms each; code/scale/zp mismatches vs GPU: %d"
+                      % (reps, per * 1e3, mism)}
+
+
 def bench_scoring(torch, ops, args):
     """Heavy-hitter scoring on the 32K decode workload: the decode launch with score
     outputs against the plain one, the head-averaged weights of the newest token
@@ -561,12 +660,13 @@ def main():
                     help="decode with the fixed block-to-wave schedule (bitwise reproducible)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged", "scoring"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged", "scoring", "quant"], default="decode",
                     help="decode: the headline single-layer decode (default); prefill: the chunked-prefill "
                          "kernel on a 2048-token chunk over 64 + 131072 INT4 + 4096 tokens (MFMA bound); "
                          "tiered: end-to-end 28-layer decode at 131072 tokens with 75%% of the INT4 KV in "
                          "pinned host memory (use small --steps/--warmup, e.g. 8 / 2); paged: batch-16 paged "
-                         "decode, contexts 8K-32K")
+                         "decode, contexts 8K-32K; scoring: heavy-hitter scoring at 32K; quant: quantize+pack "
+                         "of K, V [1, 8, 4096, 128] and the round trip back to fp16")
     ap.add_argument("--copy-calibration", type=float, default=0.0,
                     help="run only torch's device copy of this many MB (20 launches) so that rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
@@ -598,6 +698,8 @@ def main():
         return bench_tiered(torch, args)
     if args.workload == "paged":
         return bench_paged(torch, ops, args)
+    if args.workload == "quant":
+        return bench_quant(torch, ops, args)
     if args.workload == "scoring":
         return bench_scoring(torch, ops, args)
 
