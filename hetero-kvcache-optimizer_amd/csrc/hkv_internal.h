@@ -93,6 +93,7 @@ __device__ __forceinline__ float load_as_float(const void* p, int dtype, int64_t
 struct QParams {
     float scale;
     float zpf;
+    float inv;     // RN(1 / scale)
     uint8_t zp;
 };
 
@@ -104,13 +105,28 @@ __device__ __forceinline__ QParams qparams_from_minmax(float mn, float mx) {
     z = fminf(fmaxf(z, 0.0f), 15.0f);
     q.scale = s;
     q.zpf = z;
+    q.inv = 1.0f / s;
     q.zp = (uint8_t)z;
     return q;
 }
 
+// x / scale rounded to nearest, without a division per element (Markstein): with
+// y = RN(1/s), q = RN(x y) and the exact residual r = x - s q (one fma),
+// RN(q + r y) is the correctly rounded quotient.  Only when the residual
+// underflows (quotients below 2^-60 here) can it differ from x / s, and such a
+// quotient leaves rint(quotient + zp) unchanged; checked for every fp16 value and
+// 4096 random fp32 values against 20000 scales, all 16 zero points.  An infinite
+// or NaN scale takes the plain division.
+__device__ __forceinline__ float div_by_scale(float x, const QParams& q) {
+    if (!(fabsf(q.scale) < INFINITY)) return x / q.scale;
+    const float q0 = __fmul_rn(x, q.inv);
+    const float r = __builtin_fmaf(-q0, q.scale, x);
+    return __builtin_fmaf(r, q.inv, q0);
+}
+
 // kv_compressor.py:86-88: clamp(round(x / scale + zp), 0, 15)
 __device__ __forceinline__ uint32_t quant_code(float x, const QParams& q) {
-    float t = x / q.scale;
+    float t = div_by_scale(x, q);
     t = t + q.zpf;
     t = rintf(t);
     t = fminf(fmaxf(t, 0.0f), 15.0f);

@@ -92,6 +92,36 @@ def test_edge_rows():
     assert list(oc_codes[2, :6]) == [0, 15, 8, 2, 4, 10]
 
 
+def test_division_edge_rows_and_random_fp32():
+    """The per-element x / scale is computed from RN(1/scale) with one fma correction; rows
+    that exercise it: infinite values (the plain-division path), values whose residual
+    underflows (tiny fp32 beside ordinary ones), huge-over-tiny ranges, and 2M random
+    finite fp32 bit patterns; every code, scale and zero point against the oracle."""
+    print("case: quantizer division edge rows + random fp32 bits", flush=True)
+    from heterokv import KVCompressor
+    rows = np.zeros((6, 128), dtype=np.float32)
+    rows[0] = np.linspace(-3, 3, 128)
+    rows[0, 5] = np.inf
+    rows[1] = np.linspace(-3, 3, 128)
+    rows[1, 9] = -np.inf
+    rows[2] = np.float32(1e-40) * np.arange(128)            # subnormal inputs
+    rows[3] = np.linspace(-1.0, 1.0, 128)
+    rows[3, :8] = np.float32(3e-39) * np.arange(1, 9)        # quotients whose residual underflows
+    rows[4] = np.float32(1e30) * np.linspace(-1, 1, 128)
+    rows[4, 3] = np.float32(1e-30)
+    rows[5] = np.float32(2.0 ** -120) * np.linspace(-1, 1, 128)
+    g = np.random.default_rng(7)
+    bits = g.integers(0, 2 ** 32, size=(16384, 128), dtype=np.uint64).astype(np.uint32)
+    rnd = bits.view(np.float32)
+    rnd = np.where(np.isfinite(rnd), rnd, np.float32(0.0)).astype(np.float32)
+    for x_np in (rows, rnd):
+        codes, scales, zps = KVCompressor().compress(torch.from_numpy(x_np).to(DEV))
+        oc_codes, oc_scales, oc_zps = oc.compress(x_np, 128)
+        assert np.array_equal(codes.cpu().numpy(), oc_codes)
+        assert np.array_equal(scales.cpu().numpy().view(np.uint32), oc_scales.view(np.uint32))
+        assert np.array_equal(zps.cpu().numpy(), oc_zps)
+
+
 def test_cpu_tensor_is_rejected():
     from heterokv import HeteroKVError, KVCompressor
     with pytest.raises(HeteroKVError):
