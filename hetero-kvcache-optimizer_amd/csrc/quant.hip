@@ -43,17 +43,26 @@ __global__ __launch_bounds__(256) void quantize_groups_kernel(
     }
 }
 
-// kv_compressor.py:131-132: (q - zp) * scale in float32, then cast (round to nearest even).
+// kv_compressor.py:131-132: (q - zp) * scale in float32, then cast (round to nearest
+// even).  One wavefront per group (as the quantizer), so the group's scale and zero
+// point are read once and no element needs an index division.
 __global__ __launch_bounds__(256) void dequantize_groups_kernel(
     const uint8_t* __restrict__ codes, const float* __restrict__ scales,
-    const uint8_t* __restrict__ zps, int64_t n, int G, void* __restrict__ out, int out_dtype) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-        const int64_t g = i / G;
-        const float v = ((float)codes[i] - (float)zps[g]) * scales[g];
-        if (out_dtype == HKV_DTYPE_F16) ((uint16_t*)out)[i] = f2h_rn(v);
-        else if (out_dtype == HKV_DTYPE_BF16) ((uint16_t*)out)[i] = f2bf_rn(v);
-        else ((float*)out)[i] = v;
+    const uint8_t* __restrict__ zps, int64_t n, int G, int64_t ngroups, void* __restrict__ out, int out_dtype) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+    for (int64_t g = wave; g < ngroups; g += nwaves) {
+        const float zp = (float)zps[g], sc = scales[g];
+        const int64_t base = g * (int64_t)G;
+        for (int i = lane; i < G; i += 64) {
+            const int64_t idx = base + i;
+            if (idx >= n) break;
+            const float v = ((float)codes[idx] - zp) * sc;
+            if (out_dtype == HKV_DTYPE_F16) ((uint16_t*)out)[idx] = f2h_rn(v);
+            else if (out_dtype == HKV_DTYPE_BF16) ((uint16_t*)out)[idx] = f2bf_rn(v);
+            else ((float*)out)[idx] = v;
+        }
     }
 }
 
@@ -252,37 +261,79 @@ __global__ __launch_bounds__(256) void repack_codes_kernel(RepackParams p) {
     write_block_words(codes, lo, hi, rec, L, h);
 }
 
-// Pool -> reference layout, one thread per (head, token, dim).
+// Pool -> reference layout.  Thread (token, j) of head blockIdx.y writes the eight
+// codes of dims 8j..8j+7 (one 8-byte store); lane j == 0 also writes the token's
+// scale and zero point.
 __global__ __launch_bounds__(256) void unpack_tokens_kernel(
     const uint8_t* __restrict__ pool, int64_t pool_blocks, const int32_t* __restrict__ bt, int H,
     int T, int which, uint8_t* __restrict__ codes, float* __restrict__ scales,
     uint8_t* __restrict__ zps) {
-    const int64_t total = (int64_t)H * T * kHeadDim;
+    const int h = blockIdx.y;
+    const int u = blockIdx.x * blockDim.x + threadIdx.x;
+    const int tok = u >> 4, j = u & 15;
+    if (tok >= T) return;
+    const int phys = bt[tok / kBlockTokens];
+    if (phys < 0 || (int64_t)phys >= pool_blocks) return;
     const RecordLayout L(H);
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-        const int d = (int)(i % kHeadDim);
-        const int tok = (int)((i / kHeadDim) % T);
-        const int h = (int)(i / ((int64_t)kHeadDim * T));
-        const int phys = bt[tok / kBlockTokens];
-        if (phys < 0 || (int64_t)phys >= pool_blocks) continue;
-        const uint8_t* rec = pool + (int64_t)phys * L.bytes;
-        const int s = tok % kBlockTokens;
-        uint32_t code;
-        if (which == 0) {
-            const uint32_t w = *(const uint32_t*)(rec + L.kc(h) + s * kCodeRowBytes + (d >> 3) * 4);
-            code = (w >> nib_shift(d & 7)) & 0xFu;
-        } else {
-            const int g = s >> 2, ii = s & 3, c = d & 15, n = d >> 4;
-            const int m = n >> 1, k = ii + (n & 1) * 4;
-            const uint32_t w = ((const uint32_t*)(rec + L.vc(h)))[(g * 16 + c) * 4 + m];
-            code = (w >> nib_shift(k)) & 0xFu;
+    const uint8_t* rec = pool + (int64_t)phys * L.bytes;
+    const int s = tok % kBlockTokens;
+    uint32_t lo = 0, hi = 0;   // codes of dims 8j..8j+3 and 8j+4..8j+7, one per byte
+    if (which == 0) {
+        const uint32_t w = *(const uint32_t*)(rec + L.kc(h) + s * kCodeRowBytes + j * 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t code = (w >> nib_shift(e)) & 0xFu;
+            if (e < 4) lo |= code << (8 * e);
+            else hi |= code << (8 * (e - 4));
         }
-        if (codes) codes[i] = (uint8_t)code;
-        if (d == 0) {
-            const int64_t gi = (int64_t)h * T + tok;
-            if (scales) scales[gi] = ((const float*)(rec + (which ? L.vs(h) : L.ks(h))))[s];
-            if (zps) zps[gi] = (rec + (which ? L.vz(h) : L.kz(h)))[s];
+    } else {
+        // dim d = c + 16 n: word (g * 16 + c) * 4 + n / 2, nibble (s % 4) + 4 (n % 2)
+        const int g = s >> 2, ii = s & 3;
+        const uint32_t* vw = (const uint32_t*)(rec + L.vc(h));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int d = 8 * j + e, c = d & 15, n = d >> 4;
+            const uint32_t w = vw[(g * 16 + c) * 4 + (n >> 1)];
+            const uint32_t code = (w >> nib_shift(ii + (n & 1) * 4)) & 0xFu;
+            if (e < 4) lo |= code << (8 * e);
+            else hi |= code << (8 * (e - 4));
+        }
+    }
+    const int64_t row = (int64_t)h * T + tok;
+    if (codes) *(uint2*)(codes + row * kHeadDim + 8 * j) = make_uint2(lo, hi);
+    if (j == 0) {
+        if (scales) scales[row] = ((const float*)(rec + (which ? L.vs(h) : L.ks(h))))[s];
+        if (zps) zps[row] = (rec + (which ? L.vz(h) : L.kz(h)))[s];
+    }
+}
+
+// The same for group sizes and lengths that are multiples of 8 with 8-byte aligned
+// codes and 16-byte aligned output: thread t converts codes 8t..8t+7 (one group),
+// one 8-byte load and one or two 16-byte stores.
+__global__ __launch_bounds__(256) void dequantize_groups8_kernel(
+    const uint8_t* __restrict__ codes, const float* __restrict__ scales,
+    const uint8_t* __restrict__ zps, int64_t n8, int G8, void* __restrict__ out, int out_dtype) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n8; t += stride) {
+        const int64_t g = n8 <= 0x7fffffff ? (int64_t)((uint32_t)t / (uint32_t)G8) : t / G8;
+        const float zp = (float)zps[g], sc = scales[g];
+        const uint2 w = *(const uint2*)(codes + 8 * t);
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = ((float)(((e < 4 ? w.x : w.y) >> (8 * (e & 3))) & 0xffu) - zp) * sc;
+        if (out_dtype == HKV_DTYPE_F32) {
+            float4* o = (float4*)out + 2 * t;
+            o[0] = make_float4(v[0], v[1], v[2], v[3]);
+            o[1] = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+            uint32_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t a = out_dtype == HKV_DTYPE_F16 ? f2h_rn(v[2 * e]) : f2bf_rn(v[2 * e]);
+                const uint32_t b = out_dtype == HKV_DTYPE_F16 ? f2h_rn(v[2 * e + 1]) : f2bf_rn(v[2 * e + 1]);
+                h[e] = a | (b << 16);
+            }
+            ((uint4*)out)[t] = make_uint4(h[0], h[1], h[2], h[3]);
         }
     }
 }
@@ -326,9 +377,17 @@ extern "C" int hkv_dequantize_groups(const uint8_t* codes, const float* scales, 
                 HKV_ERR_ARG, "hkv_dequantize_groups: unsupported dtype %d", out_dtype);
     if (n == 0) return HKV_OK;
     HKV_REQUIRE(codes && scales && zps && out, HKV_ERR_ARG, "hkv_dequantize_groups: null pointer");
-    const int blocks = grid_for(n, 256 * 4);
+    if (group_size % 8 == 0 && n % 8 == 0 && ((uintptr_t)codes & 7) == 0 && ((uintptr_t)out & 15) == 0) {
+        const int64_t n8 = n / 8;
+        hipLaunchKernelGGL(dequantize_groups8_kernel, dim3(grid_for(n8, 256)), dim3(256), 0, (hipStream_t)stream,
+                           codes, scales, zps, n8, group_size / 8, out, out_dtype);
+        HKV_LAUNCH_CHECK("dequantize_groups8_kernel");
+        return HKV_OK;
+    }
+    const int64_t ngroups = (n + group_size - 1) / group_size;
+    const int blocks = grid_for(ngroups, 4);
     hipLaunchKernelGGL(dequantize_groups_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
-                       codes, scales, zps, n, group_size, out, out_dtype);
+                       codes, scales, zps, n, group_size, ngroups, out, out_dtype);
     HKV_LAUNCH_CHECK("dequantize_groups_kernel");
     return HKV_OK;
 }
@@ -383,8 +442,11 @@ extern "C" int hkv_unpack_tokens(const uint8_t* pool, int64_t pool_blocks, const
     HKV_REQUIRE(num_kv_heads > 0 && num_tokens >= 0, HKV_ERR_ARG, "hkv_unpack_tokens: bad sizes");
     if (num_tokens == 0) return HKV_OK;
     HKV_REQUIRE(pool && block_table && pool_blocks > 0, HKV_ERR_ARG, "hkv_unpack_tokens: null pool/table");
-    const int64_t total = (int64_t)num_kv_heads * num_tokens * kHeadDim;
-    hipLaunchKernelGGL(unpack_tokens_kernel, dim3(grid_for(total, 256 * 4)), dim3(256), 0,
+    HKV_REQUIRE(num_kv_heads <= 65535 && num_tokens <= (1 << 26), HKV_ERR_ARG, "hkv_unpack_tokens: grid too large");
+    HKV_REQUIRE(codes == nullptr || ((uintptr_t)codes & 7) == 0, HKV_ERR_ARG,
+                "hkv_unpack_tokens: codes must be 8-byte aligned");
+    const int64_t threads = (int64_t)num_tokens * 16;
+    hipLaunchKernelGGL(unpack_tokens_kernel, dim3((unsigned)((threads + 255) / 256), num_kv_heads), dim3(256), 0,
                        (hipStream_t)stream, pool, pool_blocks, block_table, num_kv_heads, num_tokens,
                        which, codes, scales, zps);
     HKV_LAUNCH_CHECK("unpack_tokens_kernel");
