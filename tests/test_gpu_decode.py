@@ -182,6 +182,32 @@ def test_schedules_agree_on_long_windows():
     _check(c, splits=1)
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_random_geometries(seed):
+    """Seeded random geometries against the float64 oracle in both schedules: batch 1-4,
+    1-8 kv heads, n_rep 1-16, sink 0-100, ragged INT4 (0-6000) and recent (0-700) lengths,
+    and forced range counts, so that single-kind and mixed ranges, partial blocks,
+    empty zones and several placements of the XCD-local hand-off all occur."""
+    from heterokv import ops
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 5))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    nrep = int(rng.choice([1, 2, 4, 7, 8, 16]))
+    sink = int(rng.choice([0, 16, 64, 100]))
+    mids = [int(x) for x in rng.integers(0, 6001, B)]
+    recents = [int(x) for x in rng.integers(0, 701, B)]
+    for b in range(B):
+        if sink + mids[b] + recents[b] == 0:
+            recents[b] = 1
+    splits = int(rng.choice([0, 0, 1, 3, 7, 64]))
+    print("case: seed %d B=%d hkv=%d nrep=%d sink=%d mids=%s recents=%s splits=%d"
+          % (seed, B, hkv, nrep, sink, mids, recents, splits), flush=True)
+    c = Case(2000 + seed, B, hkv * nrep, hkv, sink, mids, recents)
+    ws = ops.DecodeWorkspace(DEV)
+    _check(c, splits=splits, workspace=ws)
+    assert ws.error_flag() == 0
+
+
 def test_reference_api_fused_dequant_attn_decode():
     """fused_dequant_attn_decode with the reference harness's inputs
     (unified_benchmark.py:142-164: per-head compress, float zero points)."""
