@@ -105,6 +105,30 @@ __device__ __forceinline__ void load16(const void* src, int dtype, int64_t off, 
     }
 }
 
+// Every lane of the 256 assembles one V word of head h's part of the record from the
+// V codes staged in LDS; rows outside [lo, hi) keep their previous contents.
+__device__ __forceinline__ void write_v_words(const uint8_t (&codes)[2][kBlockTokens][kHeadDim], int lo, int hi,
+                                              uint8_t* rec, const RecordLayout& L, int h) {
+    const int t = threadIdx.x;
+    // V word t = (g*16 + c)*4 + m: tokens 4g..4g+3, dims c+32m (x0..x3) and c+32m+16 (x4..x7).
+    const int g = t >> 6, c = (t >> 2) & 15, m = t & 3;
+    uint32_t w = 0, mask = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int tok = 4 * g + (k & 3);
+        const int dim = c + 32 * m + (k >> 2) * 16;
+        if (tok >= lo && tok < hi) {
+            w |= (uint32_t)codes[1][tok][dim] << nib_shift(k);
+            mask |= 0xFu << nib_shift(k);
+        }
+    }
+    if (mask) {
+        uint32_t* dst = (uint32_t*)(rec + L.vc(h)) + t;
+        if (mask != 0xFFFFFFFFu) w |= (*dst & ~mask);
+        *dst = w;
+    }
+}
+
 // Phase 2 of both packers: every lane of the 256 assembles one K word and one V
 // word of head h's part of the record from codes staged in LDS; rows outside
 // [lo, hi) keep their previous contents.
@@ -162,7 +186,7 @@ __global__ __launch_bounds__(256) void pack_tokens_kernel(PackParams p) {
     const RecordLayout L(p.H);
     uint8_t* rec = p.pool + (int64_t)phys * L.bytes;
 
-    __shared__ uint8_t codes[2][kBlockTokens][kHeadDim];
+    __shared__ __align__(16) uint8_t codes[2][kBlockTokens][kHeadDim];
 
     const int t = threadIdx.x;
     const int row = t >> 3;
@@ -187,8 +211,27 @@ __global__ __launch_bounds__(256) void pack_tokens_kernel(PackParams p) {
     }
     if (active) {
         const QParams q = qparams_from_minmax(mn, mx);
+        uint32_t cw[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) codes[kv][slot][part * 16 + i] = (uint8_t)quant_code(vals[i], q);
+        for (int i = 0; i < 16; ++i) cw[i] = quant_code(vals[i], q);
+        if (kv == 0) {
+            // this lane's 16 K codes are K words 2 part and 2 part + 1 of the row: packed
+            // here and written to the record directly
+            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                w0 |= cw[k] << nib_shift(k);
+                w1 |= cw[8 + k] << nib_shift(k);
+            }
+            *(uint2*)(rec + L.kc(h) + slot * kCodeRowBytes + part * 8) = make_uint2(w0, w1);
+        } else {
+            // V words mix four tokens: the codes go through LDS, one 16-byte write
+            uint32_t b4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                b4[i] = cw[4 * i] | (cw[4 * i + 1] << 8) | (cw[4 * i + 2] << 16) | (cw[4 * i + 3] << 24);
+            *(uint4*)&codes[1][slot][part * 16] = make_uint4(b4[0], b4[1], b4[2], b4[3]);
+        }
         if (part == 0) {
             float* sc = (float*)(rec + (kv ? L.vs(h) : L.ks(h))) + slot;
             uint8_t* zp = rec + (kv ? L.vz(h) : L.kz(h)) + slot;
@@ -197,7 +240,7 @@ __global__ __launch_bounds__(256) void pack_tokens_kernel(PackParams p) {
         }
     }
     __syncthreads();
-    write_block_words(codes, lo, hi, rec, L, h);
+    write_v_words(codes, lo, hi, rec, L, h);
 }
 
 // Already-quantized tokens in the reference layout (codes uint8 [.., T, 128] and
