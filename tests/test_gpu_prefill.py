@@ -137,3 +137,25 @@ def test_reference_api_fused_dequant_attn_forward():
     err = np.abs(out[0].float().cpu().numpy() - ref).max()
     print("  max abs err %.3e" % err, flush=True)
     assert out.shape == (1, H, Sq, 128) and err <= TOL
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_geometries(seed):
+    """Seeded random shapes: batch 1-3, 1-4 kv heads, GQA ratio 1-8, 1-200 queries, ragged
+    INT4 / recent lengths (zeros included), sink on or off, with or without the causal chunk,
+    and a softmax sharpness between flat and sharp."""
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 4))
+    Hkv = int(rng.integers(1, 5))
+    nrep = int(rng.integers(1, 9))
+    Sq = int(rng.integers(1, 201))
+    sink = int(rng.choice([0, 1, 17, 64, 80]))
+    mids = [int(rng.choice([0, int(rng.integers(1, 700))])) for _ in range(B)]
+    recents = [int(rng.integers(0, 300)) for _ in range(B)]
+    causal = bool(rng.integers(0, 2))
+    if not causal and (sink == 0 and min(m + r for m, r in zip(mids, recents)) == 0):
+        causal = True   # every row must see at least one token
+    q_scale = float(rng.choice([0.5, 1.0, 4.0]))
+    print("case: prefill seed %d B=%d %d/%d Sq=%d sink %d mids %s recents %s causal %s q_scale %g" % (
+        seed, B, Hkv * nrep, Hkv, Sq, sink, mids, recents, causal, q_scale), flush=True)
+    _case(2000 + seed, B, Hkv * nrep, Hkv, Sq, sink, mids, recents, causal=causal, q_scale=q_scale)
