@@ -134,3 +134,68 @@ def test_prefetcher_and_gather_argument_errors(lib):
     assert lib.hkv_gather_blocks(None, 0, None, 0, None, 0, 8832, None, None, None) == 0
     assert lib.hkv_gather_blocks(4096, 4, None, 0, 4096, 2, 8830, 4096, None, None) == -1
     assert lib.hkv_gather_blocks(4096, 4, None, 2, 4096, 2, 8832, 4096, None, None) == -1
+
+
+def _err(lib, rc, code, text):
+    assert rc == code, (rc, lib.hkv_last_error())
+    assert text in lib.hkv_last_error(), lib.hkv_last_error()
+
+
+def test_pack_and_unpack_argument_errors(lib):
+    from heterokv import _lib
+    a = _lib.PackArgs()
+    a.batch, a.num_kv_heads, a.head_dim, a.num_tokens, a.dtype = 1, 8, 64, 16, 0
+    _err(lib, lib.hkv_pack_tokens(ctypes.byref(a), None), -4, b"head_dim")
+    a.head_dim = 128
+    a.dtype = 2                                     # fp32 K/V are not packed (the reference's K/V are fp16/bf16)
+    _err(lib, lib.hkv_pack_tokens(ctypes.byref(a), None), -1, b"dtype")
+    a.dtype = 0
+    a.num_kv_heads = 0
+    _err(lib, lib.hkv_pack_tokens(ctypes.byref(a), None), -1, b"hkv_pack_tokens")
+    a.num_kv_heads = 8
+    _err(lib, lib.hkv_pack_tokens(ctypes.byref(a), None), -1, b"hkv_pack_tokens")   # null pointers
+    a.k = a.v = a.start_pos = a.block_table = a.pool = 4096
+    a.bt_stride, a.pool_blocks = 1, 0
+    _err(lib, lib.hkv_pack_tokens(ctypes.byref(a), None), -1, b"empty")
+    # unpack(pool, pool_blocks, block_table, num_kv_heads, head_dim, num_tokens, which, codes, scales, zps, stream)
+    _err(lib, lib.hkv_unpack_tokens(4096, 1, 4096, 8, 64, 16, 0, None, None, None, None), -4, b"head_dim")
+    _err(lib, lib.hkv_unpack_tokens(4096, 1, 4096, 8, 128, 16, 2, None, None, None, None), -1, b"which")
+    _err(lib, lib.hkv_unpack_tokens(4096, 1, 4096, 0, 128, 16, 0, None, None, None, None), -1, b"sizes")
+    _err(lib, lib.hkv_unpack_tokens(None, 1, 4096, 8, 128, 16, 0, None, None, None, None), -1, b"null")
+    _err(lib, lib.hkv_unpack_tokens(4096, 1, 4096, 8, 128, 16, 0, 4097, None, None, None), -1, b"hkv_unpack_tokens")
+    # dequantize_groups(codes, scales, zps, n, group_size, out, out_dtype, stream)
+    _err(lib, lib.hkv_dequantize_groups(4096, 4096, 4096, 128, 0, 4096, 0, None), -1, b"group_size")
+    _err(lib, lib.hkv_dequantize_groups(4096, 4096, 4096, 128, 128, 4096, 9, None), -1, b"hkv_dequantize_groups")
+    _err(lib, lib.hkv_dequantize_groups(None, 4096, 4096, 128, 128, 4096, 0, None), -1, b"null")
+
+
+def test_prefill_argument_errors(lib):
+    from heterokv import _lib
+    a = _lib.PrefillArgs()
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.num_queries = 1, 32, 8, 64, 4
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -4, b"head_dim")
+    a.head_dim = 128
+    a.num_q_heads = 30
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"multiple")
+    a.num_q_heads = 32
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"null q/out")
+    a.q, a.out = 4098, 8192                        # q not 16-byte aligned
+    a.q_stride_b, a.q_stride_h, a.q_stride_t = 32 * 4 * 128, 4 * 128, 128
+    a.out_stride_b, a.out_stride_h, a.out_stride_t = 32 * 4 * 128, 4 * 128, 128
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"16-byte")
+    a.q = 4096
+    a.chunk_k = 16384                              # chunk K without chunk V
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"both")
+    a.chunk_k = None
+    a.int4_max_len = -1
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"int4_max_len")
+    a.int4_max_len = 100
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"block table")
+    a.block_table, a.pool, a.pool_blocks, a.bt_stride = 4096, 65536, 8, 6   # 6 blocks hold 96 < 100 tokens
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -3, b"stride")
+    a.bt_stride = 7
+    a.num_f16_zones = 1
+    a.f16[0] = _lib.F16Zone(k=4096, v=4096, capacity=64, max_len=65, lens=None)
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"zone 0")
+    a.f16[0] = _lib.F16Zone(k=4100, v=4096, capacity=64, max_len=64, lens=None)
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"misaligned")
