@@ -199,3 +199,41 @@ def test_prefill_argument_errors(lib):
     _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"zone 0")
     a.f16[0] = _lib.F16Zone(k=4100, v=4096, capacity=64, max_len=64, lens=None)
     _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"misaligned")
+
+
+def test_zone_and_scoring_argument_errors(lib):
+    from heterokv import _lib
+    w = _lib.ZoneWriteArgs()
+    w.batch, w.num_kv_heads, w.head_dim, w.num_tokens, w.capacity = 1, 8, 64, 4, 64
+    _err(lib, lib.hkv_zone_write(ctypes.byref(w), None), -4, b"head_dim")
+    w.head_dim, w.capacity = 128, 60                 # capacity must be a multiple of 16
+    _err(lib, lib.hkv_zone_write(ctypes.byref(w), None), -1, b"hkv_zone_write")
+    w.capacity = 64
+    _err(lib, lib.hkv_zone_write(ctypes.byref(w), None), -1, b"hkv_zone_write")   # null pointers
+    w.k = w.v = w.zone_k = w.zone_v = 4096
+    w.ring = 65                                      # ring longer than the zone
+    _err(lib, lib.hkv_zone_write(ctypes.byref(w), None), -1, b"hkv_zone_write")
+    # zone_read(zone_k, zone_v, batch, num_kv_heads, head_dim, capacity, n, out_k, out_v, stream)
+    _err(lib, lib.hkv_zone_read(4096, 4096, 1, 8, 64, 64, 4, 4096, 4096, None), -4, b"head_dim")
+    _err(lib, lib.hkv_zone_read(4096, 4096, 1, 8, 128, 64, 65, 4096, 4096, None), -1, b"hkv_zone_read")
+    _err(lib, lib.hkv_zone_read(4096, 4096, 1, 8, 128, 64, 4, None, None, None), -1, b"null")
+    # zone_copy(src_k, src_v, src_cap, src_slot, dst_k, dst_v, dst_cap, dst_slot, batch, heads, head_dim, n, stream)
+    _err(lib, lib.hkv_zone_copy(4096, 4096, 64, 0, 8192, 8192, 64, 0, 1, 8, 64, 4, None), -4, b"head_dim")
+    _err(lib, lib.hkv_zone_copy(4096, 4096, 64, 62, 8192, 8192, 64, 0, 1, 8, 128, 4, None), -3, b"slot range")
+    _err(lib, lib.hkv_zone_copy(None, 4096, 64, 0, 8192, 8192, 64, 0, 1, 8, 128, 4, None), -1, b"null")
+    # attn_weights(scores, sb, sh, stats, batch, heads, n_items, order, out, out_stride_b, accumulate, stream)
+    _err(lib, lib.hkv_attn_weights(4096, 64, 64, 4096, 0, 4, 64, None, 4096, 64, 0, None), -1, b"sizes")
+    _err(lib, lib.hkv_attn_weights(None, 64, 64, 4096, 1, 4, 64, None, 4096, 64, 0, None), -1, b"null")
+    _err(lib, lib.hkv_attn_weights(4096, 64, 64, 4096, 1, 4, 64, None, 4096, 32, 0, None), -1, b"stride")
+    # block_scores(token_scores, seq_len, block_size, out, stream)
+    _err(lib, lib.hkv_block_scores(4096, 64, 0, 4096, None), -1, b"sizes")
+    _err(lib, lib.hkv_block_scores(None, 64, 16, 4096, None), -1, b"null")
+    # eviction_candidates(scores, seq_len, block_size, sink, window, max_blocks, out, num_out, ws, ws_bytes, stream)
+    n = ctypes.c_int32()
+    _err(lib, lib.hkv_eviction_candidates(4096, 64, 0, 0, 0, 4, 4096, ctypes.byref(n), 4096, 1 << 20, None), -1,
+         b"hkv_eviction_candidates")
+    _err(lib, lib.hkv_eviction_candidates(4096, 64, 16, 0, 0, 4, 4096, None, 4096, 1 << 20, None), -1, b"num_out")
+    need = lib.hkv_eviction_workspace_bytes(4096, 16, 0, 0, 4)
+    assert need > 0
+    _err(lib, lib.hkv_eviction_candidates(4096, 4096, 16, 0, 0, 4, 4096, ctypes.byref(n), 4096, need - 8, None), -3,
+         b"workspace")
