@@ -677,8 +677,8 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the decode path shards by kv head or "
-              "sequence with no exchange; see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the decode path would shard by kv head or "
+              "sequence, with no exchange between GPUs); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
