@@ -237,3 +237,27 @@ def test_zone_and_scoring_argument_errors(lib):
     assert need > 0
     _err(lib, lib.hkv_eviction_candidates(4096, 4096, 16, 0, 0, 4, 4096, ctypes.byref(n), 4096, need - 8, None), -3,
          b"workspace")
+
+
+def test_repack_and_zone_step_argument_errors(lib):
+    from heterokv import _lib
+    r = _lib.RepackArgs()
+    r.batch, r.num_kv_heads, r.head_dim, r.num_tokens, r.zp_dtype = 1, 8, 64, 16, 3
+    _err(lib, lib.hkv_repack_codes(ctypes.byref(r), None), -4, b"head_dim")
+    r.head_dim, r.zp_dtype = 128, 0                 # zero points are uint8 or float32
+    _err(lib, lib.hkv_repack_codes(ctypes.byref(r), None), -1, b"zp dtype")
+    r.zp_dtype = 3
+    _err(lib, lib.hkv_repack_codes(ctypes.byref(r), None), -1, b"null")
+    r.num_tokens = 0
+    assert lib.hkv_repack_codes(ctypes.byref(r), None) == 0   # nothing to do
+    z = _lib.ZoneStepArgs()
+    z.batch, z.num_kv_heads, z.head_dim = 1, 8, 64
+    _err(lib, lib.hkv_zone_step(ctypes.byref(z), None), -4, b"head_dim")
+    z.head_dim = 128
+    _err(lib, lib.hkv_zone_step(ctypes.byref(z), None), -1, b"null")
+    z.k = z.v = z.tail_k = z.tail_v = z.state = 4096
+    z.tail_capacity, z.tail_ring = 64, 80           # ring longer than the tail zone
+    _err(lib, lib.hkv_zone_step(ctypes.byref(z), None), -1, b"tail ring")
+    z.tail_ring = 64
+    z.hh_budget, z.hh_capacity = 32, 16             # heavy-hitter zone smaller than its budget
+    _err(lib, lib.hkv_zone_step(ctypes.byref(z), None), -1, b"heavy-hitter")
