@@ -30,15 +30,19 @@
 // workgroup 0 rotates from launch to launch, so only the id modulo the XCD count
 // is fixed).  When every range of a pair shares an XCD (pairs a multiple of the
 // XCD count), the hand-off stays in that XCD's L2: plain stores, an L2 atomic
-// ticket and L1-bypassing loads.  Otherwise it goes through memory with
-// agent-scope (sc1) accesses.  Each range tags its L2 partial state with its XCD
-// id; the merging workgroup reports a tag that is not its own in the error word
-// (bit 2) and clears the tags.
+// ticket and L1-bypassing loads.  Otherwise (or with HKV_DECODE_AGENT_HANDOFF) it
+// goes through memory with agent-scope (sc1) accesses.  The placement is checked
+// on every launch: each workgroup ORs its XCD bit into a device-scope mask of its
+// pair as its first memory operation and reads the old mask back before its
+// ticket; a foreign bit (or a ticket beyond the range count, left by such a
+// launch) sets HKV_ERR_BIT_PLACEMENT.  The merging workgroup clears the mask.
 #include "hkv_internal.h"
 #include "nibble_decode.h"
 
 #include <math.h>
 #include <string.h>
+
+#include <mutex>
 
 namespace hkv {
 namespace {
@@ -83,6 +87,7 @@ struct ZoneP {
 struct DecodeParams {
     int B, Hkv, nrep;
     float scale_log2;
+    int q_bf16, out_bf16;     // q / out dtype is bfloat16 (else fp16)
     const uint16_t* q;
     int64_t q_sb, q_sh;
     int nz;
@@ -100,6 +105,7 @@ struct DecodeParams {
     int64_t o_sb, o_sh;
     int* err;
     int* counters;            // agent-scope tickets, one int per pair
+    unsigned* owners;         // agent-scope XCD masks, one per pair (placement check)
     int* counters_l2;         // XCD-local tickets, one 256-byte line per pair
     float* partials;
     int max_splits;
@@ -512,8 +518,14 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const int c = lane & 15, g = lane >> 4;
     const int kzsh = 8 * (c & 3);
     const int nrep = p.nrep;
-    // this workgroup's XCD (HW_REG_XCC_ID); tags its partial state in the L2 hand-off
-    const int xcc_tag = p.xcc_local ? (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15) + 1 : 0;
+    // XCD-local hand-off: OR this workgroup's XCD bit (HW_REG_XCC_ID) into the pair's
+    // device-scope mask first; the old mask is only examined before the ticket, so the
+    // round trip overlaps the streaming
+    unsigned owner_old = 0u, owner_bit = 0u;
+    if (p.xcc_local && threadIdx.x == 0) {
+        owner_bit = 1u << (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
+        owner_old = __hip_atomic_fetch_or(&p.owners[bh], owner_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 
     const int len4 = p.int4_lens ? min(max(p.int4_lens[b], 0), p.int4_max_len) : p.int4_max_len;
     int lenz[HKV_MAX_F16_ZONES];
@@ -560,11 +572,24 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     {
         const bool has = c < nrep;
         const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)(h * nrep + (has ? c : 0)) * p.q_sh + 32 * g;
+        bool over = false;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const u4 w = has ? *(const u4*)(qp + 8 * j) : u4{0u, 0u, 0u, 0u};
+            u4 w = has ? *(const u4*)(qp + 8 * j) : u4{0u, 0u, 0u, 0u};
+            if (p.q_bf16) {
+                // bf16 -> fp16: exact in [2^-14, 65504]; a finite value beyond becomes inf
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xffff0000u);
+                    const uint32_t a = f2h_rn(lo), bb = f2h_rn(hi);
+                    over |= (((a & 0x7fffu) == 0x7c00u) && fabsf(lo) < INFINITY) ||
+                            (((bb & 0x7fffu) == 0x7c00u) && fabsf(hi) < INFINITY);
+                    w[e] = a | (bb << 16);
+                }
+            }
             qf[j] = __builtin_bit_cast(h8, w);
         }
+        if (__ballot(over) && lane == 0 && p.err) atomicOr(p.err, HKV_ERR_BIT_RANGE);
     }
 
     f4 acc[8];
@@ -731,7 +756,8 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             L += sm_l[w * 16 + hd] * e;
         }
         if (nsplit == 1) {
-            p.out[(int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d] = f2h_rn(L > 0.f ? O / L : 0.f);
+            const float r = L > 0.f ? O / L : 0.f;
+            p.out[(int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d] = p.out_bf16 ? f2bf_rn(r) : f2h_rn(r);
             if (kScores && d == 0) {
                 float* st = p.stats + ((int64_t)b * p.Hkv * nrep + h * nrep + hd) * 2;
                 st[0] = M;
@@ -742,7 +768,6 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             if (d == 0) {
                 part[hd * kPartStride + kHeadDim] = M;
                 part[hd * kPartStride + kHeadDim + 1] = L;
-                if (hd == 0) reinterpret_cast<int*>(part)[kHeadDim + 2] = xcc_tag;
             }
         } else {
             st_agent(part + hd * kPartStride + d, O);
@@ -762,10 +787,24 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     __syncthreads();
     if (threadIdx.x == 0) {
         // the stores above have completed (in L2, or in memory for sc1 stores)
+        int tk;
         if (p.xcc_local)
-            sm_ticket = __hip_atomic_fetch_add(&p.counters_l2[bh * 64], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            tk = __hip_atomic_fetch_add(&p.counters_l2[bh * 64], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         else
-            sm_ticket = __hip_atomic_fetch_add(&p.counters[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            tk = __hip_atomic_fetch_add(&p.counters[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // another XCD's bit in the mask: this pair's ranges did not share one L2.  A
+        // ticket beyond the range count is what such a launch leaves behind; it is
+        // reset so that later launches count from zero again.
+        const bool foreign = (owner_old & ~owner_bit) != 0u;
+        if (tk >= nsplit) {
+            if (p.xcc_local)
+                __hip_atomic_store(&p.counters_l2[bh * 64], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            else
+                __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if ((foreign || tk >= nsplit) && p.err)
+            __hip_atomic_fetch_or(p.err, HKV_ERR_BIT_PLACEMENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sm_ticket = tk;
     }
     __syncthreads();
     if (sm_ticket != nsplit - 1) return;
@@ -778,13 +817,6 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const float* parts = p.partials + (int64_t)bh * p.part_pair_stride;
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)parts, 0, (int)(nsplit * nrep * kPartStride * sizeof(float)), 0x00020000);
-    // Placement check: a range that ran on another XCD left its state and tag in that
-    // XCD's L2, and this L2 still holds the tag the last merge cleared.  Thread s
-    // reads range s's tag (head 0's row) ahead of the merge loads and checks and
-    // clears it at the end.
-    int tag = xcc_tag;
-    if (p.xcc_local && (int)threadIdx.x < nsplit)
-        tag = __float_as_int(ld_l2(prs, ((int)threadIdx.x * (nrep * kPartStride) + kHeadDim + 2) * 4));
     const int units = nrep * (kHeadDim / 4);
     const int K = kThreads / units;                  // >= 1 because nrep <= 16
     float* sm = smem;                                // [K][units][6] = (M, L, O[4])
@@ -846,25 +878,29 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         const float inv = L > 0.f ? 1.0f / L : 0.f;
         uint16_t* op = p.out + (int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d4;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) op[v] = f2h_rn(O[v] * inv);
+        for (int v = 0; v < 4; ++v) op[v] = p.out_bf16 ? f2bf_rn(O[v] * inv) : f2h_rn(O[v] * inv);
         if (kScores && d4 == 0) {
             float* st = p.stats + ((int64_t)b * p.Hkv * nrep + h * nrep + hd) * 2;
             st[0] = M;
             st[1] = L;
         }
     }
+    // last in the kernel, so that no barrier waits for these stores: every workgroup of
+    // the pair has taken its ticket, so its mask update is done
     if (threadIdx.x == 0) {
-        if (p.xcc_local)
+        if (p.xcc_local) {
             __hip_atomic_store(&p.counters_l2[bh * 64], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        else
+            __hip_atomic_store(&p.owners[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
             __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
-    // last in the kernel, so that no barrier waits for these stores
-    if (p.xcc_local && (int)threadIdx.x < nsplit) {
-        if (tag != xcc_tag && p.err) atomicOr(p.err, 4);
-        // the clear is ordered after the tag load by its use of the loaded value
-        if (tag != -1) reinterpret_cast<int*>(const_cast<float*>(parts))[threadIdx.x * (nrep * kPartStride) + kHeadDim + 2] = 0;
-    }
+}
+
+// Clears a workspace's ticket area (int words) before a launch whose geometry differs
+// from the previous launch on the same workspace.
+__global__ __launch_bounds__(256) void clear_words_kernel(int* w, int64_t n) {
+    for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) w[i] = 0;
 }
 
 constexpr size_t kWsHeader = 256;
@@ -898,14 +934,48 @@ int choose_splits(int BH, int int4_max_len, const int32_t* f16_max_lens, int nz,
     return (int)s;
 }
 
-// Workspace: [header (error word) | agent tickets | XCD-local tickets (256 B each) |
-// partial states, one 256-byte aligned block per (sequence, kv head)].
+// Workspace: [header (error word) | agent tickets | XCD masks | XCD-local tickets
+// (256 B each) | partial states, one 256-byte aligned block per (sequence, kv head)].
+// The ticket area [kWsHeader, partials) must be zero at a launch; it depends only on
+// the pair count.
 size_t pair_part_bytes(int nrep, int nsplit) { return align256((size_t)nsplit * nrep * kPartStride * sizeof(float)); }
+
+size_t ticket_area_end(size_t BH) { return kWsHeader + 2 * align256(BH * sizeof(int)) + BH * 256; }
 
 size_t workspace_bytes(int B, int Hq, int Hkv, int nsplit) {
     const size_t BH = (size_t)B * Hkv;
     const int nrep = Hq / Hkv;
-    return kWsHeader + align256(BH * sizeof(int)) + BH * 256 + BH * pair_part_bytes(nrep, nsplit);
+    return ticket_area_end(BH) + BH * pair_part_bytes(nrep, nsplit);
+}
+
+// Pair count of the last launch on each workspace address.  A launch with another
+// pair count moves the ticket area over bytes that held partial states, so the area
+// is cleared first (one small kernel on the launch's stream).
+struct WsGeom {
+    const void* ws;
+    int64_t bh;
+};
+std::mutex g_ws_mu;
+WsGeom g_ws[64];
+int g_ws_next = 0;
+
+bool ws_needs_clear(const void* ws, int64_t bh) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    for (auto& e : g_ws)
+        if (e.ws == ws) {
+            const bool changed = e.bh != bh;
+            e.bh = bh;
+            return changed;
+        }
+    g_ws[g_ws_next] = WsGeom{ws, bh};
+    g_ws_next = (g_ws_next + 1) % 64;
+    return true;
+}
+
+void ws_forget(const void* ws) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    for (auto& e : g_ws)
+        if (e.ws == ws) e = WsGeom{nullptr, 0};
 }
 
 // XCDs that workgroups are dispatched over round-robin: gfx950 has 32 CUs per
@@ -958,8 +1028,12 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     HKV_REQUIRE(nrep <= 16, HKV_ERR_UNSUPPORTED, "hkv_decode_attn: n_rep %d > 16", nrep);
     HKV_REQUIRE(a->num_f16_zones >= 0 && a->num_f16_zones <= HKV_MAX_F16_ZONES, HKV_ERR_ARG,
                 "hkv_decode_attn: num_f16_zones %d out of range", a->num_f16_zones);
-    HKV_REQUIRE((a->flags & ~HKV_DECODE_DETERMINISTIC) == 0, HKV_ERR_ARG, "hkv_decode_attn: unknown flags 0x%x",
-                (unsigned)a->flags);
+    HKV_REQUIRE((a->flags & ~(HKV_DECODE_DETERMINISTIC | HKV_DECODE_AGENT_HANDOFF)) == 0, HKV_ERR_ARG,
+                "hkv_decode_attn: unknown flags 0x%x", (unsigned)a->flags);
+    HKV_REQUIRE((a->q_dtype == HKV_DTYPE_F16 || a->q_dtype == HKV_DTYPE_BF16) &&
+                    (a->out_dtype == HKV_DTYPE_F16 || a->out_dtype == HKV_DTYPE_BF16),
+                HKV_ERR_ARG, "hkv_decode_attn: q/out dtype must be fp16 or bf16 (got %d / %d)", a->q_dtype,
+                a->out_dtype);
     if (a->scores) {
         HKV_REQUIRE(a->score_stats != nullptr, HKV_ERR_ARG, "hkv_decode_attn: scores without score_stats");
         int64_t row = a->int4_max_len;
@@ -1012,6 +1086,8 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     p.Hkv = a->num_kv_heads;
     p.nrep = nrep;
     p.scale_log2 = a->sm_scale * kLog2e;
+    p.q_bf16 = a->q_dtype == HKV_DTYPE_BF16;
+    p.out_bf16 = a->out_dtype == HKV_DTYPE_BF16;
     p.q = a->q;
     p.q_sb = a->q_stride_b;
     p.q_sh = a->q_stride_h;
@@ -1037,13 +1113,15 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     p.o_sb = a->out_stride_b;
     p.o_sh = a->out_stride_h;
     char* ws = (char*)a->workspace;
-    p.err = (int*)ws;
+    p.err = a->err_flag ? (int*)a->err_flag : (int*)ws;
     p.counters = (int*)(ws + kWsHeader);
-    p.counters_l2 = (int*)(ws + kWsHeader + align256((size_t)BH * sizeof(int)));
-    p.partials = (float*)(ws + kWsHeader + align256((size_t)BH * sizeof(int)) + (size_t)BH * 256);
+    p.owners = (unsigned*)(ws + kWsHeader + align256((size_t)BH * sizeof(int)));
+    p.counters_l2 = (int*)(ws + kWsHeader + 2 * align256((size_t)BH * sizeof(int)));
+    p.partials = (float*)(ws + ticket_area_end((size_t)BH));
     p.part_pair_stride = (int64_t)(pair_part_bytes(nrep, ms) / sizeof(float));
     p.nxcc = num_xcc();
-    p.xcc_local = (BH % p.nxcc) == 0 ? 1 : 0;
+    // one range per pair needs no hand-off (and must not leave a mask bit behind)
+    p.xcc_local = (BH % p.nxcc) == 0 && ms > 1 && !(a->flags & HKV_DECODE_AGENT_HANDOFF) ? 1 : 0;
     p.max_splits = ms;
     p.scores = a->scores;
     p.sc_sb = a->scores_stride_b;
@@ -1068,6 +1146,15 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     if (!raised[var]) {
         HKV_HIP_CHECK(hipFuncSetAttribute(fns[var], hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
         raised[var] = true;
+    }
+    if (ws_needs_clear(a->workspace, BH)) {
+        const int64_t words = (int64_t)(ticket_area_end((size_t)BH) - kWsHeader) / 4;
+        hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024)),
+                           dim3(256), 0, (hipStream_t)stream, (int*)(ws + kWsHeader), words);
+        if (hipGetLastError() != hipSuccess) {
+            ws_forget(a->workspace);
+            HKV_REQUIRE(false, HKV_ERR_HIP, "hkv_decode_attn: launch of the ticket clear failed");
+        }
     }
     const dim3 grid((unsigned)(BH * ms)), block(kThreads);
     switch (var) {

@@ -54,6 +54,7 @@ struct ZoneP {
 struct PrefillParams {
     int B, Hkv, nrep, Sq;
     float scale_log2;
+    int q_bf16, c_bf16, out_bf16;   // q / chunk / out dtype is bfloat16 (else fp16)
     const uint16_t* q;
     int64_t q_sb, q_sh, q_st;
     int nz;
@@ -94,6 +95,24 @@ __device__ __forceinline__ int vt_pair_addr(int dim, int gr, int hh) {
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return (uint32_t)f2h_rn(a) | ((uint32_t)f2h_rn(b) << 16);
+}
+__device__ __forceinline__ uint32_t pack2bf(float a, float b) {
+    return (uint32_t)f2bf_rn(a) | ((uint32_t)f2bf_rn(b) << 16);
+}
+
+// Eight bf16 values to fp16: exact in [2^-14, 65504]; `over` is set when a finite
+// value leaves the fp16 range (it becomes +-inf).
+__device__ __forceinline__ u4 bf16x8_to_f16(u4 w, bool& over) {
+    u4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xffff0000u);
+        const uint32_t a = f2h_rn(lo), b = f2h_rn(hi);
+        over |= (((a & 0x7fffu) == 0x7c00u) && fabsf(lo) < INFINITY) ||
+                (((b & 0x7fffu) == 0x7c00u) && fabsf(hi) < INFINITY);
+        r[e] = a | (b << 16);
+    }
+    return r;
 }
 
 // Staged global data of one tile for one thread (all tile kinds).
@@ -160,8 +179,19 @@ __device__ __forceinline__ void stage_load(const PrefillParams& p, const TileMap
 
 // Writes the staged data of one tile into LDS buffer `lds` (K rows + V^T), zeros for
 // slots past the valid length so that masked probabilities multiply finite values.
-__device__ __forceinline__ void stage_store(const Stage& s, uint8_t* lds, float scale_log2) {
+__device__ __forceinline__ void stage_store(Stage& s, uint8_t* lds, float scale_log2, bool chunk_bf16, int* err) {
     const int t = threadIdx.x;
+    if (chunk_bf16 && s.kind == 2) {
+        // rows past the chunk were not loaded: converted (and later zeroed), never checked
+        bool over = false;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            s.a[j] = bf16x8_to_f16(s.a[j], over);
+            s.b[j] = bf16x8_to_f16(s.b[j], over);
+        }
+        over = over && (t >> 2) < s.valid;
+        if (__ballot(over) && (t & 63) == 0 && err) atomicOr(err, HKV_ERR_BIT_RANGE);
+    }
     if (t < kT) {
         ((float*)(lds + kSkOff))[t] = scale_log2;
         ((float*)(lds + kSvOff))[t] = 1.0f;
@@ -416,11 +446,14 @@ __global__ __launch_bounds__(kThreadsP, 2) void prefill_attn_kernel(PrefillParam
     {
         const bool ok = head_ok && qrow < p.Sq;
         const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)qh * p.q_sh + (int64_t)(ok ? qrow : 0) * p.q_st + 8 * hh;
+        bool over = false;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const u4 w = ok ? *(const u4*)(qp + 16 * s) : u4{0u, 0u, 0u, 0u};
+            u4 w = ok ? *(const u4*)(qp + 16 * s) : u4{0u, 0u, 0u, 0u};
+            if (p.q_bf16) w = bf16x8_to_f16(w, over);
             qf[s] = __builtin_bit_cast(h8, w);
         }
+        if (__ballot(over) && lane == 0 && p.err) atomicOr(p.err, HKV_ERR_BIT_RANGE);
     }
     f16v acc[4];
 #pragma unroll
@@ -471,7 +504,7 @@ __global__ __launch_bounds__(kThreadsP, 2) void prefill_attn_kernel(PrefillParam
     const int par0 = n4p;   // LDS buffer parity continues after the INT4 tiles
     if (ntiles > n4) {
         stage_load(p, tm, b, h, n4, st);
-        stage_store(st, lds_raw + (par0 & 1) * kBufBytes, p.scale_log2);
+        stage_store(st, lds_raw + (par0 & 1) * kBufBytes, p.scale_log2, p.c_bf16 != 0, p.err);
     }
     __syncthreads();
     for (int tile = n4; tile < ntiles; ++tile) {
@@ -506,7 +539,7 @@ __global__ __launch_bounds__(kThreadsP, 2) void prefill_attn_kernel(PrefillParam
             attend_tile<true>(cur, tvalid, causal_base, n, hh, qrow, qf, acc, m, l);
         else
             attend_tile<false>(cur, tvalid, causal_base, n, hh, qrow, qf, acc, m, l);
-        if (tile + 1 < ntiles) stage_store(st, nxt, p.scale_log2);
+        if (tile + 1 < ntiles) stage_store(st, nxt, p.scale_log2, p.c_bf16 != 0, p.err);
         __syncthreads();
     }
     (void)first_chunk_tile;
@@ -520,8 +553,12 @@ __global__ __launch_bounds__(kThreadsP, 2) void prefill_attn_kernel(PrefillParam
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int d = 32 * db + 8 * j + 4 * hh;
-                *(u2*)(op + d) = u2{pack2(acc[db][4 * j + 0] * inv, acc[db][4 * j + 1] * inv),
-                                    pack2(acc[db][4 * j + 2] * inv, acc[db][4 * j + 3] * inv)};
+                if (p.out_bf16)
+                    *(u2*)(op + d) = u2{pack2bf(acc[db][4 * j + 0] * inv, acc[db][4 * j + 1] * inv),
+                                        pack2bf(acc[db][4 * j + 2] * inv, acc[db][4 * j + 3] * inv)};
+                else
+                    *(u2*)(op + d) = u2{pack2(acc[db][4 * j + 0] * inv, acc[db][4 * j + 1] * inv),
+                                        pack2(acc[db][4 * j + 2] * inv, acc[db][4 * j + 3] * inv)};
             }
     }
 }
@@ -543,6 +580,10 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
     HKV_REQUIRE(a->num_f16_zones >= 0 && a->num_f16_zones <= HKV_MAX_F16_ZONES, HKV_ERR_ARG,
                 "hkv_prefill_attn: num_f16_zones out of range");
     HKV_REQUIRE(a->q && a->out, HKV_ERR_ARG, "hkv_prefill_attn: null q/out");
+    HKV_REQUIRE((a->q_dtype == HKV_DTYPE_F16 || a->q_dtype == HKV_DTYPE_BF16) &&
+                    (a->chunk_dtype == HKV_DTYPE_F16 || a->chunk_dtype == HKV_DTYPE_BF16) &&
+                    (a->out_dtype == HKV_DTYPE_F16 || a->out_dtype == HKV_DTYPE_BF16),
+                HKV_ERR_ARG, "hkv_prefill_attn: q/chunk/out dtype must be fp16 or bf16");
     HKV_REQUIRE((((uintptr_t)a->q) & 15) == 0 && a->q_stride_b % 8 == 0 && a->q_stride_h % 8 == 0 &&
                     a->q_stride_t % 8 == 0,
                 HKV_ERR_ARG, "hkv_prefill_attn: q must be 16-byte aligned with strides multiple of 8");
@@ -584,6 +625,9 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
     p.nrep = nrep;
     p.Sq = a->num_queries;
     p.scale_log2 = a->sm_scale * kLog2eP;
+    p.q_bf16 = a->q_dtype == HKV_DTYPE_BF16;
+    p.c_bf16 = a->chunk_dtype == HKV_DTYPE_BF16;
+    p.out_bf16 = a->out_dtype == HKV_DTYPE_BF16;
     p.q = a->q;
     p.q_sb = a->q_stride_b;
     p.q_sh = a->q_stride_h;

@@ -35,23 +35,92 @@ struct ZoneWriteParams {
     int cap, ring;
     uint16_t* zk;
     uint16_t* zv;
+    int bf16;      // source is bfloat16 (converted to fp16, range-checked)
+    int* err;
 };
 
-// One workgroup of 128 lanes per (token, head, sequence); lane = dim.
-__global__ __launch_bounds__(128) void zone_write_kernel(ZoneWriteParams p) {
-    const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int d = threadIdx.x;
-    int slot = (p.slot_start ? p.slot_start[b] : p.slot_base) + t;
-    if (p.ring > 0) {
-        slot %= p.ring;
-        if (slot < 0) slot += p.ring;
-    }
-    if (slot < 0 || slot >= p.cap) return;
-    const int64_t src = (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)t * p.st + d;
+// fp16 bits of a source element; sets `over` when a finite bf16 value leaves the fp16
+// range (it becomes +-inf).  In range the conversion is exact (8 significant bits fit
+// in 11) down to 2^-14; below that fp16 subnormals round to 2^-24.
+__device__ __forceinline__ uint16_t to_f16(uint16_t x, bool bf16, bool& over) {
+    if (!bf16) return x;
+    const float f = bf2f(x);
+    const uint16_t h = f2h_rn(f);
+    over |= ((h & 0x7fffu) == 0x7c00u) && fabsf(f) < INFINITY;
+    return h;
+}
+
+__device__ __forceinline__ void report_range(bool over, int* err) {
+    if (__ballot(over) && (threadIdx.x & 63) == 0 && err) atomicOr(err, HKV_ERR_BIT_RANGE);
+}
+
+// One workgroup of 256 lanes per 16 source tokens (and head, sequence): lane t moves
+// 16 bytes (8 dims) of token t/16.  K rows are copied with 16-byte accesses.  When the
+// 16 tokens fill one whole V tile (their slots are 16 consecutive slots starting at a
+// multiple of 16), the tile is transposed through LDS and written with one 16-byte
+// store per lane; otherwise each lane writes its 8 V values into their tile slots.
+__global__ __launch_bounds__(256) void zone_write_kernel(ZoneWriteParams p) {
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) uint16_t sv[kBlockTokens][kHeadDim + 8];   // +8 halves: rows start on different banks
+    const int j = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int t = threadIdx.x, r = t >> 4, q = t & 15;
+    const int base = p.slot_start ? p.slot_start[b] : p.slot_base;
+    auto slot_of = [&](int ts) {
+        int s = base + ts;
+        if (p.ring > 0) {
+            s %= p.ring;
+            if (s < 0) s += p.ring;
+        }
+        return s;
+    };
+    const int ts = j * kBlockTokens + r;
+    const int s0 = slot_of(j * kBlockTokens);
+    const bool whole_tile = j * kBlockTokens + kBlockTokens <= p.T && (s0 & (kBlockTokens - 1)) == 0 &&
+                            s0 >= 0 && s0 + kBlockTokens <= p.cap && (p.ring == 0 || s0 + kBlockTokens <= p.ring);
     const int64_t bh = (int64_t)b * p.H + h;
-    p.zk[(bh * p.cap + slot) * kHeadDim + d] = p.k[src];
-    const int64_t tile = bh * (p.cap / kBlockTokens) + slot / kBlockTokens;
-    p.zv[tile * (kBlockTokens * kHeadDim) + vtile_off(slot & 15, d)] = p.v[src];
+    bool over = false;
+    uint16_t vv[8];
+    int slot = -1;
+    if (ts < p.T) {
+        const int64_t src = (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)ts * p.st + 8 * q;
+        const u4v kw = *(const u4v*)(p.k + src);
+        const u4v vw = *(const u4v*)(p.v + src);
+        const bool bf = p.bf16 != 0;
+        u4v ko;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = to_f16((uint16_t)(kw[e] & 0xffffu), bf, over);
+            const uint32_t hi = to_f16((uint16_t)(kw[e] >> 16), bf, over);
+            ko[e] = lo | (hi << 16);
+            vv[2 * e] = to_f16((uint16_t)(vw[e] & 0xffffu), bf, over);
+            vv[2 * e + 1] = to_f16((uint16_t)(vw[e] >> 16), bf, over);
+        }
+        slot = slot_of(ts);
+        if (slot >= 0 && slot < p.cap) *(u4v*)(p.zk + (bh * p.cap + slot) * kHeadDim + 8 * q) = ko;
+    }
+    report_range(over, p.err);
+    if (whole_tile) {
+        u4v pw;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pw[e] = (uint32_t)vv[2 * e] | ((uint32_t)vv[2 * e + 1] << 16);
+        *(u4v*)&sv[r][8 * q] = pw;
+        __syncthreads();
+        // 16-byte piece t of the tile: halves [g][c][n][i] with g = t/64, c = (t/4)%16,
+        // n = 2(t%4) + {0,1}, i = 0..3, i.e. V[4g+i][c+16n]
+        const int g = t >> 6, c = (t >> 2) & 15, n0 = 2 * (t & 3);
+        uint16_t o[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) o[u] = sv[4 * g + (u & 3)][c + 16 * (n0 + (u >> 2))];
+        u4v w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = (uint32_t)o[2 * e] | ((uint32_t)o[2 * e + 1] << 16);
+        const int64_t tile = bh * (p.cap / kBlockTokens) + s0 / kBlockTokens;
+        *(u4v*)(p.zv + tile * (kBlockTokens * kHeadDim) + 8 * t) = w;
+    } else if (ts < p.T && slot >= 0 && slot < p.cap) {
+        const int64_t tile = bh * (p.cap / kBlockTokens) + slot / kBlockTokens;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p.zv[tile * (kBlockTokens * kHeadDim) + vtile_off(slot & 15, 8 * q + e)] = vv[e];
+    }
 }
 
 __global__ __launch_bounds__(128) void zone_copy_kernel(const uint16_t* __restrict__ sk,
@@ -100,6 +169,8 @@ struct ZoneStepParams {
     int* tail_lens;
     int* hh_lens;
     int B;
+    int bf16;
+    int* err;
 };
 
 __device__ __forceinline__ int64_t vtile_index(int64_t bh, int cap, int slot, int d) {
@@ -126,8 +197,10 @@ __global__ __launch_bounds__(128) void zone_step_kernel(ZoneStepParams p) {
         p.hv[vtile_index(bh, p.hcap, hh, d)] = p.tv[vtile_index(bh, p.tcap, head, d)];
     }
     const int64_t src = (int64_t)b * p.sb + (int64_t)h * p.sh + d;
-    p.tk[(bh * p.tcap + slot) * kHeadDim + d] = p.k[src];
-    p.tv[vtile_index(bh, p.tcap, slot, d)] = p.v[src];
+    bool over = false;
+    p.tk[(bh * p.tcap + slot) * kHeadDim + d] = to_f16(p.k[src], p.bf16 != 0, over);
+    p.tv[vtile_index(bh, p.tcap, slot, d)] = to_f16(p.v[src], p.bf16 != 0, over);
+    report_range(over, p.err);
 }
 
 // Advances the state after the step and publishes the zone lengths per sequence.
@@ -168,6 +241,8 @@ extern "C" int hkv_zone_step(const HkvZoneStepArgs* a, void* stream) {
     HKV_REQUIRE(a->batch > 0 && a->batch <= 65535 && a->num_kv_heads > 0 && a->num_kv_heads <= 65535, HKV_ERR_ARG,
                 "hkv_zone_step: bad sizes");
     HKV_REQUIRE(a->k && a->v && a->tail_k && a->tail_v && a->state, HKV_ERR_ARG, "hkv_zone_step: null pointer");
+    HKV_REQUIRE(a->dtype == HKV_DTYPE_F16 || a->dtype == HKV_DTYPE_BF16, HKV_ERR_ARG,
+                "hkv_zone_step: dtype %d is neither fp16 nor bf16", a->dtype);
     HKV_REQUIRE(a->tail_capacity > 0 && a->tail_capacity % kBlockTokens == 0 && a->tail_ring > 0 &&
                     a->tail_ring <= a->tail_capacity,
                 HKV_ERR_ARG, "hkv_zone_step: tail ring %d / capacity %d", a->tail_ring, a->tail_capacity);
@@ -192,6 +267,8 @@ extern "C" int hkv_zone_step(const HkvZoneStepArgs* a, void* stream) {
     p.tail_lens = a->tail_lens;
     p.hh_lens = a->hh_lens;
     p.B = a->batch;
+    p.bf16 = a->dtype == HKV_DTYPE_BF16;
+    p.err = a->err_flag;
     hipLaunchKernelGGL(zone_step_kernel, dim3(a->num_kv_heads, a->batch), dim3(128), 0, (hipStream_t)stream, p);
     HKV_LAUNCH_CHECK("zone_step_kernel");
     hipLaunchKernelGGL(zone_advance_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, p);
@@ -222,6 +299,11 @@ extern "C" int hkv_zone_write(const HkvZoneWriteArgs* a, void* stream) {
     HKV_REQUIRE(a->num_kv_heads <= 65535 && a->batch <= 65535, HKV_ERR_ARG, "hkv_zone_write: grid too large");
     HKV_REQUIRE(a->ring >= 0 && a->ring <= a->capacity, HKV_ERR_ARG,
                 "hkv_zone_write: ring %d must be in [0, capacity %d]", a->ring, a->capacity);
+    HKV_REQUIRE(a->dtype == HKV_DTYPE_F16 || a->dtype == HKV_DTYPE_BF16, HKV_ERR_ARG,
+                "hkv_zone_write: dtype %d is neither fp16 nor bf16", a->dtype);
+    HKV_REQUIRE((((uintptr_t)a->k | (uintptr_t)a->v) & 15) == 0 && a->src_stride_b % 8 == 0 &&
+                    a->src_stride_h % 8 == 0 && a->src_stride_t % 8 == 0,
+                HKV_ERR_ARG, "hkv_zone_write: k/v must be 16-byte aligned with strides multiple of 8");
     ZoneWriteParams p;
     p.k = a->k;
     p.v = a->v;
@@ -236,8 +318,11 @@ extern "C" int hkv_zone_write(const HkvZoneWriteArgs* a, void* stream) {
     p.ring = a->ring;
     p.zk = a->zone_k;
     p.zv = a->zone_v;
-    hipLaunchKernelGGL(zone_write_kernel, dim3(a->num_tokens, a->num_kv_heads, a->batch), dim3(128), 0,
-                       (hipStream_t)stream, p);
+    p.bf16 = a->dtype == HKV_DTYPE_BF16;
+    p.err = a->err_flag;
+    hipLaunchKernelGGL(zone_write_kernel, dim3((a->num_tokens + kBlockTokens - 1) / kBlockTokens, a->num_kv_heads,
+                                               a->batch),
+                       dim3(256), 0, (hipStream_t)stream, p);
     HKV_LAUNCH_CHECK("zone_write_kernel");
     return HKV_OK;
 }

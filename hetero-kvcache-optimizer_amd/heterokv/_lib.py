@@ -13,15 +13,37 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libheterokv.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_U8 = 0, 1, 2, 3
 MAX_F16_ZONES = 3
 DECODE_DETERMINISTIC = 1   # HKV_DECODE_DETERMINISTIC
+DECODE_AGENT_HANDOFF = 2   # HKV_DECODE_AGENT_HANDOFF
 BLOCK_TOKENS = 16
 HEAD_DIM = 128
 
 HKV_OK = 0
-ERR_NAMES = {-1: "HKV_ERR_ARG", -2: "HKV_ERR_HIP", -3: "HKV_ERR_CAPACITY", -4: "HKV_ERR_UNSUPPORTED"}
+ERR_NAMES = {-1: "HKV_ERR_ARG", -2: "HKV_ERR_HIP", -3: "HKV_ERR_CAPACITY", -4: "HKV_ERR_UNSUPPORTED",
+             -5: "HKV_ERR_DEVICE"}
+ERR_DEVICE = -5   # HKV_ERR_DEVICE: a device error word came back non-zero
+
+# device error-word bits (HKV_ERR_BIT_*)
+ERR_BIT_BLOCK_ID, ERR_BIT_SLOT, ERR_BIT_PLACEMENT, ERR_BIT_RANGE = 1, 2, 4, 8
+_ERR_BIT_TEXT = {
+    ERR_BIT_BLOCK_ID: "a block table held an id outside the pool / staging records",
+    ERR_BIT_SLOT: "a token slot lay beyond its block table row",
+    ERR_BIT_PLACEMENT: "decode ranges of one (sequence, kv head) ran on more than one XCD; that launch's "
+                       "output is invalid (later launches use the device-scope hand-off)",
+    ERR_BIT_RANGE: "a finite bf16 value beyond the fp16 range (|x| > 65504) was narrowed to fp16",
+}
+
+
+def describe_error_bits(bits):
+    """Human-readable text of a device error word."""
+    parts = [t for b, t in sorted(_ERR_BIT_TEXT.items()) if bits & b]
+    unknown = bits & ~sum(_ERR_BIT_TEXT)
+    if unknown:
+        parts.append("unknown error bits 0x%x" % unknown)
+    return "; ".join(parts)
 
 
 class HeteroKVError(RuntimeError):
@@ -60,7 +82,7 @@ class ZoneWriteArgs(ctypes.Structure):
                 ("src_stride_b", i64), ("src_stride_h", i64), ("src_stride_t", i64),
                 ("batch", i32), ("num_kv_heads", i32), ("head_dim", i32), ("num_tokens", i32),
                 ("slot_start", vp), ("capacity", i32), ("ring", i32),
-                ("zone_k", vp), ("zone_v", vp), ("slot_base", i32)]
+                ("zone_k", vp), ("zone_v", vp), ("slot_base", i32), ("dtype", i32), ("err_flag", vp)]
 
 
 class ZoneStepArgs(ctypes.Structure):
@@ -68,7 +90,7 @@ class ZoneStepArgs(ctypes.Structure):
                 ("batch", i32), ("num_kv_heads", i32), ("head_dim", i32),
                 ("tail_k", vp), ("tail_v", vp), ("tail_capacity", i32), ("tail_ring", i32),
                 ("hh_k", vp), ("hh_v", vp), ("hh_capacity", i32), ("hh_budget", i32),
-                ("state", vp), ("tail_lens", vp), ("hh_lens", vp)]
+                ("state", vp), ("tail_lens", vp), ("hh_lens", vp), ("dtype", i32), ("err_flag", vp)]
 
 
 class F16Zone(ctypes.Structure):
@@ -85,7 +107,8 @@ class DecodeArgs(ctypes.Structure):
                 ("out", vp), ("out_stride_b", i64), ("out_stride_h", i64),
                 ("workspace", vp), ("workspace_bytes", ctypes.c_size_t), ("splits_hint", i32),
                 ("staging", vp), ("staging_blocks", i64), ("flags", i32),
-                ("scores", vp), ("scores_stride_b", i64), ("scores_stride_h", i64), ("score_stats", vp)]
+                ("scores", vp), ("scores_stride_b", i64), ("scores_stride_h", i64), ("score_stats", vp),
+                ("q_dtype", i32), ("out_dtype", i32), ("err_flag", vp)]
 
 
 class PrefillArgs(ctypes.Structure):
@@ -98,7 +121,8 @@ class PrefillArgs(ctypes.Structure):
                 ("chunk_k", vp), ("chunk_v", vp),
                 ("chunk_stride_b", i64), ("chunk_stride_h", i64), ("chunk_stride_t", i64),
                 ("out", vp), ("out_stride_b", i64), ("out_stride_h", i64), ("out_stride_t", i64),
-                ("err_flag", vp), ("staging", vp), ("staging_blocks", i64)]
+                ("err_flag", vp), ("staging", vp), ("staging_blocks", i64),
+                ("q_dtype", i32), ("chunk_dtype", i32), ("out_dtype", i32)]
 
 
 class CopyDesc(ctypes.Structure):

@@ -8,9 +8,11 @@ Attention routes.
   * Prefill (new_len > 1): the reference hands transformers the full chunk (first
     chunk) or sink + old tail + chunk (later chunks) and lets SDPA attend
     (manager.py:533-535,562-563); the same tensors are returned here.  With
-    fused_prefill=True they are tagged, and the registered attention function runs
-    the MFMA prefill kernel instead of SDPA: the cached prefix as an fp16 zone, the
-    chunk causally (the mask SDPA would get for an unpadded batch).
+    fused_prefill=True update() returns the chunk itself, tagged, and the registered
+    attention function runs the MFMA prefill kernel over the manager's own sink and
+    tail zones (as they were before the chunk) plus the chunk causally -- the
+    attention SDPA computes on the reference's tensors for an unpadded batch, with
+    nothing concatenated or copied; the chunk enters the tail ring afterwards.
   * Decode, default (Path C, engine_wrapper.py:236-245): the reference prepends every
     DRAM token, dequantized to fp16, to sink + tail + heavy hitters.  With
     fused_decode=True (default) update() returns the new token's K/V tagged with a
@@ -19,9 +21,20 @@ Attention routes.
     nothing is dequantized or concatenated.  With fused_decode=False the reference's
     concatenated tensors are materialized and returned.
 The Path C gate is the reference's: DRAM tokens join a layer's attention only
-while _swap_in_tokens > 0, which layer 0 refreshes after its own decode update.
+while _swap_in_tokens > 0, which layer 0 refreshes after its own update.
 adaptive_self_healing=True selects the reference's Path A (engine_wrapper.py:204-222):
-only the top-w_t chunks by score join, w_t from AdaptivePrefetchController.
+only the top-w_t chunks by score join, w_t from AdaptivePrefetchController, attended
+in place by the fused kernel; with enable_triton=False (or fused_decode=False) it is
+Path B (:223-234): the chosen chunks are dequantized to bf16 and concatenated.
+
+Sequence lengths.  By default get_seq_length is the number of tokens the layer has
+seen (what transformers derives cache_position and RoPE positions from, as its
+sliding-window layers do), get_mask_sizes the exact key length update() returns,
+and the DRAM-tier gate counts the exact INT4 tokens and is refreshed after prefill
+too.  reference_lengths=True keeps the reference's arithmetic instead
+(engine_wrapper.py:256-301, manager.py:1218-1229): the HBM length plus #chunks x
+first chunk size, refreshed only by layer 0's decode updates -- 3,904 tokens short
+at 128K with keep_tail=4160, and no DRAM tokens for layer 0's first decode step.
 """
 import gc
 import math
@@ -44,11 +57,8 @@ class FusedHeteroCache(DynamicCache):
                  enable_quant: bool = True, enable_prefetch: bool = True, enable_triton: bool = True,
                  bandwidth_limiter=None, self_healing: bool = True, adaptive_self_healing: bool = False,
                  enable_method_d: bool = False, method_d_alpha: float = 1.0, fused_decode: bool = True,
-                 fused_prefill: bool = False, track_attention: bool = False):
+                 fused_prefill: bool = False, track_attention: bool = False, reference_lengths: bool = False):
         super().__init__()
-        if adaptive_self_healing and not fused_decode:
-            raise HeteroKVError(-4, "windowed retrieval (adaptive_self_healing) runs on the fused decode path; "
-                                    "use fused_decode=True")
         self.sink_tokens = sink_tokens
         self.keep_tail = keep_tail
         self.chunk_size = chunk_size
@@ -62,16 +72,18 @@ class FusedHeteroCache(DynamicCache):
         self.adaptive_self_healing = adaptive_self_healing
         self.enable_method_d = enable_method_d
         self.method_d_alpha = method_d_alpha
-        self.fused_decode = fused_decode
+        # Path B (adaptive retrieval without the fused kernel) concatenates bf16 K/V
+        self.fused_decode = fused_decode and not (adaptive_self_healing and not enable_triton)
         self.fused_prefill = fused_prefill
+        self.reference_lengths = reference_lengths
         # feed the heavy-hitter oracle with the last layer's decode attention weights
         # (engine_wrapper.py:165-180 intends this; the reference's patch never sets them)
         self.track_attention = track_attention
-        self._prefill_zone = None
         self._num_layers = num_layers
         self._manager: Optional[HeteroKVManager] = None
         self.real_seq_len: int = 0
         self._swap_in_tokens: int = 0
+        self._layer_seen: Dict[int, int] = {}    # tokens each layer has been given
 
     def _ensure_manager(self, layer_idx: int) -> HeteroKVManager:
         if self._manager is not None:
@@ -82,7 +94,7 @@ class FusedHeteroCache(DynamicCache):
                                         enable_quant=self.enable_quant, enable_prefetch=self.enable_prefetch,
                                         group_size=self.group_size, bandwidth_limiter=self._bandwidth_limiter,
                                         enable_method_d=self.enable_method_d, method_d_alpha=self.method_d_alpha)
-        if self.adaptive_self_healing:
+        if self.adaptive_self_healing and self.fused_decode:
             self._manager.retrieval_window = "adaptive"
         return self._manager
 
@@ -101,31 +113,45 @@ class FusedHeteroCache(DynamicCache):
             route = (self, layer_idx, include_dram)
             out_k._hkv_route = route
             out_v._hkv_route = route
+        elif mode == "prefill" and self.fused_prefill:
+            # the chunk is attended by attend_prefill over the manager's own zones: nothing
+            # is concatenated
+            manager.update(layer_idx, key_states, value_states, mode="prefill", seq_offset=self.real_seq_len,
+                           materialize=False)
+            out_k, out_v = key_states, value_states
+            tag = (self, layer_idx)
+            out_k._hkv_prefill = tag
+            out_v._hkv_prefill = tag
         else:
             out_k, out_v = manager.update(layer_idx, key_states, value_states, mode=mode,
                                           seq_offset=self.real_seq_len)
-            if mode == "prefill" and self.fused_prefill:
-                tag = (self, out_k.shape[-2] - new_len)
-                out_k._hkv_prefill = tag
-                out_v._hkv_prefill = tag
             if include_dram:
-                dram_k, dram_v, count = manager.decompress_dram_chunks(layer_idx)
+                if self.adaptive_self_healing:
+                    # Path B (engine_wrapper.py:223-234): top-w_t chunks as bf16
+                    dram_k, dram_v, count = manager.decompress_selected(layer_idx)
+                else:
+                    dram_k, dram_v, count = manager.decompress_dram_chunks(layer_idx)
                 if dram_k is not None and count > 0:
                     out_k = torch.cat([dram_k.to(out_k.dtype), out_k], dim=-2)
                     out_v = torch.cat([dram_v.to(out_v.dtype), out_v], dim=-2)
+        self._layer_seen[layer_idx] = self._layer_seen.get(layer_idx, 0) + new_len
         if layer_idx == 0:
             self.real_seq_len += new_len
-            if mode == "decode" and self.self_healing:
+            if self.self_healing and (mode == "decode" or not self.reference_lengths):
                 self._refresh_swap_count()
         return out_k, out_v
 
     def get_seq_length(self, layer_idx: int = 0, *args, **kwargs) -> int:
-        """engine_wrapper.py:256-264: HBM cache length + DRAM swap-in count."""
+        """Tokens the layer has seen (its next token's position).  With
+        reference_lengths=True: engine_wrapper.py:256-264, the HBM length plus the DRAM
+        swap-in count."""
         if self._manager is None:
             return 0
         n = self._manager.hbm_length(layer_idx)
         if n is None:
             return 0
+        if not self.reference_lengths:
+            return self._layer_seen.get(layer_idx, 0)
         return n + self._swap_in_tokens
 
     @property
@@ -133,24 +159,64 @@ class FusedHeteroCache(DynamicCache):
         return self.real_seq_len
 
     def get_mask_sizes(self, query, layer_idx: int = 0, *args, **kwargs) -> Tuple[int, int]:
-        """engine_wrapper.py:274-301.  `query` is the query length (transformers >= 5) or the
-        cache_position tensor (4.57, as the reference was written for)."""
+        """(key length update() will return, key offset) for a query of this length,
+        computed before the update as transformers does (engine_wrapper.py:274-301 with
+        exact counts; reference_lengths=True keeps its arithmetic).  The offset pairs with
+        get_query_offset so that a prefill query sees the cached prefix and the chunk
+        causally and a decode query sees every key.  `query` is the query length
+        (transformers >= 5) or the cache_position tensor (4.57, as the reference was
+        written for)."""
         query_len = int(query.shape[0]) if isinstance(query, torch.Tensor) else int(query)
-        if self._manager is None:
+        mgr = self._manager
+        if mgr is None:
             return query_len, 0
-        phys = self._manager.hbm_length(layer_idx)
+        phys = mgr.hbm_length(layer_idx)
         if phys is None:
             return query_len, 0
+        if self.reference_lengths:
+            if query_len > 1:
+                return phys + query_len, 0
+            tail = mgr.tail_length(layer_idx)
+            if tail is not None and tail >= mgr.tail_budget:
+                return phys + self._swap_in_tokens, 0
+            return phys + self._swap_in_tokens + 1, 0
+        shift = self._dram_shift(layer_idx)
         if query_len > 1:
-            return phys + query_len, 0
-        tail = self._manager.tail_length(layer_idx)
-        if tail is not None and tail >= self._manager.tail_budget:
-            return phys + self._swap_in_tokens, 0
-        return phys + self._swap_in_tokens + 1, 0
+            # keys = [sink | old tail | chunk]; query i sits at key phys + i, which with
+            # get_query_offset = phys + shift needs kv_offset = shift
+            return phys + query_len, shift
+        tail = mgr.tail_length(layer_idx)
+        grows = tail is None or tail < mgr.tail_budget or mgr.heavy_hitter_length(layer_idx) < mgr.heavy_hitter_budget
+        dram = 0
+        if shift:
+            dram = mgr.selected_tokens(layer_idx) if (self.adaptive_self_healing and not self.fused_decode) else shift
+        return phys + (1 if grows else 0) + dram, 0
+
+    def _dram_shift(self, layer_idx: int) -> int:
+        """INT4 tokens of the layer while the DRAM tier is attended at decode (else 0)."""
+        if not (self.self_healing and self._swap_in_tokens > 0) or self._manager is None:
+            return 0
+        return self._manager.dram_tokens(layer_idx)
+
+    def get_query_offset(self, layer_idx: int = 0) -> int:
+        """Offset of the first query among the keys update() returns, as transformers' mask
+        builder reads it (it defaults to get_seq_length, which here counts seen tokens):
+        the cached prefix plus the DRAM tokens a decode step would prepend -- every key is
+        then visible to a decode query, and a prefill chunk's mask keeps its causal
+        alignment through the matching kv_offset of get_mask_sizes."""
+        if self.reference_lengths:
+            return self.get_seq_length(layer_idx)
+        if self._manager is None:
+            return 0
+        phys = self._manager.hbm_length(layer_idx)
+        if phys is None:
+            return 0
+        return phys + self._dram_shift(layer_idx)
 
     def _refresh_swap_count(self) -> None:
         if self._manager is not None:
-            self._swap_in_tokens = self._manager.count_dram_tokens(layer_idx=0)
+            self._swap_in_tokens = (self._manager.count_dram_tokens(layer_idx=0) if self.reference_lengths
+                                    else self._manager.dram_tokens(0))
 
     @property
     def is_compileable(self) -> bool:
@@ -197,32 +263,26 @@ class FusedHeteroCache(DynamicCache):
         return self._manager.prefetch_stats(reset)
 
     def schedule_prefetch(self, chunk_key: str) -> None:
-        """The INT4 tier of this build is resident in HBM (or streamed by the block prefetcher),
-        so there is nothing to stage per chunk."""
-        return None
+        """engine_wrapper.py:332-336: dequantize a chunk on the prefetcher's side stream."""
+        if self._manager is not None:
+            self._manager.schedule_prefetch(chunk_key)
+
+    def swap_in_chunk(self, chunk_key: str) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+        """engine_wrapper.py:338-344: remove a chunk from the INT4 tier, returning bf16 K/V."""
+        if self._manager is None:
+            return None
+        return self._manager.swap_in(0, chunk_key)
 
     def swap_in_quantized(self, chunk_key: str) -> Optional[Dict[str, torch.Tensor]]:
-        if self._manager is None or chunk_key not in self._manager._chunks:
+        """engine_wrapper.py:346-355: a chunk's INT4 data without dequantizing it."""
+        if self._manager is None:
             return None
-        return self._manager.chunk_codes(chunk_key)
+        return self._manager.swap_in_quantized(0, chunk_key)
 
-    def _fused_prefill_attention(self, query, key, value, prefix, scaling):
-        """Prefill attention on the MFMA kernel: every query sees the `prefix` cached rows of
-        key/value (written into a reusable fp16 zone) and the chunk rows causally."""
-        from . import ops
-        B, H, S, _ = key.shape
-        zones = []
-        if prefix:
-            z = self._prefill_zone
-            if z is None or z.capacity < prefix or z.batch != B or z.num_kv_heads != H:
-                z = self._prefill_zone = ops.F16Zone(B, H, prefix, key.device)
-            z.write(key[:, :, :prefix].to(torch.float16), value[:, :, :prefix].to(torch.float16), [0] * B)
-            zones.append((z, None, prefix))
-        ck = key[:, :, prefix:].to(torch.float16).contiguous()
-        cv = value[:, :, prefix:].to(torch.float16).contiguous()
-        out = ops.prefill_attention(query.to(torch.float16), zones=zones, chunk_k=ck, chunk_v=cv,
-                                    sm_scale=scaling)
-        return out.to(query.dtype)
+    def check_errors(self) -> None:
+        """Raise HeteroKVError if a kernel reported a device error (synchronizes)."""
+        if self._manager is not None:
+            self._manager.check_errors()
 
     def fused_attn_on_swapped(self, q: torch.Tensor, chunk_key: str,
                               sm_scale: Optional[float] = None) -> Optional[torch.Tensor]:
@@ -252,9 +312,9 @@ def heterokv_attention_forward(module, query, key, value, attention_mask, scalin
                                            feed_oracle=feed)
         return out.transpose(1, 2).contiguous(), None
     pre = getattr(key, "_hkv_prefill", None)
-    if pre is not None and query.shape[2] == key.shape[2] - pre[1]:
-        cache, prefix = pre
-        out = cache._fused_prefill_attention(query, key, value, prefix, scaling)
+    if pre is not None and query.shape[2] == key.shape[2]:
+        cache, layer_idx = pre
+        out = cache._manager.attend_prefill(layer_idx, query, key, value, sm_scale=scaling)
         return out.transpose(1, 2).contiguous(), None
     from transformers.integrations.sdpa_attention import sdpa_attention_forward
     return sdpa_attention_forward(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout,
@@ -364,6 +424,7 @@ class DecodeGraph:
         cache = self.cache
         for li in range(mgr.num_layers):
             mgr.advance_decode_host(li, cache.real_seq_len)
+            cache._layer_seen[li] = cache._layer_seen.get(li, 0) + 1
             if li == 0:
                 cache.real_seq_len += 1
                 if cache.self_healing:

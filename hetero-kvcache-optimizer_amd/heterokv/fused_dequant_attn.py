@@ -12,15 +12,40 @@ exactly that formula, and it also accepts GQA (q heads a multiple of kv heads).
 The reference passes unpacked codes (one uint8 per value) with per-token
 scales/zps [B, H, S]; they are repacked into INT4 block records on the device
 (hkv_repack_codes) and attended by the split-K decode kernel (hkv_decode_attn) or the
-MFMA prefill kernel (hkv_prefill_attn).
+MFMA prefill kernel (hkv_prefill_attn).  q may be fp16 or bf16 (bf16 is narrowed to
+fp16 operands exactly within the fp16 range).  Device errors (an out-of-range bf16
+value, a decode placement failure) go to a per-device error word that is read without
+blocking at the next call -- a later call raises HeteroKVError -- or at once by
+check_errors().
 """
 import math
 from typing import Optional
 
 import torch
 
-from . import ops
+from . import _lib, ops
 from ._lib import BLOCK_TOKENS, HeteroKVError
+
+
+_ERR = {}   # device -> ErrorWord shared by the calls on that device
+_WS = {}    # device -> DecodeWorkspace shared by the decode calls on that device
+
+
+def _errword(device):
+    w = _ERR.get(device)
+    if w is None:
+        w = _ERR[device] = ops.ErrorWord(device)
+        _WS[device] = ops.DecodeWorkspace(device)
+        w.on_error = lambda bits: _WS[device].placement_failed() if bits & _lib.ERR_BIT_PLACEMENT else None
+    return w
+
+
+def check_errors(device=None) -> None:
+    """Raise HeteroKVError if a call on `device` (default: every device used) reported a
+    device error (synchronizes)."""
+    for d, w in list(_ERR.items()):
+        if device is None or torch.device(device) == d:
+            w.check()
 
 
 def _as_4d(t):
@@ -49,17 +74,20 @@ def fused_dequant_attn_decode(q: torch.Tensor, k_data: torch.Tensor, k_scales: t
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
     nblk = (S + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+    err = _errword(q.device)
+    err.poll()
     pool = ops.Int4Pool(B * nblk, Hkv, q.device)
     bt = torch.arange(B * nblk, dtype=torch.int32, device=q.device).reshape(B, nblk)
     start = torch.zeros(B, dtype=torch.int32, device=q.device)
-    ops.repack_codes(pool, kd, vd, ks, vs, kz, vz, start, bt)
-    q16 = q if q.dtype == torch.float16 else q.to(torch.float16)
-    out = ops.decode_attention(q16, zones=(), pool=pool, block_table=bt, int4_lens=None, int4_max_len=S,
-                               sm_scale=sm_scale)
+    ops.repack_codes(pool, kd, vd, ks, vs, kz, vz, start, bt, err=err)
+    qq = q if q.dtype in (torch.float16, torch.bfloat16) else q.to(torch.float16)
+    out = ops.decode_attention(qq, zones=(), pool=pool, block_table=bt, int4_lens=None, int4_max_len=S,
+                               sm_scale=sm_scale, workspace=_WS[q.device], err=err, out_dtype=qq.dtype)
+    err.post()
     return out.to(q.dtype)
 
 
-def _repack_reference(q, k_data, k_scales, k_zps, v_data, v_scales, v_zps):
+def _repack_reference(q, k_data, k_scales, k_zps, v_data, v_scales, v_zps, err):
     B = q.shape[0]
     kd, vd = _as_4d(k_data), _as_4d(v_data)
     Hkv, S = kd.shape[1], kd.shape[2]
@@ -68,7 +96,7 @@ def _repack_reference(q, k_data, k_scales, k_zps, v_data, v_scales, v_zps):
     bt = torch.arange(B * nblk, dtype=torch.int32, device=q.device).reshape(B, nblk)
     start = torch.zeros(B, dtype=torch.int32, device=q.device)
     ops.repack_codes(pool, kd, vd, k_scales.reshape(B, Hkv, S), v_scales.reshape(B, Hkv, S),
-                     k_zps.reshape(B, Hkv, S), v_zps.reshape(B, Hkv, S), start, bt)
+                     k_zps.reshape(B, Hkv, S), v_zps.reshape(B, Hkv, S), start, bt, err=err)
     return pool, bt, S
 
 
@@ -81,8 +109,11 @@ def fused_dequant_attn_forward(q: torch.Tensor, k_data: torch.Tensor, k_scales: 
         raise HeteroKVError(-1, "Forward expects [B,H,S,D], got %s" % (tuple(q.shape),))
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(q.shape[-1])
-    pool, bt, S = _repack_reference(q, k_data, k_scales, k_zps, v_data, v_scales, v_zps)
-    q16 = q if q.dtype == torch.float16 else q.to(torch.float16)
-    out = ops.prefill_attention(q16, pool=pool, block_table=bt, int4_max_len=S, sm_scale=sm_scale)
-    pool.check_errors()
+    err = _errword(q.device)
+    err.poll()
+    pool, bt, S = _repack_reference(q, k_data, k_scales, k_zps, v_data, v_scales, v_zps, err)
+    qq = q if q.dtype in (torch.float16, torch.bfloat16) else q.to(torch.float16)
+    out = ops.prefill_attention(qq, pool=pool, block_table=bt, int4_max_len=S, sm_scale=sm_scale, err=err,
+                                out_dtype=qq.dtype)
+    err.post()
     return out.to(q.dtype)

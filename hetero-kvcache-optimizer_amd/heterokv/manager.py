@@ -21,7 +21,10 @@ attended token: tokens that the reference leaves in its competition queue after
 the heavy-hitter zone is full are not retained (they are never attended again);
 the queue is kept per layer (equal to the reference's shared queue when layers
 update in lockstep, the only way transformers drives a cache); zones store
-fp16 (bf16 inputs are stored as fp16 and returned in the caller's dtype).
+fp16: bf16 inputs are narrowed by the zone kernels, exactly for magnitudes in
+[2^-14, 65504], and a finite value beyond the fp16 range is reported as a
+HeteroKVError (the manager's device error word, read without a per-launch sync
+at the next step, or at once by check_errors()).
 """
 from collections import OrderedDict, deque
 from typing import Any, Dict, List, Optional, Tuple
@@ -30,19 +33,17 @@ import numpy as np
 import torch
 
 from . import ops
+from . import _lib
 from ._lib import BLOCK_TOKENS, HEAD_DIM, HeteroKVError
 from .heavy_hitter import HeavyHitterOracle
 from .kv_compressor import KVCompressor
-from .prefetcher import AdaptivePrefetchController, Prefetcher
-
-
-def _as16(t):
-    return t if t.dtype == torch.float16 else t.to(torch.float16)
+from .prefetcher import AdaptivePrefetchController, AsyncPrefetcher, Prefetcher
 
 
 class _LayerState:
-    def __init__(self, B, H, device, dtype, sink_tokens, tail_budget, hh_budget):
+    def __init__(self, B, H, device, dtype, sink_tokens, tail_budget, hh_budget, err):
         self.B, self.H, self.device, self.dtype = B, H, device, dtype
+        self.err = err                             # the manager's ErrorWord
         self.sink = ops.F16Zone(B, H, max(sink_tokens, 1), device)
         self.sink_len = 0
         self.sink_pos: List[int] = []
@@ -77,6 +78,9 @@ class _LayerState:
         self.host_lbs: Optional[np.ndarray] = None
         self.version = 0                           # bumped whenever bt or pool change
         self.resident_cache = None
+        # deferred write of a prefill chunk into the tail ring: (k, v, first chunk token
+        # written, its ring slot, tail length before the chunk); see _incremental_prefill
+        self.pending = None
 
     # -------------------------------------------------------------- INT4 pool
     def ensure_int4(self, n_tokens):
@@ -107,22 +111,39 @@ class _LayerState:
         self.version += 1
 
     # -------------------------------------------------------------- tail ring
-    def tail_tensors(self):
-        """Tail K/V in logical (oldest first) order, fp16 [B, H, tail_len, 128]."""
-        if self.tail_len == 0:
+    def flush(self):
+        """Apply a deferred prefill-chunk write to the tail ring."""
+        if self.pending is None:
+            return
+        k, v, i0, slot, _ = self.pending
+        self.pending = None
+        if k.shape[2] > i0:
+            self.tail.write(k[:, :, i0:], v[:, :, i0:], slot, ring=self.ring, err=self.err)
+
+    def tail_tensors(self, i0=0, i1=None):
+        """Tail tokens [i0, i1) in logical (oldest first) order, fp16 [B, H, i1 - i0, 128]."""
+        self.flush()
+        i1 = self.tail_len if i1 is None else i1
+        n = i1 - i0
+        if n <= 0:
             e = torch.empty((self.B, self.H, 0, HEAD_DIM), dtype=torch.float16, device=self.device)
             return e, e.clone()
-        k, v = self.tail.read(self.ring if self.tail_head + self.tail_len > self.ring else self.tail_head + self.tail_len)
-        if self.tail_head == 0:
-            return k[:, :, :self.tail_len], v[:, :, :self.tail_len]
-        idx = (torch.arange(self.tail_len, device=self.device) + self.tail_head) % self.ring
+        s0 = self.tail_head + i0
+        if s0 % self.ring + n <= self.ring and s0 < self.ring:
+            if s0 == 0:
+                return self.tail.read(n)
+            k, v = self.tail.read(s0 + n)
+            return k[:, :, s0:], v[:, :, s0:]
+        k, v = self.tail.read(self.ring)
+        idx = (torch.arange(n, device=self.device) + s0) % self.ring
         return k.index_select(2, idx), v.index_select(2, idx)
 
     def write_tail(self, k, v):
         """Replace the tail with k, v (logical order), starting at ring slot 0."""
+        self.pending = None
         n = k.shape[2]
         if n:
-            self.tail.write(_as16(k), _as16(v), [0] * self.B)
+            self.tail.write(k, v, 0, err=self.err)
         self.tail_head, self.tail_len = 0, n
         self.dev_state = None
 
@@ -158,6 +179,9 @@ class HeteroKVManager:
         self._eviction_counter = 0
         self._queued_tokens = 0      # tokens the reference would leave in its competition queue
         self._workspace = None
+        self._err: Optional[ops.ErrorWord] = None
+        self._async_pf: Optional[AsyncPrefetcher] = None
+        self._top_layer = -1         # highest layer index attended so far (end of a decode step)
         # True: decode launches use the fixed block-to-wave schedule (bitwise
         # reproducible); False: blocks go to waves on demand (faster)
         self.deterministic_decode = False
@@ -174,6 +198,7 @@ class HeteroKVManager:
         self._waited: List[int] = []
         self._selection_of: Dict[int, Any] = {}
         self._window_tables: Dict[Any, Tuple[torch.Tensor, int]] = {}
+        self._selection_b: Dict[int, List[str]] = {}
         # retrieval of the INT4 middle at decode: None = every chunk (decompress_dram_chunks,
         # manager.py:779-821); an int or "adaptive" = the top-w chunks by score
         # (get_dram_chunks_quantized_adaptive, manager.py:931-1056)
@@ -191,6 +216,25 @@ class HeteroKVManager:
     def tail_budget(self) -> int:
         return self.hbm_budget_tokens - self.sink_tokens
 
+    # ---------------------------------------------------------------- device error word
+    def _errword(self) -> "ops.ErrorWord":
+        """The device int32 every kernel of this manager reports HKV_ERR_BIT_* into."""
+        if self._err is None:
+            self._err = ops.ErrorWord(self.device)
+            self._err.on_error = self._on_device_error
+        return self._err
+
+    def _on_device_error(self, bits: int) -> None:
+        if bits & _lib.ERR_BIT_PLACEMENT and self._workspace is not None:
+            self._workspace.placement_failed()
+
+    def check_errors(self) -> None:
+        """Raise HeteroKVError if any kernel of this manager reported a device error
+        (bad block id, slot, decode placement, bf16 range) since the last check.  This
+        synchronizes; attend_decode checks without blocking (one step late)."""
+        if self._err is not None:
+            self._err.check()
+
     def _state(self, layer_idx, key_states) -> _LayerState:
         if layer_idx < 0:
             raise ValueError("Invalid layer %d" % layer_idx)
@@ -202,7 +246,7 @@ class HeteroKVManager:
             if D != HEAD_DIM:
                 raise HeteroKVError(-4, "head_dim must be 128, got %d" % D)
             st = _LayerState(B, H, key_states.device, key_states.dtype, self.sink_tokens, self.tail_budget,
-                             self._heavyhitter_budget)
+                             self._heavyhitter_budget, self._errword())
             self._layers[layer_idx] = st
         return st
 
@@ -227,15 +271,18 @@ class HeteroKVManager:
         """manager.py:175-204.  Returns the K/V the reference would hand to attention
         (prefill: the full input or sink + old tail + chunk; decode: sink + tail + heavy
         hitters).  With materialize=False the bookkeeping is done and (None, None) is
-        returned for decode, for callers that attend with `attend_decode`."""
+        returned, for callers that attend with `attend_decode` / `attend_prefill`: a later
+        prefill chunk then leaves the old tail in place for attend_prefill and writes the
+        chunk into the tail ring after it (or at the layer's next operation)."""
         if mode not in ("prefill", "decode"):
             raise ValueError("Unknown mode: %s" % mode)
         self._check_input(key_states, value_states)
         st = self._state(layer_idx, key_states)
+        st.flush()
         if mode == "prefill":
             st.dev_state = None
             if st.prefilled:
-                return self._incremental_prefill(layer_idx, st, key_states, value_states, seq_offset)
+                return self._incremental_prefill(layer_idx, st, key_states, value_states, seq_offset, materialize)
             return self._first_prefill(layer_idx, st, key_states, value_states, seq_offset)
         return self._decode(layer_idx, st, key_states, value_states, seq_offset, materialize)
 
@@ -243,7 +290,7 @@ class HeteroKVManager:
         n = k.shape[2]
         sink_amt = min(n, self.sink_tokens)
         if sink_amt:
-            st.sink.write(_as16(k[:, :, :sink_amt]), _as16(v[:, :, :sink_amt]), [0] * st.B)
+            st.sink.write(k[:, :, :sink_amt], v[:, :, :sink_amt], 0, err=st.err)
         st.sink_len = sink_amt
         st.sink_pos = list(range(seq_offset, seq_offset + sink_amt))
         tail_amt = min(n - sink_amt, self.tail_budget)
@@ -258,7 +305,9 @@ class HeteroKVManager:
         st.seq_offset = seq_offset + n
         return k, v
 
-    def _incremental_prefill(self, layer, st, k, v, seq_offset):
+    def _incremental_prefill(self, layer, st, k, v, seq_offset, materialize=True):
+        if not materialize:
+            return self._incremental_prefill_deferred(layer, st, k, v, seq_offset)
         n = k.shape[2]
         old_k, old_v = st.tail_tensors()
         old_pos = list(st.tail_pos)
@@ -281,28 +330,66 @@ class HeteroKVManager:
         st.seq_offset = seq_offset + n
         return ret_k, ret_v
 
+    def _incremental_prefill_deferred(self, layer, st, k, v, seq_offset):
+        """_incremental_prefill_update (manager.py:537-586) without materializing
+        sink + old tail + chunk: the oldest tokens of [old tail | chunk] beyond the tail
+        budget are evicted now, and the chunk's surviving tokens are written into the
+        tail ring in place -- after attend_prefill has read the old tail (or at this
+        layer's next operation).  While the write is pending the ring still holds the
+        old tail: either it is not full and its tokens sit in slots [0, len), or it is
+        full and every slot is valid, which is all attend_prefill needs."""
+        n = k.shape[2]
+        L, R = st.tail_len, st.ring
+        old_pos = list(st.tail_pos)
+        combined_pos = old_pos + list(range(seq_offset, seq_offset + n))
+        total = L + n
+        e = max(0, total - self.tail_budget)
+        if e and self.enable_quant:
+            eo = min(e, L)
+            parts_k, parts_v = [], []
+            if eo:
+                ok, ov = st.tail_tensors(0, eo)
+                parts_k.append(ok.to(k.dtype))
+                parts_v.append(ov.to(v.dtype))
+            if e > L:
+                parts_k.append(k[:, :, :e - L])
+                parts_v.append(v[:, :, :e - L])
+            ek = parts_k[0] if len(parts_k) == 1 else torch.cat(parts_k, dim=2)
+            ev = parts_v[0] if len(parts_v) == 1 else torch.cat(parts_v, dim=2)
+            self._evict(layer, st, ek, ev, combined_pos[:e])
+        i0 = max(0, e - L)                          # chunk tokens [i0, n) survive into the tail
+        slot = (st.tail_head + L + i0) % R
+        st.pending = (k, v, i0, slot, L)
+        if e:
+            st.tail_head = (st.tail_head + e) % R
+            st.tail_len = R
+        else:
+            st.tail_len = total
+        st.tail_pos = deque(combined_pos[e:])
+        st.seq_offset = seq_offset + n
+        return None, None
+
     def _decode(self, layer, st, k, v, seq_offset, materialize):
         if k.shape[2] != 1:
             raise HeteroKVError(-1, "decode expects one new token, got %d" % k.shape[2])
-        k16, v16 = _as16(k), _as16(v)
         if self.device_decode:
             if st.dev_state is None:
                 self._sync_device_state(st)
-            st.tail.step(st.hh, k16, v16, st.ring, self._heavyhitter_budget, st.dev_state, st.dev_tail_lens,
-                         st.dev_hh_lens)
-        self._decode_host(st, seq_offset, k16, v16, launch=not self.device_decode)
+            st.tail.step(st.hh, k, v, st.ring, self._heavyhitter_budget, st.dev_state, st.dev_tail_lens,
+                         st.dev_hh_lens, err=st.err)
+        self._decode_host(st, seq_offset, k, v, launch=not self.device_decode)
         if not materialize:
             return None, None
         kk, vv = self.get_hbm_kv(layer)
         return kk.to(k.dtype), vv.to(v.dtype)
 
-    def _decode_host(self, st, seq_offset, k16, v16, launch):
+    def _decode_host(self, st, seq_offset, k, v, launch):
         """The decode step's zone decision (manager.py:588-674 as this build keeps it), with
         its kernels when `launch` (device-stepped decode takes the same decision on the GPU)."""
         pos = seq_offset
         if st.tail_len < self.tail_budget:
             if launch:
-                st.tail.write(k16, v16, [st.tail_head + st.tail_len] * st.B, ring=st.ring)
+                st.tail.write(k, v, st.tail_head + st.tail_len, ring=st.ring, err=st.err)
             st.tail_len += 1
             st.tail_pos.append(pos)
         else:
@@ -318,7 +405,7 @@ class HeteroKVManager:
             else:
                 self._queued_tokens += 1
             if launch:
-                st.tail.write(k16, v16, [st.tail_head] * st.B, ring=st.ring)
+                st.tail.write(k, v, st.tail_head, ring=st.ring, err=st.err)
             st.tail_head = (st.tail_head + 1) % st.ring
             st.tail_pos.append(pos)
         st.tail_started = True
@@ -357,7 +444,7 @@ class HeteroKVManager:
         """manager.py:1231-1299: quantize + pack into the layer's INT4 blocks, record the chunk."""
         n = k.shape[2]
         st.ensure_int4(st.int4_len + n)
-        ops.pack_tokens(st.pool, k, v, torch.full((st.B,), st.int4_len, dtype=torch.int32), st.bt)
+        ops.pack_tokens(st.pool, k, v, torch.full((st.B,), st.int4_len, dtype=torch.int32), st.bt, err=st.err)
         key = "l%d_e%d" % (layer, self._eviction_counter)
         self._chunks[key] = (layer, st.int4_len, n)
         if isinstance(first_pos, int):
@@ -492,21 +579,162 @@ class HeteroKVManager:
             outs.append(torch.stack(per_b))
         return outs[0], outs[1], st.int4_len
 
-    def get_dram_chunks_quantized(self, layer_idx: int, window_size: Optional[int] = None):
-        """manager.py:931-1056 semantics without the Python chunk copies: the chosen chunks'
-        INT4 tokens in reference layout (highest chunk score first, concatenated in eviction
-        order).  window_size None = all chunks."""
-        pre = "l%d_" % layer_idx
-        keys = [k for k in self._chunks if k.startswith(pre)]
+    def _adaptive_selection(self, layer_idx: int, window_size: Optional[int]) -> List[str]:
+        """The chunk keys manager.py:857-878 / :966-978 select: w = window_size, or the
+        controller's w_t (one compute_window call) clamped to [1, #chunks] when None; the
+        top w by chunk score (stable descending sort), returned in eviction order."""
+        keys = self._layer_chunks(layer_idx)
+        if not keys:
+            return []
+        if window_size is None:
+            w_t = int(self._adaptive_controller.compute_window(attention_weights=self._last_attention_weights,
+                                                               cache_miss=False))
+            window_size = max(1, min(w_t, len(keys)))
+        ranked = sorted(keys, key=lambda k: self._chunk_attention_scores.get(k, 0.0), reverse=True)
+        chosen = set(ranked[:max(0, int(window_size))])
+        return [k for k in self._chunk_eviction_order if k in chosen]
+
+    def get_dram_chunks_quantized_adaptive(self, layer_idx: int, window_size: Optional[int] = None
+                                           ) -> Optional[Dict[str, torch.Tensor]]:
+        """manager.py:931-1056 (Path A gather): the INT4 tokens of the top-w chunks, not
+        dequantized, as the six reference-layout tensors: k_data/v_data uint8 [B, H, T, 128]
+        concatenated along the token axis in eviction order, the 1-D scales and zero points
+        concatenated chunk after chunk.  window_size None: w_t from the adaptive controller.
+        (The reference indexes its ranked list by eviction-list positions when it
+        concatenates, :1012-1017, which only returns the selected chunks when they are the
+        first ones in eviction order -- always the case under its default 1/(c+1) chunk
+        scores; this returns the selected chunks in eviction order for any scores.)"""
+        keys = self._adaptive_selection(layer_idx, window_size)
         if not keys:
             return None
-        if window_size is not None:
-            ranked = sorted(keys, key=lambda k: self._chunk_attention_scores.get(k, 0.0), reverse=True)
-            chosen = set(ranked[:max(1, min(window_size, len(keys)))])
-            keys = [k for k in self._chunk_eviction_order if k in chosen]
         parts = [self.chunk_codes(k) for k in keys]
         return {name: torch.cat([p[name] for p in parts], dim=2 if name.endswith("_data") else 0)
                 for name in parts[0]}
+
+    def decompress_dram_chunks_adaptive(self, layer_idx: int, window_size: Optional[int] = None):
+        """manager.py:823-929 (Path B): the top-w chunks dequantized to bf16
+        (KVCompressor.decompress(..., target_dtype=bf16)), concatenated in eviction order.
+        Returns (K, V, count) or (None, None, 0)."""
+        return self._decompress_keys(self._adaptive_selection(layer_idx, window_size))
+
+    def _decompress_keys(self, keys):
+        if not keys:
+            return None, None, 0
+        ks, vs = [], []
+        for key in keys:
+            e = self.chunk_codes(key)
+            ks.append(self._compressor.decompress(e["k_data"], e["k_scales"], e["k_zps"], target_dtype=torch.bfloat16))
+            vs.append(self._compressor.decompress(e["v_data"], e["v_scales"], e["v_zps"], target_dtype=torch.bfloat16))
+        K = ks[0] if len(ks) == 1 else torch.cat(ks, dim=-2)
+        V = vs[0] if len(vs) == 1 else torch.cat(vs, dim=-2)
+        return K, V, K.shape[-2]
+
+    def _path_b_keys(self, layer_idx: int) -> List[str]:
+        """The chunks Path B attends at this decode step, chosen once per layer and step
+        (one compute_window call, as decompress_dram_chunks_adaptive makes), so that
+        get_mask_sizes and update agree."""
+        keys = self._selection_b.get(layer_idx)
+        if keys is None:
+            keys = self._selection_b[layer_idx] = self._adaptive_selection(layer_idx, None)
+        return keys
+
+    def selected_tokens(self, layer_idx: int) -> int:
+        """INT4 tokens of the chunks Path B attends at this step."""
+        return sum(self._chunks[k][2] for k in self._path_b_keys(layer_idx))
+
+    def decompress_selected(self, layer_idx: int):
+        """Path B for this step: the chosen chunks as bf16 (K, V, count)."""
+        keys = self._path_b_keys(layer_idx)
+        self._selection_b.pop(layer_idx, None)
+        return self._decompress_keys(keys)
+
+    @property
+    def heavy_hitter_budget(self) -> int:
+        return self._heavyhitter_budget
+
+    def heavy_hitter_length(self, layer_idx: int) -> int:
+        st = self._layers[layer_idx] if layer_idx < len(self._layers) else None
+        return 0 if st is None else st.hh_len
+
+    # ---------------------------------------------------------------- per-chunk swap-in
+    def swap_in_quantized(self, layer_idx: int, chunk_key: str) -> Optional[Dict[str, torch.Tensor]]:
+        """manager.py:233-263: one chunk's INT4 data on the device without dequantizing
+        (k_data, k_scales, k_zps, v_data, v_scales, v_zps), or None; the chunk stays."""
+        if chunk_key not in self._chunks:
+            return None
+        return self.chunk_codes(chunk_key)
+
+    def schedule_prefetch(self, chunk_key: str) -> None:
+        """manager.py:335-350: dequantize the chunk to bf16 on the prefetcher's side stream
+        (AsyncPrefetcher) so that a later swap_in finds it ready."""
+        if not self.enable_prefetch or chunk_key not in self._chunks:
+            return
+        if self._async_pf is None:
+            self._async_pf = AsyncPrefetcher(self.device)
+        self._async_pf.submit_prefetch_task(chunk_key, self.chunk_codes(chunk_key), self._compressor)
+
+    def swap_in(self, layer_idx: int, chunk_key: str) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+        """manager.py:265-292: remove the chunk from the INT4 tier and return its K, V as
+        bf16 [B, H, T, 128] (decompress to fp16, then .to(bf16), as the reference), from a
+        finished schedule_prefetch when there is one.  Later Path C gathers no longer see
+        the chunk.  None if the key is unknown."""
+        if chunk_key not in self._chunks:
+            return None
+        got = self._async_pf.fetch_if_ready(chunk_key) if self._async_pf is not None else None
+        if got is None:
+            e = self.chunk_codes(chunk_key)
+            k = self._compressor.decompress(e["k_data"], e["k_scales"], e["k_zps"]).to(torch.bfloat16)
+            v = self._compressor.decompress(e["v_data"], e["v_scales"], e["v_zps"]).to(torch.bfloat16)
+        else:
+            k, v = got
+        self._remove_chunk(chunk_key)
+        return k, v
+
+    def _remove_chunk(self, key: str) -> None:
+        """Drop one chunk from its layer's INT4 tier.  A chunk that starts on a block
+        boundary and ends on one (or at the layer's end) leaves by a block-table edit;
+        otherwise the later tokens move down by unpack + repack (per-token groups, so the
+        codes are unchanged)."""
+        layer, start, n = self._chunks.pop(key)
+        # as the reference's _dram.remove: the chunk's eviction-order entry and score stay
+        st = self._layers[layer]
+        for k2, (l2, s2, n2) in list(self._chunks.items()):
+            if l2 == layer and s2 > start:
+                self._chunks[k2] = (l2, s2 - n, n2)
+        del st.int4_pos[start:start + n]
+        end = start + n
+        if start % BLOCK_TOKENS == 0 and (n % BLOCK_TOKENS == 0 or end == st.int4_len):
+            lb0, lb1 = start // BLOCK_TOKENS, (end + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+            d = lb1 - lb0
+            st.bt_host[:, lb0:st.nb - d] = st.bt_host[:, lb1:st.nb].copy()
+            st.nb -= d
+            if st.host_lbs is not None:
+                hl = st.host_lbs
+                st.host_lbs = np.where(hl >= lb1, hl - d, np.where(hl >= lb0, lb0, hl))
+        else:
+            if st.n_host:
+                raise HeteroKVError(-4, "swap_in: chunk %s is not block aligned (%d+%d) and its layer has "
+                                        "records in host memory" % (key, start, n))
+            rest = st.int4_len - end
+            if rest:
+                pieces = {}
+                for which, name in ((0, "k"), (1, "v")):
+                    cs, ss, zs = [], [], []
+                    for b in range(st.B):
+                        c, sc, z = ops.unpack_tokens(st.pool, st.bt[b], st.int4_len, which)
+                        cs.append(c[:, end:])
+                        ss.append(sc.view(st.H, -1)[:, end:])
+                        zs.append(z.view(st.H, -1)[:, end:])
+                    pieces[name] = (torch.stack(cs), torch.stack(ss), torch.stack(zs))
+                ops.repack_codes(st.pool, pieces["k"][0], pieces["v"][0], pieces["k"][1], pieces["v"][1],
+                                 pieces["k"][2], pieces["v"][2], torch.full((st.B,), start, dtype=torch.int32),
+                                 st.bt, err=st.err)
+            st.nb = (st.int4_len - n + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+        st.int4_len -= n
+        st.bt = torch.from_numpy(np.ascontiguousarray(st.bt_host)).to(self.device)
+        st.version += 1
+        st.resident_cache = None
+        self._window_tables = {k2: v for k2, v in self._window_tables.items() if k2[0] != layer}
 
     # ---------------------------------------------------------------- host tier
     def offload_to_host(self, fraction: float, seed: int = 0, layers: Optional[List[int]] = None) -> int:
@@ -693,7 +921,9 @@ class HeteroKVManager:
 
     def prefetch_stats(self, reset: bool = True) -> Dict[str, Any]:
         """Stall of every layer that waited for host records since the last call: per layer
-        max(0, t(copies done) - t(kernel needs them)) in ms (synchronizes on those events)."""
+        max(0, t(copies done) - t(kernel needs them)) in ms (synchronizes on those events,
+        and raises if a kernel reported a device error meanwhile)."""
+        self.check_errors()
         per = [(slot // 2, self._pf.stall_ms(slot)) for slot in self._waited] if self._pf is not None else []
         if reset:
             self._waited = []
@@ -714,8 +944,13 @@ class HeteroKVManager:
         st = self._layers[layer_idx]
         if st is None:
             raise RuntimeError("Layer %d has not been allocated yet." % layer_idx)
+        st.flush()
         if self._workspace is None:
             self._workspace = ops.DecodeWorkspace(self.device)
+        err = self._errword()
+        capturing = torch.cuda.is_current_stream_capturing()
+        if layer_idx == 0 and not capturing:
+            err.poll()           # a step's errors surface at the next step's first layer
         if feed_oracle and self.device_decode:
             raise HeteroKVError(-1, "attend_decode: feed_oracle needs host-stepped decode")
         zones = []
@@ -752,18 +987,19 @@ class HeteroKVManager:
             self._prefetch_after(layer_idx)
         if staged:
             self._pf.wait(slot)
-        q16 = _as16(query_states)
+        q = query_states
         scores = stats = None
         if feed_oracle:
             n_items = n4 + sum(z[2] for z in zones)
-            scores = torch.full((q16.shape[0], q16.shape[1], max(n_items, 1)), float("-inf"),
-                                dtype=torch.float32, device=q16.device)
-            stats = torch.empty((q16.shape[0], q16.shape[1], 2), dtype=torch.float32, device=q16.device)
-        out = ops.decode_attention(q16, zones=zones, pool=st.pool if n4 else None,
+            scores = torch.full((q.shape[0], q.shape[1], max(n_items, 1)), float("-inf"),
+                                dtype=torch.float32, device=q.device)
+            stats = torch.empty((q.shape[0], q.shape[1], 2), dtype=torch.float32, device=q.device)
+        out = ops.decode_attention(q, zones=zones, pool=st.pool if n4 else None,
                                    block_table=bt if n4 else None, int4_max_len=n4,
                                    sm_scale=sm_scale, workspace=self._workspace,
                                    staging=self._staging[buf] if staged else None,
-                                   deterministic=self.deterministic_decode, scores=scores, score_stats=stats)
+                                   deterministic=self.deterministic_decode, scores=scores, score_stats=stats,
+                                   err=err, out_dtype=q.dtype)
         if feed_oracle:
             w = ops.attn_weights(scores[:1], stats[:1], order=self._score_order(st, n4))
             self.update_attention_scores(w[0])
@@ -772,7 +1008,33 @@ class HeteroKVManager:
             self._pending.pop(layer_idx, None)
             self._waited.append(slot)
         self._selection_of.pop(layer_idx, None)
-        return out.to(query_states.dtype)
+        if layer_idx >= self._top_layer and not capturing:
+            self._top_layer = layer_idx
+            err.post()           # the step's last layer: its error word heads back to the host
+        return out
+
+    # ---------------------------------------------------------------- fused prefill
+    def attend_prefill(self, layer_idx: int, query_states: torch.Tensor, key_states: torch.Tensor,
+                       value_states: torch.Tensor, sm_scale: Optional[float] = None) -> torch.Tensor:
+        """Attention of a prefill chunk exactly as the reference hands it to SDPA
+        (manager.py:533-535,562-563), on the MFMA prefill kernel: every query sees the sink
+        and the tail as they were before this chunk, and the chunk causally.  The chunk's
+        K/V are those just given to update(..., materialize=False); its deferred tail write
+        happens right after.  query [B, Hq, S, 128]; returns [B, Hq, S, 128] in its dtype."""
+        st = self._layers[layer_idx]
+        if st is None:
+            raise RuntimeError("Layer %d has not been allocated yet." % layer_idx)
+        zones = []
+        if st.pending is not None:
+            old_len = st.pending[4]
+            if st.sink_len:
+                zones.append((st.sink, None, st.sink_len))
+            if old_len:
+                zones.append((st.tail, None, old_len))
+        out = ops.prefill_attention(query_states, zones=zones, chunk_k=key_states, chunk_v=value_states,
+                                    sm_scale=sm_scale, err=self._errword(), out_dtype=query_states.dtype)
+        st.flush()
+        return out
 
     # ---------------------------------------------------------------- heavy-hitter scores
     def update_attention_scores(self, attention_weights: torch.Tensor) -> None:

@@ -28,6 +28,61 @@ def _p(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
 
+def _aligned16(t):
+    """16-byte aligned base and strides (in elements) that are multiples of 8, unit last stride."""
+    return t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(st % 8 == 0 for st in t.stride()[:-1])
+
+
+_F16_OR_BF16 = (torch.float16, torch.bfloat16)
+
+
+class ErrorWord:
+    """A device int32 that kernels OR HKV_ERR_BIT_* into, with a pinned host mirror.
+
+    post() enqueues a copy of the word to the mirror and records an event on the current
+    stream; poll() looks at the last posted copy only if that event has completed (it
+    never blocks) and raises HeteroKVError if a bit was set; check() synchronizes.  A
+    raised error clears the word."""
+
+    def __init__(self, device):
+        self.device = torch.device(device)
+        self.dev = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self._event = None
+        self.on_error = None   # optional callback(bits) run before the exception
+
+    def ptr(self):
+        return self.dev.data_ptr()
+
+    def post(self):
+        self.host.copy_(self.dev, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self._event = ev
+
+    def poll(self):
+        ev = self._event
+        if ev is None or not ev.query():
+            return
+        self._event = None
+        bits = int(self.host[0])
+        if bits:
+            self._fail(bits)
+
+    def check(self):
+        self._event = None
+        bits = int(self.dev.item())
+        if bits:
+            self._fail(bits)
+
+    def _fail(self, bits):
+        self.dev.zero_()
+        self.host.zero_()
+        if self.on_error is not None:
+            self.on_error(bits)
+        raise HeteroKVError(_lib.ERR_DEVICE, "device error word 0x%x: %s" % (bits, _lib.describe_error_bits(bits)))
+
+
 def record_bytes(num_kv_heads, head_dim=HEAD_DIM):
     n = load().hkv_block_bytes(num_kv_heads, head_dim)
     if n < 0:
@@ -115,8 +170,9 @@ def _check_table(bt, sp, B, T, what):
                             (what, bt.shape[0], sp.numel(), B))
 
 
-def pack_tokens(pool, k, v, start_pos, block_table):
-    """Quantize + pack k, v [B, H, T, 128] (fp16/bf16) into `pool` at INT4 slots start_pos[b] + t."""
+def pack_tokens(pool, k, v, start_pos, block_table, err=None):
+    """Quantize + pack k, v [B, H, T, 128] (fp16/bf16) into `pool` at INT4 slots start_pos[b] + t.
+    Bad block ids / slots are reported in `err` (an ErrorWord; default the pool's word)."""
     _require_gpu(k, v)
     if k.shape != v.shape or k.dim() != 4 or k.shape[-1] != HEAD_DIM:
         raise HeteroKVError(-1, "pack_tokens: k/v must both be [B, H, T, 128], got %s / %s" %
@@ -137,11 +193,12 @@ def pack_tokens(pool, k, v, start_pos, block_table):
                       src_stride_b=k.stride(0), src_stride_h=k.stride(1), src_stride_t=k.stride(2),
                       batch=B, num_kv_heads=H, head_dim=HEAD_DIM, num_tokens=T,
                       start_pos=sp.data_ptr(), block_table=bt.data_ptr(), bt_stride=bt.shape[1],
-                      pool=pool.data.data_ptr(), pool_blocks=pool.num_blocks, err_flag=pool.err.data_ptr())
+                      pool=pool.data.data_ptr(), pool_blocks=pool.num_blocks,
+                      err_flag=err.ptr() if err is not None else pool.err.data_ptr())
     check(load().hkv_pack_tokens(ctypes.byref(a), stream_ptr(k.device)), "hkv_pack_tokens")
 
 
-def repack_codes(pool, k_codes, v_codes, k_scales, v_scales, k_zps, v_zps, start_pos, block_table):
+def repack_codes(pool, k_codes, v_codes, k_scales, v_scales, k_zps, v_zps, start_pos, block_table, err=None):
     """Reference-layout INT4 (codes uint8 [B,H,T,128], scales/zps [B,H,T]) -> pool records."""
     _require_gpu(k_codes, v_codes, k_scales, v_scales, k_zps, v_zps)
     B, H, T, D = k_codes.shape
@@ -165,7 +222,8 @@ def repack_codes(pool, k_codes, v_codes, k_scales, v_scales, k_zps, v_zps, start
                         meta_stride_b=ks.stride(0), meta_stride_h=ks.stride(1), meta_stride_t=ks.stride(2),
                         batch=B, num_kv_heads=H, head_dim=HEAD_DIM, num_tokens=T,
                         start_pos=sp.data_ptr(), block_table=bt.data_ptr(), bt_stride=bt.shape[1],
-                        pool=pool.data.data_ptr(), pool_blocks=pool.num_blocks, err_flag=pool.err.data_ptr())
+                        pool=pool.data.data_ptr(), pool_blocks=pool.num_blocks,
+                        err_flag=err.ptr() if err is not None else pool.err.data_ptr())
     check(load().hkv_repack_codes(ctypes.byref(a), stream_ptr(kc.device)), "hkv_repack_codes")
 
 
@@ -201,16 +259,17 @@ class F16Zone:
     def device(self):
         return self.k.device
 
-    def write(self, k, v, slot_start, ring=0):
-        """Write k, v [B, H, T, 128] fp16 at slots slot_start[b] + t (mod `ring` if ring > 0;
-        ring=True means the whole capacity).  An int slot_start (or a list of equal ints)
-        is passed by value: no host-to-device copy."""
+    def write(self, k, v, slot_start, ring=0, err=None):
+        """Write k, v [B, H, T, 128] (fp16, or bf16 narrowed to fp16 with a range check that
+        sets HKV_ERR_BIT_RANGE in `err`, an ErrorWord) at slots slot_start[b] + t (mod `ring`
+        if ring > 0; ring=True means the whole capacity).  An int slot_start (or a list of
+        equal ints) is passed by value: no host-to-device copy."""
         _require_gpu(k, v)
-        if k.dtype != torch.float16 or v.dtype != torch.float16:
-            raise HeteroKVError(-1, "F16Zone.write: k/v must be fp16")
+        if k.dtype != v.dtype or k.dtype not in _F16_OR_BF16:
+            raise HeteroKVError(-1, "F16Zone.write: k/v must both be fp16 or bf16")
         if k.shape != v.shape or k.dim() != 4 or k.shape[-1] != HEAD_DIM:
             raise HeteroKVError(-1, "F16Zone.write: k/v must be [B, H, T, 128]")
-        if k.stride() != v.stride() or k.stride(-1) != 1:
+        if k.stride() != v.stride() or not _aligned16(k) or not _aligned16(v):
             k, v = k.contiguous(), v.contiguous()
         B, H, T, _ = k.shape
         if B != self.batch or H != self.num_kv_heads:
@@ -229,7 +288,8 @@ class F16Zone:
                                src_stride_h=k.stride(1), src_stride_t=k.stride(2), batch=B, num_kv_heads=H,
                                head_dim=HEAD_DIM, num_tokens=T, slot_start=ss.data_ptr() if ss is not None else None,
                                capacity=self.capacity, ring=(self.capacity if ring is True else int(ring)),
-                               zone_k=self.k.data_ptr(), zone_v=self.v.data_ptr(), slot_base=base)
+                               zone_k=self.k.data_ptr(), zone_v=self.v.data_ptr(), slot_base=base,
+                               dtype=_DTYPES[k.dtype], err_flag=err.ptr() if err is not None else None)
         check(load().hkv_zone_write(ctypes.byref(a), stream_ptr(k.device)), "hkv_zone_write")
 
     def copy_to(self, dst, src_slot, dst_slot, n):
@@ -238,14 +298,14 @@ class F16Zone:
                                    dst.capacity, dst_slot, self.batch, self.num_kv_heads, HEAD_DIM, n,
                                    stream_ptr(self.device)), "hkv_zone_copy")
 
-    def step(self, hh, k, v, ring, hh_budget, state, tail_lens=None, hh_lens=None):
+    def step(self, hh, k, v, ring, hh_budget, state, tail_lens=None, hh_lens=None, err=None):
         """Device-stepped decode update (hkv_zone_step) of this ring zone and the heavy-hitter
-        zone hh: k, v [B, H, 1, 128] fp16; state int32 [4] (ring head, ring length,
-        heavy-hitter length, dropped) is read and advanced on the GPU; tail_lens / hh_lens
-        (int32 [B]) receive the new lengths."""
+        zone hh: k, v [B, H, 1, 128] fp16 or bf16 (range-checked into `err`); state int32 [4]
+        (ring head, ring length, heavy-hitter length, dropped) is read and advanced on the
+        GPU; tail_lens / hh_lens (int32 [B]) receive the new lengths."""
         _require_gpu(k, v, state)
-        if k.dtype != torch.float16 or v.dtype != torch.float16 or k.shape != v.shape or k.shape[2] != 1:
-            raise HeteroKVError(-1, "F16Zone.step: k/v must be fp16 [B, H, 1, 128]")
+        if k.dtype != v.dtype or k.dtype not in _F16_OR_BF16 or k.shape != v.shape or k.shape[2] != 1:
+            raise HeteroKVError(-1, "F16Zone.step: k/v must be fp16 or bf16 [B, H, 1, 128]")
         if k.stride() != v.stride() or k.stride(-1) != 1:
             k, v = k.contiguous(), v.contiguous()
         a = _lib.ZoneStepArgs(k=k.data_ptr(), v=v.data_ptr(), src_stride_b=k.stride(0), src_stride_h=k.stride(1),
@@ -254,7 +314,8 @@ class F16Zone:
                               hh_k=_p(hh.k) if hh is not None else None, hh_v=_p(hh.v) if hh is not None else None,
                               hh_capacity=hh.capacity if hh is not None else 0, hh_budget=int(hh_budget),
                               state=state.data_ptr(), tail_lens=_p(tail_lens) if tail_lens is not None else None,
-                              hh_lens=_p(hh_lens) if hh_lens is not None else None)
+                              hh_lens=_p(hh_lens) if hh_lens is not None else None, dtype=_DTYPES[k.dtype],
+                              err_flag=err.ptr() if err is not None else None)
         check(load().hkv_zone_step(ctypes.byref(a), stream_ptr(k.device)), "hkv_zone_step")
 
     def read(self, n):
@@ -277,24 +338,40 @@ def decode_workspace_bytes(batch, num_q_heads, num_kv_heads, int4_max_len, f16_m
 
 
 class DecodeWorkspace:
-    """Zero-initialised scratch for hkv_decode_attn; grows on demand (re-zeroed when it grows)."""
+    """Zero-initialised scratch for hkv_decode_attn; grows on demand (re-zeroed when it
+    grows; the library clears its ticket area itself when the geometry changes).
 
-    def __init__(self, device):
+    agent_handoff: launches on this workspace combine their ranges through device-scope
+    memory (HKV_DECODE_AGENT_HANDOFF).  It is switched on by placement_failed(), which
+    callers run when a launch reported HKV_ERR_BIT_PLACEMENT."""
+
+    def __init__(self, device, agent_handoff=False):
         self.device = torch.device(device)
         self.buf = None
+        self.agent_handoff = bool(agent_handoff)
 
     def get(self, nbytes):
         if self.buf is None or self.buf.numel() < nbytes:
             self.buf = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=self.device)
         return self.buf
 
+    def placement_failed(self):
+        """A launch's ranges did not share one XCD: its tickets may be left inconsistent.
+        Clear the workspace and use the device-scope hand-off from now on."""
+        self.agent_handoff = True
+        if self.buf is not None:
+            self.buf.zero_()
+
     def error_flag(self):
-        """Non-zero if a decode kernel met an out-of-range block id since the last call (syncs)."""
+        """Error bits (HKV_ERR_BIT_*) that launches without their own error word left in the
+        workspace's first word since the last call (synchronizes); clears them."""
         if self.buf is None:
             return 0
         v = int(self.buf[:4].view(torch.int32).item())
         if v:
             self.buf[:4].zero_()
+            if v & _lib.ERR_BIT_PLACEMENT:
+                self.placement_failed()
         return v
 
 
@@ -305,10 +382,12 @@ def _int4_source(pool, staging):
 
 def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
                      sm_scale=None, workspace=None, out=None, splits=0, staging=None, deterministic=False,
-                     scores=None, score_stats=None):
+                     scores=None, score_stats=None, err=None, out_dtype=None):
     """Split-K decode attention over fp16 zones and the INT4 pool.
 
-    q: [B, Hq, 128] or [B, Hq, 1, 128] fp16.
+    q: [B, Hq, 128] or [B, Hq, 1, 128] fp16 or bf16 (bf16 is range-checked into the error
+    word).  out_dtype: fp16 or bf16 (default: q's dtype).  err: ErrorWord for
+    HKV_ERR_BIT_* (default: the workspace's first word).
     zones: sequence of (F16Zone, lens int32 [B] or None, max_len).
     pool / block_table [B, nblk] / int4_lens [B] / int4_max_len: the INT4 zone.
     staging: Int4Pool whose record i a block-table entry ~i (negative) names.
@@ -326,8 +405,12 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
     _require_gpu(q)
     squeeze = q.dim() == 4
     q3 = q.reshape(q.shape[0], q.shape[1], q.shape[-1]) if squeeze else q
-    if q3.dtype != torch.float16 or q3.shape[-1] != HEAD_DIM:
-        raise HeteroKVError(-1, "decode_attention: q must be fp16 [B, Hq, 128]")
+    if q3.dtype not in _F16_OR_BF16 or q3.shape[-1] != HEAD_DIM:
+        raise HeteroKVError(-1, "decode_attention: q must be fp16 or bf16 [B, Hq, 128]")
+    if out_dtype is None:
+        out_dtype = q3.dtype if out is None else out.dtype
+    if out_dtype not in _F16_OR_BF16:
+        raise HeteroKVError(-1, "decode_attention: out dtype must be fp16 or bf16")
     if q3.stride(-1) != 1 or q3.data_ptr() % 16 or q3.stride(0) % 8 or q3.stride(1) % 8:
         q3 = q3.contiguous()
     B, Hq, _ = q3.shape
@@ -340,8 +423,12 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
         sm_scale = 1.0 / math.sqrt(HEAD_DIM)
     dev = q3.device
     if out is None:
-        out = torch.empty((B, Hq, HEAD_DIM), dtype=torch.float16, device=dev)
+        out = torch.empty((B, Hq, HEAD_DIM), dtype=out_dtype, device=dev)
+    elif out.dtype != out_dtype:
+        raise HeteroKVError(-1, "decode_attention: out is %s, out_dtype %s" % (out.dtype, out_dtype))
     a = _lib.DecodeArgs()
+    a.q_dtype, a.out_dtype = _DTYPES[q3.dtype], _DTYPES[out_dtype]
+    a.err_flag = err.ptr() if err is not None else None
     a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, HEAD_DIM
     a.sm_scale = float(sm_scale)
     a.q, a.q_stride_b, a.q_stride_h = q3.data_ptr(), q3.stride(0), q3.stride(1)
@@ -382,7 +469,8 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
     ws = workspace.get(nbytes)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     a.splits_hint = int(splits)
-    a.flags = _lib.DECODE_DETERMINISTIC if deterministic else 0
+    a.flags = (_lib.DECODE_DETERMINISTIC if deterministic else 0) | \
+        (_lib.DECODE_AGENT_HANDOFF if workspace.agent_handoff else 0)
     if scores is not None:
         _require_gpu(scores, score_stats)
         if score_stats is None or scores.dtype != torch.float32 or score_stats.dtype != torch.float32:
@@ -398,7 +486,7 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
 
 
 # ----------------------------------------------------------------------- record gather
-def gather_blocks(src, ids, dst, staging=None, dst_offset=0):
+def gather_blocks(src, ids, dst, staging=None, dst_offset=0, err=None):
     """dst record dst_offset + i = record ids[i] of src (ids >= 0) or of staging (~ids[i]).
 
     src / staging / dst: Int4Pool with the same record size.  ids: int32 (device or host)."""
@@ -419,7 +507,8 @@ def gather_blocks(src, ids, dst, staging=None, dst_offset=0):
                                    src.num_blocks if src is not None else 0,
                                    staging.data.data_ptr() if staging is not None else None,
                                    staging.num_blocks if staging is not None else 0,
-                                   ids.data_ptr(), n, rb, dst.data[dst_offset].data_ptr(), dst.err.data_ptr(),
+                                   ids.data_ptr(), n, rb, dst.data[dst_offset].data_ptr(),
+                                   err.ptr() if err is not None else dst.err.data_ptr(),
                                    stream_ptr(dev)), "hkv_gather_blocks")
     return dst
 
@@ -482,16 +571,23 @@ def eviction_candidates(token_scores, seq_len, block_size, sink_tokens, local_wi
 
 # ----------------------------------------------------------------------- prefill attention
 def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
-                      chunk_k=None, chunk_v=None, sm_scale=None, out=None, staging=None):
+                      chunk_k=None, chunk_v=None, sm_scale=None, out=None, staging=None, err=None,
+                      out_dtype=None):
     """Chunked-prefill attention (hkv_prefill_attn).
 
-    q: [B, Hq, Sq, 128] fp16.  Every query attends to all fp16-zone tokens and all INT4
-    tokens, plus -- when chunk_k/chunk_v [B, Hkv, Sq, 128] fp16 are given -- causally to
-    the chunk itself.  Returns fp16 [B, Hq, Sq, 128].
+    q: [B, Hq, Sq, 128] fp16 or bf16.  Every query attends to all fp16-zone tokens and all
+    INT4 tokens, plus -- when chunk_k/chunk_v [B, Hkv, Sq, 128] (fp16 or bf16) are given --
+    causally to the chunk itself.  bf16 inputs are range-checked into the error word
+    (err: ErrorWord; default: the INT4 pool's).  Returns [B, Hq, Sq, 128] in out_dtype
+    (default q's dtype).
     """
     _require_gpu(q, chunk_k, chunk_v)
-    if q.dtype != torch.float16 or q.dim() != 4 or q.shape[-1] != HEAD_DIM:
-        raise HeteroKVError(-1, "prefill_attention: q must be fp16 [B, Hq, Sq, 128]")
+    if q.dtype not in _F16_OR_BF16 or q.dim() != 4 or q.shape[-1] != HEAD_DIM:
+        raise HeteroKVError(-1, "prefill_attention: q must be fp16 or bf16 [B, Hq, Sq, 128]")
+    if out_dtype is None:
+        out_dtype = q.dtype if out is None else out.dtype
+    if out_dtype not in _F16_OR_BF16:
+        raise HeteroKVError(-1, "prefill_attention: out dtype must be fp16 or bf16")
     if q.stride(-1) != 1 or q.data_ptr() % 16 or any(st % 8 for st in q.stride()[:3]):
         q = q.contiguous()
     B, Hq, Sq, _ = q.shape
@@ -503,8 +599,12 @@ def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, 
         sm_scale = 1.0 / math.sqrt(HEAD_DIM)
     dev = q.device
     if out is None:
-        out = torch.empty((B, Hq, Sq, HEAD_DIM), dtype=torch.float16, device=dev)
+        out = torch.empty((B, Hq, Sq, HEAD_DIM), dtype=out_dtype, device=dev)
+    elif out.dtype != out_dtype:
+        raise HeteroKVError(-1, "prefill_attention: out is %s, out_dtype %s" % (out.dtype, out_dtype))
     a = _lib.PrefillArgs()
+    a.q_dtype, a.out_dtype = _DTYPES[q.dtype], _DTYPES[out_dtype]
+    a.chunk_dtype = _DTYPES[chunk_k.dtype] if chunk_k is not None else _lib.DTYPE_F16
     a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.num_queries = B, Hq, Hkv, HEAD_DIM, Sq
     a.sm_scale = float(sm_scale)
     a.q, a.q_stride_b, a.q_stride_h, a.q_stride_t = q.data_ptr(), q.stride(0), q.stride(1), q.stride(2)
@@ -517,7 +617,7 @@ def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, 
             keep.append(lt)
         a.f16[i] = _lib.F16Zone(k=z.k.data_ptr(), v=z.v.data_ptr(), capacity=z.capacity, max_len=int(max_len),
                                 lens=lt.data_ptr() if lt is not None else 0)
-    err = None
+    pool_err = None
     if int4_max_len > 0:
         bt = _i32(block_table, dev)
         if bt.dim() == 1:
@@ -530,7 +630,7 @@ def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, 
         if staging is not None:
             a.staging, a.staging_blocks = staging.data.data_ptr(), staging.num_blocks
         a.block_table, a.bt_stride = bt.data_ptr(), bt.shape[1]
-        err = (pool if pool is not None else staging).err
+        pool_err = (pool if pool is not None else staging).err
         if int4_lens is not None:
             il = _i32(int4_lens, dev)
             keep.append(il)
@@ -539,13 +639,16 @@ def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, 
     if chunk_k is not None:
         if chunk_k.shape != (B, Hkv, Sq, HEAD_DIM) or chunk_v.shape != chunk_k.shape:
             raise HeteroKVError(-1, "prefill_attention: chunk K/V must be [B, Hkv, Sq, 128]")
-        if chunk_k.dtype != torch.float16 or chunk_v.dtype != torch.float16:
-            raise HeteroKVError(-1, "prefill_attention: chunk K/V must be fp16")
-        if chunk_k.stride() != chunk_v.stride() or chunk_k.stride(-1) != 1:
+        if chunk_k.dtype != chunk_v.dtype or chunk_k.dtype not in _F16_OR_BF16:
+            raise HeteroKVError(-1, "prefill_attention: chunk K/V must both be fp16 or bf16")
+        if chunk_k.stride() != chunk_v.stride() or not _aligned16(chunk_k) or not _aligned16(chunk_v):
             chunk_k, chunk_v = chunk_k.contiguous(), chunk_v.contiguous()
         a.chunk_k, a.chunk_v = chunk_k.data_ptr(), chunk_v.data_ptr()
         a.chunk_stride_b, a.chunk_stride_h, a.chunk_stride_t = chunk_k.stride(0), chunk_k.stride(1), chunk_k.stride(2)
     a.out, a.out_stride_b, a.out_stride_h, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1), out.stride(2)
-    a.err_flag = err.data_ptr() if err is not None else 0
+    if err is not None:
+        a.err_flag = err.ptr()
+    else:
+        a.err_flag = pool_err.data_ptr() if pool_err is not None else 0
     check(load().hkv_prefill_attn(ctypes.byref(a), stream_ptr(dev)), "hkv_prefill_attn")
     return out

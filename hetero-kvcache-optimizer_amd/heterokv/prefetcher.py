@@ -228,6 +228,9 @@ class AsyncPrefetcher:
         self._free_slots = list(range(self._SLOTS))
 
     def submit_prefetch_task(self, chunk_key: str, dram_data: Dict[str, Any], compressor) -> None:
+        """prefetcher.py:47-98.  Entries held in host memory are copied on the side stream
+        first; entries already on this device (the GPU manager's chunks) are dequantized
+        there directly."""
         if chunk_key in self.buffer:
             return
         split = "k_data" in dram_data and "v_data" in dram_data
@@ -239,9 +242,13 @@ class AsyncPrefetcher:
         if not self._free_slots:
             raise HeteroKVError(-3, "AsyncPrefetcher: more than %d chunks pending" % self._SLOTS)
         names = _ENTRY_KEYS if split else ("q_data", "scales", "zps")
+        on_device = all(dram_data[k].device == self.device for k in names)
         dev_t, copies = {}, []
         for k in names:
             src = dram_data[k]
+            if on_device:
+                dev_t[k] = (None, src)
+                continue
             if src.device.type != "cpu":
                 src = src.cpu()
             src = src.contiguous()
@@ -251,11 +258,14 @@ class AsyncPrefetcher:
             dev_t[k] = (src, dst)
         slot = self._free_slots.pop()
         side = self._pf.side_stream
-        # the destinations were allocated on the current stream: the side stream must not
-        # write them before that stream reaches this point
+        # the destinations (or the device entry) come from the current stream: the side
+        # stream must not touch them before that stream reaches this point
         side.wait_stream(torch.cuda.current_stream(self.device))
         self._pf.submit(copies, slot)
         with torch.cuda.stream(side):
+            if on_device:
+                for _, t in dev_t.values():
+                    t.record_stream(side)
             if split:
                 rk = compressor.decompress(dev_t["k_data"][1], dev_t["k_scales"][1], dev_t["k_zps"][1]).to(torch.bfloat16)
                 rv = compressor.decompress(dev_t["v_data"][1], dev_t["v_scales"][1], dev_t["v_zps"][1]).to(torch.bfloat16)
@@ -265,7 +275,7 @@ class AsyncPrefetcher:
         self._pf.record(slot)
         # keep host sources alive until the copies are done (consumed at fetch)
         self._host_refs = getattr(self, "_host_refs", {})
-        self._host_refs[chunk_key] = [s for s, _ in dev_t.values()]
+        self._host_refs[chunk_key] = [s for s, _ in dev_t.values() if s is not None]
         self.buffer[chunk_key] = (rk, rv)
         self._slot_of[chunk_key] = slot
 

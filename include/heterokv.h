@@ -54,6 +54,19 @@
  * [B][H][cap][128]; V is stored in 16-token transposed tiles
  * [B][H][cap/16][4 g][16 c][8 n][4 i] fp16 holding V[token 4g+i][dim c+16n].
  * Slots [0, len) of a zone are attended; their order does not matter.
+ *
+ * bfloat16 models.  Entry points that take model activations (zone writes, the
+ * decode query and output, the prefill query, chunk and output) accept bf16 as well
+ * as fp16.  Zones and MFMA operands stay fp16: a bf16 value converts to fp16
+ * exactly when its magnitude lies in [2^-14, 65504] (bf16 carries 8 significant
+ * bits, fp16 11), smaller magnitudes lose at most 2^-25 absolutely, and a finite
+ * value beyond the fp16 range becomes +-inf and sets HKV_ERR_BIT_RANGE in the
+ * call's error word.  Results are written in the requested output dtype.
+ *
+ * Device error words.  Kernels that can meet bad data report it by OR-ing bits
+ * into a caller-owned device int32 instead of faulting or failing silently; the
+ * caller reads it at a synchronization point it already has and clears it (the
+ * HKV_ERR_BIT_* values below).
  */
 #ifndef HETEROKV_H
 #define HETEROKV_H
@@ -65,7 +78,7 @@
 extern "C" {
 #endif
 
-#define HKV_ABI_VERSION 5
+#define HKV_ABI_VERSION 6
 
 /* dtype codes */
 #define HKV_DTYPE_F16  0
@@ -79,6 +92,17 @@ extern "C" {
 #define HKV_ERR_HIP         -2   /* a HIP runtime call failed */
 #define HKV_ERR_CAPACITY    -3   /* a caller buffer or pool is too small */
 #define HKV_ERR_UNSUPPORTED -4   /* shape the kernels do not handle (e.g. head_dim != 128) */
+#define HKV_ERR_DEVICE      -5   /* reserved for bindings: a device error word read non-zero */
+
+/* device error-word bits */
+#define HKV_ERR_BIT_BLOCK_ID  1   /* a block-table id outside the pool / staging records
+                                     (a valid record was read in its place) */
+#define HKV_ERR_BIT_SLOT      2   /* a token slot beyond its block-table row (nothing written) */
+#define HKV_ERR_BIT_PLACEMENT 4   /* decode: the ranges of one (sequence, kv head) ran on more
+                                     than one XCD while the launch relied on an XCD-local
+                                     hand-off; that launch's output is invalid.  Pass
+                                     HKV_DECODE_AGENT_HANDOFF from then on. */
+#define HKV_ERR_BIT_RANGE     8   /* a finite bf16 value beyond the fp16 range was narrowed */
 
 #define HKV_BLOCK_TOKENS 16
 #define HKV_MAX_F16_ZONES 3
@@ -174,14 +198,14 @@ int hkv_unpack_tokens(const uint8_t* pool, int64_t pool_blocks, const int32_t* b
                       uint8_t* codes, float* scales, uint8_t* zps, void* stream);
 
 /*
- * Write `num_tokens` fp16 tokens into an fp16 zone (sink / recent window /
+ * Write `num_tokens` fp16 or bf16 tokens into an fp16 zone (sink / recent window /
  * heavy hitters).  Token t of sequence b goes to slot slot_start[b] + t (or
  * slot_base + t when slot_start is NULL), taken modulo `ring` when ring > 0 (a
  * ring of that many slots, ring <= capacity).  K rows are copied; V goes to
  * transposed tiles.
  */
 typedef struct HkvZoneWriteArgs {
-    const uint16_t* k;
+    const uint16_t* k;             /* source tokens, dtype below */
     const uint16_t* v;
     int64_t src_stride_b, src_stride_h, src_stride_t;
     int32_t batch, num_kv_heads, head_dim, num_tokens;
@@ -191,6 +215,8 @@ typedef struct HkvZoneWriteArgs {
     uint16_t* zone_k;              /* [batch][H][capacity][128] */
     uint16_t* zone_v;              /* [batch][H][capacity/16][4096 B tiles] */
     int32_t slot_base;
+    int32_t dtype;                 /* source dtype: F16 or BF16 */
+    int32_t* err_flag;             /* optional device int: HKV_ERR_BIT_RANGE */
 } HkvZoneWriteArgs;
 
 int hkv_zone_write(const HkvZoneWriteArgs* args, void* stream);
@@ -223,7 +249,7 @@ int hkv_zone_copy(const uint16_t* src_k, const uint16_t* src_v, int32_t src_capa
  * receive the new lengths, as zone lengths for hkv_decode_attn.
  */
 typedef struct HkvZoneStepArgs {
-    const uint16_t* k;             /* new token [batch][num_kv_heads][1][128] fp16 */
+    const uint16_t* k;             /* new token [batch][num_kv_heads][1][128], dtype below */
     const uint16_t* v;
     int64_t src_stride_b, src_stride_h;
     int32_t batch, num_kv_heads, head_dim;
@@ -236,6 +262,8 @@ typedef struct HkvZoneStepArgs {
     int32_t* state;
     int32_t* tail_lens;
     int32_t* hh_lens;
+    int32_t dtype;                 /* F16 or BF16 */
+    int32_t* err_flag;             /* optional device int: HKV_ERR_BIT_RANGE */
 } HkvZoneStepArgs;
 
 int hkv_zone_step(const HkvZoneStepArgs* args, void* stream);
@@ -258,7 +286,7 @@ typedef struct HkvF16Zone {
 typedef struct HkvDecodeArgs {
     int32_t batch, num_q_heads, num_kv_heads, head_dim;
     float sm_scale;
-    const uint16_t* q;             /* fp16 [batch][num_q_heads][128] with strides below */
+    const uint16_t* q;             /* q_dtype [batch][num_q_heads][128] with strides below */
     int64_t q_stride_b, q_stride_h;
     int32_t num_f16_zones;
     HkvF16Zone f16[HKV_MAX_F16_ZONES];
@@ -268,9 +296,9 @@ typedef struct HkvDecodeArgs {
     int32_t bt_stride;
     const int32_t* int4_lens;      /* [batch] device; NULL -> int4_max_len */
     int32_t int4_max_len;
-    uint16_t* out;                 /* fp16 [batch][num_q_heads][128] */
+    uint16_t* out;                 /* out_dtype [batch][num_q_heads][128] */
     int64_t out_stride_b, out_stride_h;
-    void* workspace;               /* hkv_decode_workspace_bytes(); zero-filled once before first use */
+    void* workspace;               /* hkv_decode_workspace_bytes(), 256-byte aligned; see below */
     size_t workspace_bytes;
     int32_t splits_hint;           /* 0 = auto */
     const uint8_t* staging;        /* records addressed by negative block ids (may be NULL) */
@@ -285,6 +313,9 @@ typedef struct HkvDecodeArgs {
     float* scores;
     int64_t scores_stride_b, scores_stride_h;
     float* score_stats;
+    int32_t q_dtype;               /* F16 or BF16 */
+    int32_t out_dtype;             /* F16 or BF16 */
+    int32_t* err_flag;             /* device int for HKV_ERR_BIT_*; NULL: the workspace's first word */
 } HkvDecodeArgs;
 
 /* Decode flag: every wave of a range takes a fixed subset of the range's blocks, so
@@ -293,6 +324,18 @@ typedef struct HkvDecodeArgs {
  * on long contexts and large batches) and changes the summation order, so outputs
  * can differ in the last bits between runs. */
 #define HKV_DECODE_DETERMINISTIC 1
+/* Decode flag: combine the ranges of a (sequence, kv head) through device-coherent
+ * memory.  Without it, when (batch x kv heads) is a multiple of the XCD count, the
+ * combine stays in one XCD's L2, relying on the dispatcher placing workgroup ids of
+ * one residue modulo the XCD count on one XCD; every launch checks that with one
+ * device-scope atomic per workgroup and reports a violation as HKV_ERR_BIT_PLACEMENT. */
+#define HKV_DECODE_AGENT_HANDOFF 2
+
+/* Workspace rules.  The workspace must be zero-filled before its first use.  The
+ * kernels leave their tickets zero after every launch; when the geometry (batch x kv
+ * heads, q heads) differs from the previous launch that used the same workspace
+ * address, the library clears the ticket area itself (one small kernel on `stream`)
+ * before the launch.  Launches that share a workspace must be ordered on one stream. */
 
 size_t hkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                                   int32_t head_dim, int32_t int4_max_len,
@@ -306,7 +349,7 @@ int hkv_decode_attn(const HkvDecodeArgs* args, void* stream);
  * query row of q attends to all tokens of the fp16 zones and of the INT4 pool
  * (dequantized to fp16 exactly as KVCompressor.decompress) and, when chunk_k/chunk_v
  * are given, causally to the chunk's own tokens (row i sees chunk rows 0..i).
- * fp16 in, fp16 out, fp32 accumulation on MFMA.
+ * q, chunk and out are fp16 or bf16 (see "bfloat16 models"); fp32 accumulation on MFMA.
  */
 typedef struct HkvPrefillArgs {
     int32_t batch, num_q_heads, num_kv_heads, head_dim, num_queries;
@@ -326,9 +369,12 @@ typedef struct HkvPrefillArgs {
     int64_t chunk_stride_b, chunk_stride_h, chunk_stride_t;
     uint16_t* out;                 /* [batch][num_q_heads][num_queries][128] with strides */
     int64_t out_stride_b, out_stride_h, out_stride_t;
-    int32_t* err_flag;             /* optional: bit 0 set if a block id was out of range */
+    int32_t* err_flag;             /* optional: HKV_ERR_BIT_BLOCK_ID, HKV_ERR_BIT_RANGE */
     const uint8_t* staging;        /* records addressed by negative block ids (may be NULL) */
     int64_t staging_blocks;
+    int32_t q_dtype;               /* F16 or BF16 */
+    int32_t chunk_dtype;           /* F16 or BF16 */
+    int32_t out_dtype;             /* F16 or BF16 */
 } HkvPrefillArgs;
 
 int hkv_prefill_attn(const HkvPrefillArgs* args, void* stream);

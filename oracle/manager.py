@@ -21,6 +21,12 @@ so the build's manager can be checked index for index.  Followed line by line:
     _update_legacy_cache          :752-777 _key_cache = sink + tail + hh
     decompress_dram_chunks        :779-821 every "l{layer}_" chunk in dict (eviction) order
     count_dram_tokens             :1218-1229 #chunks(layer) * |first chunk|
+    decompress_dram_chunks_adaptive / get_dram_chunks_quantized_adaptive
+                                  :857-878,966-978 the layer's chunks in dict order, ranked
+                                           by chunk score descending (stable), the first w
+                                           kept, returned in eviction order
+    swap_in                       :265-278 the chunk leaves the DRAM table (its eviction-order
+                                           entry and score stay)
     _evict_to_dram                :1231-1299 key "l{layer}_e{counter}"; score 1/(counter+1)
                                            without oracle scores; counter += 1 only on layer 0
   src/memory/attention_competition_queue.py
@@ -143,6 +149,16 @@ class ManagerOracle:
             if k.startswith(pre):
                 out.extend(v)
         return out
+
+    def select_chunks(self, layer, window_size):
+        pre = "l%d_" % layer
+        keys = [k for k in self.dram if k.startswith(pre)]
+        ranked = sorted(keys, key=lambda k: self.chunk_scores.get(k, 0.0), reverse=True)
+        chosen = ranked[:window_size]
+        return sorted(chosen, key=lambda k: self.chunk_order.index(k))
+
+    def remove_chunk(self, key):
+        return self.dram.pop(key, None)
 
     def count_dram_tokens(self, layer=0):
         pre = "l%d_" % layer

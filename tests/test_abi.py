@@ -32,7 +32,7 @@ def test_header_symbols_exported(lib):
 
 
 def test_version_and_record_size(lib):
-    assert lib.hkv_abi_version() == 5
+    assert lib.hkv_abi_version() == 6
     assert lib.hkv_block_bytes(8, 128) == 17664
     assert lib.hkv_block_bytes(4, 128) == 8832
     assert lib.hkv_block_bytes(8, 64) == -1
@@ -111,9 +111,10 @@ def test_decode_argument_errors(lib):
 def test_workspace_size(lib):
     from heterokv import ops
     n = ops.decode_workspace_bytes(1, 32, 8, 28608, [64, 4096])
-    # header + agent tickets + one 256-byte XCD-local ticket per pair + partial states for
-    # up to 64 ranges per (sequence, kv head): 8 pairs x 64 ranges x 4 heads x 132 floats
-    assert n == 256 + 256 + 8 * 256 + 8 * 64 * 4 * 132 * 4
+    # header + agent tickets + XCD masks + one 256-byte XCD-local ticket per pair + partial
+    # states for up to 64 ranges per (sequence, kv head): 8 pairs x 64 ranges x 4 heads x
+    # 132 floats
+    assert n == 256 + 256 + 256 + 8 * 256 + 8 * 64 * 4 * 132 * 4
 
 
 def test_prefetcher_and_gather_argument_errors(lib):

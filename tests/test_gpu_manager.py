@@ -146,8 +146,11 @@ def test_cache_path_c_semantics_materialized_vs_fused():
     from heterokv.engine_wrapper import FusedHeteroCache
     L, B, H, HQ = 2, 1, 2, 8
     K, V = _kv(11, B, H, 400)
-    ref_cache = FusedHeteroCache(num_layers=L, sink_tokens=8, keep_tail=40, device=DEV, fused_decode=False)
-    fus_cache = FusedHeteroCache(num_layers=L, sink_tokens=8, keep_tail=40, device=DEV, fused_decode=True)
+    # the reference's length arithmetic, which the oracle restates
+    ref_cache = FusedHeteroCache(num_layers=L, sink_tokens=8, keep_tail=40, device=DEV, fused_decode=False,
+                                 reference_lengths=True)
+    fus_cache = FusedHeteroCache(num_layers=L, sink_tokens=8, keep_tail=40, device=DEV, fused_decode=True,
+                                 reference_lengths=True)
     orc = CacheOracle(L, sink_tokens=8, keep_tail=40)
     g = torch.Generator().manual_seed(12)
     pos = 0

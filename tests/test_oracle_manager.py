@@ -127,3 +127,24 @@ def test_max_hbm_tokens():
     assert ManagerOracle(1, 64, 8192).max_hbm_tokens() == 64 + 8192 + 4096
     assert ManagerOracle(1, 64, 4160).max_hbm_tokens() == 64 + 4160 + 2080
     assert ManagerOracle(1, 4, 8).max_hbm_tokens() == 4 + 8 + 2048
+
+
+def test_chunk_selection_and_removal_hand_traces():
+    """manager.py:966-978 and :265-278 on hand-built tables: default 1/(c+1) scores keep the
+    first w chunks; equal scores keep insertion order (stable sort); the result is in
+    eviction order; a removed chunk is no longer gathered or counted."""
+    m = ManagerOracle(1, sink_tokens=4, hbm_budget_tokens=8)
+    for c in range(4):
+        m._evict(0, list(range(10 * c, 10 * c + 5)))
+    assert m.select_chunks(0, 2) == ["l0_e0", "l0_e1"]
+    assert m.select_chunks(0, 10) == ["l0_e0", "l0_e1", "l0_e2", "l0_e3"]
+    assert m.select_chunks(0, 0) == []
+    m.chunk_scores.update({"l0_e0": 0.1, "l0_e1": 0.9, "l0_e2": 0.5, "l0_e3": 0.9})
+    # ranked: e1 (0.9), e3 (0.9, after e1 by insertion), e2, e0
+    assert m.select_chunks(0, 2) == ["l0_e1", "l0_e3"]
+    assert m.select_chunks(0, 3) == ["l0_e1", "l0_e2", "l0_e3"]
+    assert m.remove_chunk("l0_e1") == [10, 11, 12, 13, 14]
+    assert m.dram_positions(0) == [0, 1, 2, 3, 4, 20, 21, 22, 23, 24, 30, 31, 32, 33, 34]
+    assert m.count_dram_tokens(0) == 3 * 5
+    assert "l0_e1" in m.chunk_order and "l0_e1" in m.chunk_scores
+    assert m.select_chunks(0, 2) == ["l0_e2", "l0_e3"]
