@@ -1015,9 +1015,9 @@ extern "C" size_t hkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads,
     return workspace_bytes(batch, num_q_heads, num_kv_heads, kMaxSplits);
 }
 
-extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
-    clear_error();
-    HKV_REQUIRE(a != nullptr, HKV_ERR_ARG, "hkv_decode_attn: null args");
+// The launch behind both decode entry points: `wsp` / `ws_bytes` is the caller's
+// workspace (hkv_decode_attn) or this device's static scratch (hkv_decode_attn_noalloc).
+static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, void* stream) {
     HKV_REQUIRE(a->head_dim == kHeadDim, HKV_ERR_UNSUPPORTED, "hkv_decode_attn: head_dim %d != 128", a->head_dim);
     HKV_REQUIRE(a->batch > 0 && a->num_kv_heads > 0 && a->num_q_heads > 0, HKV_ERR_ARG,
                 "hkv_decode_attn: bad batch/heads");
@@ -1041,7 +1041,7 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
         HKV_REQUIRE(a->scores_stride_h >= row && a->scores_stride_b >= (int64_t)a->num_q_heads * a->scores_stride_h,
                     HKV_ERR_ARG, "hkv_decode_attn: score strides too small for %lld items per row", (long long)row);
     }
-    HKV_REQUIRE(a->q && a->out && a->workspace, HKV_ERR_ARG, "hkv_decode_attn: null q/out/workspace");
+    HKV_REQUIRE(a->q && a->out && wsp, HKV_ERR_ARG, "hkv_decode_attn: null q/out/workspace");
     HKV_REQUIRE((((uintptr_t)a->q) & 15) == 0 && (a->q_stride_b % 8) == 0 && (a->q_stride_h % 8) == 0,
                 HKV_ERR_ARG, "hkv_decode_attn: q must be 16-byte aligned with strides multiple of 8");
     HKV_REQUIRE(a->int4_max_len >= 0 && a->int4_max_len <= kMaxZoneTokens, HKV_ERR_ARG,
@@ -1077,9 +1077,8 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     HKV_REQUIRE(BH < 65536, HKV_ERR_ARG, "hkv_decode_attn: batch x kv heads too large");
     const int ms = choose_splits((int)BH, a->int4_max_len, zl, a->num_f16_zones, a->splits_hint);
     const size_t need = workspace_bytes(a->batch, a->num_q_heads, a->num_kv_heads, ms);
-    HKV_REQUIRE(a->workspace_bytes >= need, HKV_ERR_CAPACITY,
-                "hkv_decode_attn: workspace %zu bytes, need %zu", a->workspace_bytes, need);
-    HKV_REQUIRE((((uintptr_t)a->workspace) & 255) == 0, HKV_ERR_ARG, "hkv_decode_attn: workspace must be 256-byte aligned");
+    HKV_REQUIRE(ws_bytes >= need, HKV_ERR_CAPACITY, "hkv_decode_attn: workspace %zu bytes, need %zu", ws_bytes, need);
+    HKV_REQUIRE((((uintptr_t)wsp) & 255) == 0, HKV_ERR_ARG, "hkv_decode_attn: workspace must be 256-byte aligned");
 
     DecodeParams p;
     p.B = a->batch;
@@ -1112,7 +1111,7 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     p.out = a->out;
     p.o_sb = a->out_stride_b;
     p.o_sh = a->out_stride_h;
-    char* ws = (char*)a->workspace;
+    char* ws = (char*)wsp;
     p.err = a->err_flag ? (int*)a->err_flag : (int*)ws;
     p.counters = (int*)(ws + kWsHeader);
     p.owners = (unsigned*)(ws + kWsHeader + align256((size_t)BH * sizeof(int)));
@@ -1147,12 +1146,12 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
         HKV_HIP_CHECK(hipFuncSetAttribute(fns[var], hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
         raised[var] = true;
     }
-    if (ws_needs_clear(a->workspace, BH)) {
+    if (ws_needs_clear(wsp, BH)) {
         const int64_t words = (int64_t)(ticket_area_end((size_t)BH) - kWsHeader) / 4;
         hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024)),
                            dim3(256), 0, (hipStream_t)stream, (int*)(ws + kWsHeader), words);
         if (hipGetLastError() != hipSuccess) {
-            ws_forget(a->workspace);
+            ws_forget(wsp);
             HKV_REQUIRE(false, HKV_ERR_HIP, "hkv_decode_attn: launch of the ticket clear failed");
         }
     }
@@ -1165,4 +1164,44 @@ extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
     }
     HKV_LAUNCH_CHECK("decode_attn_kernel");
     return HKV_OK;
+}
+
+extern "C" int hkv_decode_attn(const HkvDecodeArgs* a, void* stream) {
+    clear_error();
+    HKV_REQUIRE(a != nullptr, HKV_ERR_ARG, "hkv_decode_attn: null args");
+    return decode_launch(a, a->workspace, a->workspace_bytes, stream);
+}
+
+// ---- allocation-free variant: the partial states, tickets and XCD masks live in a
+// file-scope device array instead of a caller workspace.  Each device holds its own
+// copy (resolved with hipGetSymbolAddress on the first call made with that device
+// current); the first launch on a device clears its ticket area, like a new workspace.
+static __device__ __align__(256) unsigned char scratch[HKV_DECODE_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+extern "C" int hkv_decode_attn_noalloc(const HkvDecodeArgs* a, void* stream) {
+    clear_error();
+    HKV_REQUIRE(a != nullptr, HKV_ERR_ARG, "hkv_decode_attn_noalloc: null args");
+    HKV_REQUIRE(a->workspace == nullptr && a->workspace_bytes == 0, HKV_ERR_ARG,
+                "hkv_decode_attn_noalloc: takes no workspace (pass NULL / 0)");
+    int dev = 0;
+    HKV_HIP_CHECK(hipGetDevice(&dev));
+    HKV_REQUIRE(dev >= 0 && dev < kMaxDevices, HKV_ERR_UNSUPPORTED, "hkv_decode_attn_noalloc: device %d", dev);
+    void* ptr = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (!g_scratch_ptr[dev]) {
+            void* p = nullptr;
+            HKV_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+            HKV_REQUIRE(p != nullptr, HKV_ERR_HIP, "hkv_decode_attn_noalloc: no scratch address on device %d", dev);
+            g_scratch_ptr[dev] = p;
+        }
+        ptr = g_scratch_ptr[dev];
+    }
+    return decode_launch(a, ptr, HKV_DECODE_SCRATCH_BYTES, stream);
 }

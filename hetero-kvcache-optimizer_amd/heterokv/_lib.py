@@ -18,6 +18,7 @@ DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_U8 = 0, 1, 2, 3
 MAX_F16_ZONES = 3
 DECODE_DETERMINISTIC = 1   # HKV_DECODE_DETERMINISTIC
 DECODE_AGENT_HANDOFF = 2   # HKV_DECODE_AGENT_HANDOFF
+DECODE_SCRATCH_BYTES = 8 << 20   # HKV_DECODE_SCRATCH_BYTES (hkv_decode_attn_noalloc)
 BLOCK_TOKENS = 16
 HEAD_DIM = 128
 
@@ -150,6 +151,7 @@ SYMBOLS = [
     ("hkv_zone_step", ctypes.c_int, [ctypes.POINTER(ZoneStepArgs), vp]),
     ("hkv_decode_workspace_bytes", ctypes.c_size_t, [i32, i32, i32, i32, i32, vp, i32]),
     ("hkv_decode_attn", ctypes.c_int, [ctypes.POINTER(DecodeArgs), vp]),
+    ("hkv_decode_attn_noalloc", ctypes.c_int, [ctypes.POINTER(DecodeArgs), vp]),
     ("hkv_prefill_attn", ctypes.c_int, [ctypes.POINTER(PrefillArgs), vp]),
     ("hkv_pf_create", ctypes.c_int, [i32, ctypes.c_size_t, i32, ctypes.POINTER(vp)]),
     ("hkv_pf_destroy", ctypes.c_int, [vp]),

@@ -382,12 +382,16 @@ def _int4_source(pool, staging):
 
 def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
                      sm_scale=None, workspace=None, out=None, splits=0, staging=None, deterministic=False,
-                     scores=None, score_stats=None, err=None, out_dtype=None):
+                     scores=None, score_stats=None, err=None, out_dtype=None, noalloc=False,
+                     agent_handoff=False):
     """Split-K decode attention over fp16 zones and the INT4 pool.
 
     q: [B, Hq, 128] or [B, Hq, 1, 128] fp16 or bf16 (bf16 is range-checked into the error
     word).  out_dtype: fp16 or bf16 (default: q's dtype).  err: ErrorWord for
     HKV_ERR_BIT_* (default: the workspace's first word).
+    noalloc: launch through hkv_decode_attn_noalloc, which takes no workspace (its scratch
+    is a static device array of HKV_DECODE_SCRATCH_BYTES shared by every such call on
+    the GPU) and allocates nothing; agent_handoff then selects the device-scope combine.
     zones: sequence of (F16Zone, lens int32 [B] or None, max_len).
     pool / block_table [B, nblk] / int4_lens [B] / int4_max_len: the INT4 zone.
     staging: Int4Pool whose record i a block-table entry ~i (negative) names.
@@ -463,14 +467,18 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
             a.int4_lens = il.data_ptr()
     a.int4_max_len = int(int4_max_len)
     a.out, a.out_stride_b, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
-    nbytes = decode_workspace_bytes(B, Hq, Hkv, int(int4_max_len), zl)
-    if workspace is None:
-        workspace = DecodeWorkspace(dev)
-    ws = workspace.get(nbytes)
-    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     a.splits_hint = int(splits)
+    if noalloc:
+        a.workspace, a.workspace_bytes = None, 0
+    else:
+        nbytes = decode_workspace_bytes(B, Hq, Hkv, int(int4_max_len), zl)
+        if workspace is None:
+            workspace = DecodeWorkspace(dev)
+        ws = workspace.get(nbytes)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        agent_handoff = agent_handoff or workspace.agent_handoff
     a.flags = (_lib.DECODE_DETERMINISTIC if deterministic else 0) | \
-        (_lib.DECODE_AGENT_HANDOFF if workspace.agent_handoff else 0)
+        (_lib.DECODE_AGENT_HANDOFF if agent_handoff else 0)
     if scores is not None:
         _require_gpu(scores, score_stats)
         if score_stats is None or scores.dtype != torch.float32 or score_stats.dtype != torch.float32:
@@ -481,7 +489,10 @@ def decode_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, i
                                     "score_stats [B, Hq, 2] expected")
         a.scores, a.scores_stride_b, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
         a.score_stats = score_stats.data_ptr()
-    check(load().hkv_decode_attn(ctypes.byref(a), stream_ptr(dev)), "hkv_decode_attn")
+    if noalloc:
+        check(load().hkv_decode_attn_noalloc(ctypes.byref(a), stream_ptr(dev)), "hkv_decode_attn_noalloc")
+    else:
+        check(load().hkv_decode_attn(ctypes.byref(a), stream_ptr(dev)), "hkv_decode_attn")
     return out.unsqueeze(2) if squeeze else out
 
 

@@ -344,6 +344,19 @@ size_t hkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t nu
 int hkv_decode_attn(const HkvDecodeArgs* args, void* stream);
 
 /*
+ * hkv_decode_attn without a workspace: no counterpart in the reference.  It is for
+ * callers that cannot allocate device memory -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  args->workspace must be NULL and
+ * workspace_bytes 0; the partial states and tickets live in a library-owned static
+ * device array of HKV_DECODE_SCRATCH_BYTES per GPU (held until the process ends), and
+ * a geometry whose hkv_decode_workspace_bytes-style need exceeds it fails with
+ * HKV_ERR_CAPACITY.  Every call on one GPU shares that array: calls that overlap on one
+ * GPU (two streams, two threads) race.  Pass err_flag to see HKV_ERR_BIT_* reports.
+ */
+#define HKV_DECODE_SCRATCH_BYTES (8u << 20)
+int hkv_decode_attn_noalloc(const HkvDecodeArgs* args, void* stream);
+
+/*
  * Chunked-prefill attention (fused_dequant_attn_forward with GQA, kernels/
  * fused_dequant_attn.py:371-435; numerics fused_dequant_attn.py:242-247): every
  * query row of q attends to all tokens of the fp16 zones and of the INT4 pool
