@@ -1,24 +1,31 @@
-"""INT4-KV decode-attention benchmark on one MI355X.
+"""INT4-KV hot-path benchmark on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--legs c1,c3,c4,c5] [--workload ...]
 
-Workload (one step = one launch of the split-K decode kernel over one batch):
-single-layer decode attention, batch 1, 32 query heads / 8 kv heads (GQA),
-head_dim 128, context 32768 = 64 fp16 sink tokens + 28608 INT4 tokens (16-token
-blocks) + 4096 fp16 recent tokens; q ~ N(0,1)/sqrt(128) fp16; K, V ~ N(0,1) fp16
-with K channels 7/31/64/100 scaled x8; seeded, synthetic.  Eight copies of the
-KV are rotated (8 x 48.6 MB > the 256 MB Infinity Cache) so reads come from HBM.
-Launches are replayed from a HIP graph.
+Headline (`value`): single-layer decode attention, batch 1, 32 query heads / 8 kv heads
+(GQA), head_dim 128, context 32768 = 64 fp16 sink tokens + 28608 INT4 tokens (16-token
+blocks) + 4096 fp16 recent tokens; q ~ N(0,1)/sqrt(128) fp16; K, V ~ N(0,1) fp16 with K
+channels 7/31/64/100 scaled x8; seeded, synthetic.  One step = one launch of the split-K
+decode kernel; eight copies of the KV are rotated (8 x 48.6 MB > the 256 MB Infinity
+Cache) and the K timed launches are replayed from a HIP graph.  value = algorithmic bytes
+x K / elapsed (GB/s).
 
-Prints one JSON line: value = algorithmic bytes per step x steps / elapsed (GB/s),
-a roofline object for the decode kernel (achieved GB/s vs the 8 TB/s HBM peak,
-kernel time from HIP events on the launch stream) and a cpu_baseline object (the
-oracle's dequantize-then-attend restatement timed on the host cores).
+The same JSON line carries one block per other configuration (each with its own roofline,
+CPU baseline and parity figure; their step counts are fixed, not --steps):
+  c1_quant      quantize+pack of K, V [1, 8, 4096, 128] fp16 and the round trip to fp16
+  c3_paged      batch-16 paged decode, contexts 8K-32K, random-permutation block table
+  c4_prefill    2048-query chunked prefill over 64 + 131072 INT4 + 4096 tokens (MFMA bound)
+  offload_128k  end-to-end 28-layer bf16 decode at 131072 tokens with 75% of the INT4 KV
+                in pinned host memory: full and windowed retrieval tok/s, prefetch stall
+CPU baselines are the reference's path restated in float32 torch (oracle/torch_ref.py) on
+the host cores (threads: the affinity mask capped by OMP_NUM_THREADS), on bounded samples
+that each block names.
 """
 import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -76,120 +83,196 @@ def read_traffic():
     return None
 
 
-def cpu_baseline(q, K, V, budget_s=10.0):
-    """The oracle's dequantize-then-attend (Path C semantics) on the host cores."""
-    import numpy as np
-    from oracle import attention as oa
-    from oracle import compressor as oc
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:
-        threads = 1
-    kn, vn = K[0].numpy(), V[0].numpy()
-    kc, ks, kz = oc.compress(kn[:, SINK:SINK + MID], 128)
-    vc, vs, vz = oc.compress(vn[:, SINK:SINK + MID], 128)
-    qn = q[0].double().numpy()[:, None]
-    hbm_k = np.concatenate([kn[:, :SINK], kn[:, SINK + MID:]], axis=1).astype(np.float64)
-    hbm_v = np.concatenate([vn[:, :SINK], vn[:, SINK + MID:]], axis=1).astype(np.float64)
+def cpu_threads(torch):
+    """Host threads for the CPU baselines: the affinity mask, capped by OMP_NUM_THREADS
+    (the box's CPU share), set on torch; returned as the `cores` figure."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    torch.set_num_threads(n)
+    return n
+
+
+def time_cpu(fn, budget_s, max_reps=50):
+    """One warmup call, then calls until `budget_s` is spent; median seconds per call."""
+    out = fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while True:
+        t0 = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() >= t_end or len(times) >= max_reps:
+            break
+    return statistics.median(times), len(times), out
+
+
+def cpu_baseline_c2(torch, q, K, V, budget_s):
+    """The reference's decode step on the host cores in float32 torch (oracle/torch_ref.py):
+    Path C dequantizes the 28608 INT4 tokens of the 8 kv heads to fp16 and concatenates them
+    before the sink and recent tokens (manager.py:779-821), then softmax(q K^T / sqrt(d)) V
+    with GQA (fused_dequant_attn.py:242-247)."""
+    from oracle import torch_ref as tr
+    n = cpu_threads(torch)
+    kc, ks, kz = tr.compress(K[0, :, SINK:SINK + MID], 128)
+    vc, vs, vz = tr.compress(V[0, :, SINK:SINK + MID], 128)
+    zk = [K[0, :, :SINK], K[0, :, SINK + MID:]]
+    zv = [V[0, :, :SINK], V[0, :, SINK + MID:]]
+    q3 = q[0][:, None].float()
 
     def step():
-        kd = oa.dequant_rows(kc, ks.reshape(HKV, MID), kz.reshape(HKV, MID))
-        vd = oa.dequant_rows(vc, vs.reshape(HKV, MID), vz.reshape(HKV, MID))
-        return oa.attend(qn, np.concatenate([kd, hbm_k], 1), np.concatenate([vd, hbm_v], 1))
+        return tr.attend(q3, tr.path_c_keys(kc, ks, kz, zk), tr.path_c_keys(vc, vs, vz, zv))
 
-    out = step()  # warmup
-    n, t0 = 0, time.perf_counter()
-    while True:
-        out = step()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 50:
-            break
-    return out, dict(value=STEP_BYTES * n / el / 1e9, unit="GB/s", cores=threads, kind="port",
-                     sample="%d full C2 decode steps (dequant INT4 -> fp16 -> float64 attention) in %.1f s"
-                            % (n, el))
+    t, reps, out = time_cpu(step, budget_s)
+    return out[:, 0], dict(value=STEP_BYTES / t / 1e9, unit="GB/s", cores=n, kind="port",
+                           sample="%d full C2 decode steps (float32 torch: Path C dequant of 28608 INT4 tokens "
+                                  "to fp16 + attention), median %.1f ms" % (reps, t * 1e3))
 
 
+def read_profile(name, key):
+    """A "key: value" figure from a committed rocprofv3 summary under profiles/, or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            for ln in f:
+                if ln.startswith(key + ":"):
+                    return float(ln.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def event_time_ms(torch, fn, n, stream=None):
+    """Average ms per call of fn over n calls, HIP events on the launch stream."""
+    stream = stream or torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(n):
+        fn(i)
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+def graph_time_ms(torch, launch, n, warmup, dev):
+    """Average ms per launch of n launches replayed from one captured HIP graph (launch(i)
+    enqueues one kernel), HIP events on the graph's stream."""
+    stream = torch.cuda.Stream(device=dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(n):
+            launch(i)
+    for _ in range(max(warmup, 1)):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+    e1.synchronize()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+# ------------------------------------------------------------------------------ C4 prefill
 P_SQ, P_SINK, P_MID, P_RECENT = 2048, 64, 131072, 4096
+P_HIST = P_SINK + P_MID + P_RECENT
 # 4*Hq*D per (query, visible key): history fully visible, the chunk causally
-P_FLOPS = 4 * HQ * D * P_SQ * (P_SINK + P_MID + P_RECENT) + 4 * HQ * D * (P_SQ * (P_SQ + 1) // 2)
+P_FLOPS = 4 * HQ * D * P_SQ * P_HIST + 4 * HQ * D * (P_SQ * (P_SQ + 1) // 2)
 MFMA_PEAK_TFLOPS = 2500.0
+P_ROWS = list(range(0, 32)) + list(range(P_SQ - 32, P_SQ))   # CPU sample / parity rows
 
 
-def bench_prefill(torch, ops, args):
-    """One step = one hkv_prefill_attn launch: 2048 fp16 queries (32 q / 8 kv heads) against
-    64 fp16 sink + 131072 INT4 + 4096 fp16 recent tokens plus the chunk itself (causal)."""
+def leg_c4(torch, ops, args):
+    """Chunked prefill (one hkv_prefill_attn launch): 2048 fp16 queries, 32 q / 8 kv heads, over
+    64 fp16 sink + 131072 INT4 + 4096 fp16 recent tokens plus the chunk itself, causally."""
+    from oracle import torch_ref as tr
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(4)
-    hist = P_SINK + P_MID + P_RECENT
-    K = torch.randn((1, HKV, hist, D), generator=g, device=dev)
+    g = torch.Generator().manual_seed(4)
+    K = torch.randn((HKV, P_HIST, D), generator=g)
     K[..., OUTLIERS] *= 8
     K = K.half()
-    V = torch.randn((1, HKV, hist, D), generator=g, device=dev).half()
-    CK = torch.randn((1, HKV, P_SQ, D), generator=g, device=dev).half()
-    CV = torch.randn((1, HKV, P_SQ, D), generator=g, device=dev).half()
-    q = (torch.randn((1, HQ, P_SQ, D), generator=g, device=dev) / math.sqrt(D)).half()
+    V = torch.randn((HKV, P_HIST, D), generator=g).half()
+    CK = torch.randn((HKV, P_SQ, D), generator=g).half()
+    CV = torch.randn((HKV, P_SQ, D), generator=g).half()
+    q = (torch.randn((HQ, P_SQ, D), generator=g) / math.sqrt(D)).half()
     sink = ops.F16Zone(1, HKV, P_SINK, dev)
-    sink.write(K[:, :, :P_SINK], V[:, :, :P_SINK], [0])
+    sink.write(K[None, :, :P_SINK].to(dev), V[None, :, :P_SINK].to(dev), 0)
     rec = ops.F16Zone(1, HKV, P_RECENT, dev)
-    rec.write(K[:, :, P_SINK + P_MID:], V[:, :, P_SINK + P_MID:], [0])
+    rec.write(K[None, :, P_SINK + P_MID:].to(dev), V[None, :, P_SINK + P_MID:].to(dev), 0)
     nb = P_MID // 16
     pool = ops.Int4Pool(nb, HKV, dev)
     bt = torch.arange(nb, dtype=torch.int32, device=dev)[None]
-    ops.pack_tokens(pool, K[:, :, P_SINK:P_SINK + P_MID], V[:, :, P_SINK:P_SINK + P_MID],
+    ops.pack_tokens(pool, K[None, :, P_SINK:P_SINK + P_MID].to(dev), V[None, :, P_SINK:P_SINK + P_MID].to(dev),
                     torch.zeros(1, dtype=torch.int32, device=dev), bt)
-    del K, V
+    qd, ckd, cvd = q[None].to(dev), CK[None].to(dev), CV[None].to(dev)
     out = torch.empty((1, HQ, P_SQ, D), dtype=torch.float16, device=dev)
     zones = [(sink, None, P_SINK), (rec, None, P_RECENT)]
 
-    def launch():
-        ops.prefill_attention(q, zones=zones, pool=pool, block_table=bt, int4_max_len=P_MID,
-                              chunk_k=CK, chunk_v=CV, out=out)
+    def launch(i):
+        ops.prefill_attention(qd, zones=zones, pool=pool, block_table=bt, int4_max_len=P_MID,
+                              chunk_k=ckd, chunk_v=cvd, out=out)
 
-    for _ in range(max(args.warmup, 1)):
-        launch()
+    for i in range(3):
+        launch(i)
     torch.cuda.synchronize()
     pool.check_errors()
-    stream = torch.cuda.current_stream(dev)
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for _ in range(args.steps):
-        launch()
-    ev1.record(stream)
-    ev1.synchronize()
-    ms = ev0.elapsed_time(ev1) / args.steps
+    ms = event_time_ms(torch, launch, 10)
     tflops = P_FLOPS / (ms * 1e-3) / 1e12
-    line = {
-        "metric": "INT4-KV chunked-prefill attention TFLOP/s (MFMA roofline fraction)",
-        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp16", "data": "synthetic (seeded N(0,1) K/V, x8 K outlier channels)",
-        "config": {"workload": "chunked prefill: 2048 fp16 queries, 32 q / 8 kv heads, head_dim 128, over "
-                               "64 fp16 sink + 131072 INT4 + 4096 fp16 recent + causal chunk",
-                   "flops_per_step": P_FLOPS},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None},
-        "cpu_baseline": None,
-    }
-    print(json.dumps(line), flush=True)
+    got = out[0][:, P_ROWS].float().cpu()
+    blk = {"workload": "chunked prefill: 2048 fp16 queries, 32 q / 8 kv heads, head_dim 128, over 64 fp16 sink "
+                       "+ 131072 INT4 + 4096 fp16 recent + the chunk causally (one launch)",
+           "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "steps": 10,
+           "flops_per_step": P_FLOPS,
+           "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                        "mfma_busy_frac": read_profile("prefill_attn_c4_mfma_busy.txt", "mfma_busy_fraction")}}
+    del pool, sink, rec, qd, ckd, cvd
+    if args.no_cpu_baseline:
+        return blk
+    n = cpu_threads(torch)
+    kc, ks, kz = tr.compress(K[:, P_SINK:P_SINK + P_MID], 128)
+    vc, vs, vz = tr.compress(V[:, P_SINK:P_SINK + P_MID], 128)
+    zk = [K[:, :P_SINK], K[:, P_SINK + P_MID:], CK]
+    zv = [V[:, :P_SINK], V[:, P_SINK + P_MID:], CV]
+
+    rows = torch.tensor(P_ROWS)
+    qr = q[:, rows]
+
+    def step():
+        keys = tr.path_c_keys(kc, ks, kz, zk)
+        vals = tr.path_c_keys(vc, vs, vz, zv)
+        return tr.attend(qr, keys, vals, causal_from=P_HIST, rows=rows)
+
+    t, reps, ref = time_cpu(step, args.cpu_budget, max_reps=5)
+    flops = sum(4 * HQ * D * (P_HIST + r + 1) for r in P_ROWS)
+    blk["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": n, "kind": "port",
+                           "sample": "Path C dequant of the 131072 INT4 tokens to fp16 plus float32 attention "
+                                     "of 64 query rows (0-31, 2016-2047) x 32 heads, %d rep(s), median %.2f s"
+                                     % (reps, t)}
+    blk["parity"] = {"rows_checked": len(P_ROWS) * HQ,
+                     "max_abs_err_vs_cpu": round(float((got - ref).abs().max()), 6), "tolerance": 2e-3}
+    return blk
 
 
-def bench_paged(torch, ops, args):
+# ------------------------------------------------------------------------------ C3 paged decode
+C3_B, C3_SAMPLE = 16, 2
+
+
+def leg_c3(torch, ops, args):
     """Batched paged decode: 16 sequences, contexts uniform in [8192, 32768] (seeded), 32 q / 8 kv
-    heads, each context = 64 fp16 sink + INT4 middle + 4096 fp16 recent; the INT4 middle lives in
-    16-token blocks of one pool addressed through a seeded random-permutation block table."""
+    heads, each context = 64 fp16 sink + INT4 middle + 4096 fp16 recent; the INT4 middle lives
+    in 16-token blocks of one pool addressed through a seeded random-permutation block table."""
+    from oracle import torch_ref as tr
     dev = torch.device("cuda:0")
-    Bp = 16
     gen = torch.Generator().manual_seed(7)
-    ctx = torch.randint(8192, 32769, (Bp,), generator=gen)
+    ctx = torch.randint(8192, 32769, (C3_B,), generator=gen)
     mids = (ctx - SINK - RECENT).tolist()
     nbs = [(m + 15) // 16 for m in mids]
-    nbmax = max(nbs)
-    total = sum(nbs)
+    nbmax, total = max(nbs), sum(nbs)
     perm = torch.randperm(total, generator=gen).to(torch.int32)
-    bt = torch.zeros((Bp, nbmax), dtype=torch.int32)
+    bt = torch.zeros((C3_B, nbmax), dtype=torch.int32)
     off = 0
     for b, nb in enumerate(nbs):
         bt[b, :nb] = perm[off:off + nb]
@@ -197,74 +280,115 @@ def bench_paged(torch, ops, args):
     g = torch.Generator(device=dev).manual_seed(8)
     pool = ops.Int4Pool(total, HKV, dev)
     bt_d = bt.to(dev)
-    for b in range(Bp):
-        K = torch.randn((1, HKV, mids[b], D), generator=g, device=dev)
-        K[..., OUTLIERS] *= 8
-        V = torch.randn((1, HKV, mids[b], D), generator=g, device=dev)
-        ops.pack_tokens(pool, K.half(), V.half(), torch.zeros(1, dtype=torch.int32, device=dev), bt_d[b:b + 1])
+    keep = []
+    for b in range(C3_B):
+        Kb = torch.randn((1, HKV, mids[b], D), generator=g, device=dev)
+        Kb[..., OUTLIERS] *= 8
+        Kb = Kb.half()
+        Vb = torch.randn((1, HKV, mids[b], D), generator=g, device=dev).half()
+        ops.pack_tokens(pool, Kb, Vb, torch.zeros(1, dtype=torch.int32, device=dev), bt_d[b:b + 1])
+        if b < C3_SAMPLE:
+            keep.append((Kb[0].cpu(), Vb[0].cpu()))
     pool.check_errors()
-    sink = ops.F16Zone(Bp, HKV, SINK, dev)
-    rec = ops.F16Zone(Bp, HKV, RECENT, dev)
-    sink.write(torch.randn((Bp, HKV, SINK, D), generator=g, device=dev).half(),
-               torch.randn((Bp, HKV, SINK, D), generator=g, device=dev).half(), 0)
-    rec.write(torch.randn((Bp, HKV, RECENT, D), generator=g, device=dev).half(),
-              torch.randn((Bp, HKV, RECENT, D), generator=g, device=dev).half(), 0)
-    q = (torch.randn((Bp, HQ, D), generator=g, device=dev) / math.sqrt(D)).half()
+    sk = torch.randn((C3_B, HKV, SINK, D), generator=g, device=dev).half()
+    sv = torch.randn((C3_B, HKV, SINK, D), generator=g, device=dev).half()
+    rk = torch.randn((C3_B, HKV, RECENT, D), generator=g, device=dev).half()
+    rv = torch.randn((C3_B, HKV, RECENT, D), generator=g, device=dev).half()
+    sink = ops.F16Zone(C3_B, HKV, SINK, dev)
+    rec = ops.F16Zone(C3_B, HKV, RECENT, dev)
+    sink.write(sk, sv, 0)
+    rec.write(rk, rv, 0)
+    q = (torch.randn((C3_B, HQ, D), generator=g, device=dev) / math.sqrt(D)).half()
     lens = torch.tensor(mids, dtype=torch.int32, device=dev)
-    out = torch.empty((Bp, HQ, D), dtype=torch.float16, device=dev)
+    out = torch.empty((C3_B, HQ, D), dtype=torch.float16, device=dev)
     ws = ops.DecodeWorkspace(dev)
+    err = ops.ErrorWord(dev)
 
-    def launch():
+    def launch(i):
         ops.decode_attention(q, zones=[(sink, None, SINK), (rec, None, RECENT)], pool=pool, block_table=bt_d,
-                             int4_lens=lens, int4_max_len=max(mids), workspace=ws, out=out,
-                             deterministic=args.deterministic)
+                             int4_lens=lens, int4_max_len=max(mids), workspace=ws, out=out, err=err)
 
-    for _ in range(max(args.warmup, 1)):
-        launch()
+    for i in range(3):
+        launch(i)
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for _ in range(args.steps):
-        launch()
-    ev1.record(stream)
-    ev1.synchronize()
-    if ws.error_flag():
-        raise RuntimeError("decode kernel reported an out-of-range block id")
-    ms = ev0.elapsed_time(ev1) / args.steps
-    step_bytes = sum(2 * HKV * (m * (D // 2 + 5) + (SINK + RECENT) * D * 2) for m in mids) + 2 * Bp * HQ * D * 2
+    ms = graph_time_ms(torch, launch, 40, 2, dev)
+    err.check()
+    step_bytes = sum(2 * HKV * (m * (D // 2 + 5) + (SINK + RECENT) * D * 2) for m in mids) + \
+        2 * C3_B * HQ * D * 2 + 4 * total
     gbs = step_bytes / (ms * 1e-3) / 1e9
-    line = {
-        "metric": "INT4-KV batched paged decode-attn GB/s (HBM roofline fraction)",
-        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp16", "data": "synthetic (seeded N(0,1) K/V, x8 K outlier channels)",
-        "config": {"workload": "batched paged decode: batch 16, contexts uniform in [8192, 32768] (64 fp16 sink + "
-                               "INT4 middle + 4096 fp16 recent), 32 q / 8 kv heads, head_dim 128, INT4 blocks via "
-                               "a random-permutation block table; %d pool blocks; one pool (fits the 256 MB "
-                               "Infinity Cache only partly)" % total,
-                   "contexts": ctx.tolist(), "bytes_per_step": step_bytes,
-                   "schedule": "fixed (deterministic)" if args.deterministic else "on demand"},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
-        "cpu_baseline": None,
-    }
-    print(json.dumps(line), flush=True)
+    traffic = read_profile("decode_attn_c3_traffic.txt", "traffic_bytes_per_launch")
+    launch(0)
+    got = out[:C3_SAMPLE].float().cpu()
+    blk = {"workload": "batched paged decode: batch 16, contexts uniform in [8192, 32768] (64 fp16 sink + INT4 "
+                       "middle + 4096 fp16 recent), 32 q / 8 kv heads, head_dim 128, INT4 blocks through a "
+                       "random-permutation block table (%d blocks, one pool)" % total,
+           "contexts": ctx.tolist(), "bytes_per_step": step_bytes,
+           "value": round(gbs, 2), "unit": "GB/s", "ms_per_step": round(ms, 6), "steps": 40, "launch": "hip graph",
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic}}
+    if args.no_cpu_baseline:
+        return blk
+    n = cpu_threads(torch)
+    # the sampled sequences' INT4 data as the reference keeps it (codes per token row), in
+    # 16-token blocks of a host pool at the same random-permutation positions
+    cpu_pool_k = torch.zeros((total, HKV, 16, D), dtype=torch.uint8)
+    cpu_pool_v = torch.zeros_like(cpu_pool_k)
+    meta = torch.zeros((total, 4, HKV, 16), dtype=torch.float32)
+    for b, (Kb, Vb) in enumerate(keep):
+        nb, m = nbs[b], mids[b]
+        ids = bt[b, :nb].long()
+        for pool_c, X, mi in ((cpu_pool_k, Kb, 0), (cpu_pool_v, Vb, 2)):
+            c, s_, z = tr.compress(X, 128)
+            cp = torch.zeros((HKV, nb * 16, D), dtype=torch.uint8)
+            cp[:, :m] = c
+            pool_c[ids] = cp.view(HKV, nb, 16, D).transpose(0, 1)
+            sp = torch.zeros((HKV, nb * 16))
+            zp = torch.zeros((HKV, nb * 16))
+            sp[:, :m] = s_.view(HKV, m)
+            zp[:, :m] = z.view(HKV, m).float()
+            meta[ids, mi] = sp.view(HKV, nb, 16).transpose(0, 1)
+            meta[ids, mi + 1] = zp.view(HKV, nb, 16).transpose(0, 1)
+    skc, svc, rkc, rvc, qc = sk[:C3_SAMPLE].cpu(), sv[:C3_SAMPLE].cpu(), rk[:C3_SAMPLE].cpu(), rv[:C3_SAMPLE].cpu(), \
+        q[:C3_SAMPLE].cpu()
+
+    def one(b, pool_c, mi, zones):
+        nb, m = nbs[b], mids[b]
+        ids = bt[b, :nb].long()
+        codes = pool_c.index_select(0, ids).transpose(0, 1).reshape(HKV, nb * 16, D)[:, :m]
+        md = meta.index_select(0, ids)[:, mi:mi + 2].permute(1, 2, 0, 3).reshape(2, HKV, nb * 16)[:, :, :m]
+        return tr.path_c_keys(codes, md[0].reshape(-1).contiguous(), md[1].reshape(-1).to(torch.uint8), zones)
+
+    def step():
+        outs = []
+        for b in range(C3_SAMPLE):
+            keys = one(b, cpu_pool_k, 0, [skc[b], rkc[b]])
+            vals = one(b, cpu_pool_v, 2, [svc[b], rvc[b]])
+            outs.append(tr.attend(qc[b][:, None].float(), keys, vals)[:, 0])
+        return torch.stack(outs)
+
+    t, reps, ref = time_cpu(step, args.cpu_budget)
+    sb = sum(2 * HKV * (mids[b] * (D // 2 + 5) + (SINK + RECENT) * D * 2) + 2 * HQ * D * 2 for b in range(C3_SAMPLE))
+    blk["cpu_baseline"] = {"value": round(sb / t / 1e9, 4), "unit": "GB/s", "cores": n, "kind": "port",
+                           "sample": "sequences 0-%d of the batch (contexts %s): block-table gather of the INT4 "
+                                     "rows, Path C dequant to fp16, float32 attention; %d rep(s), median %.1f ms"
+                                     % (C3_SAMPLE - 1, ctx[:C3_SAMPLE].tolist(), reps, t * 1e3)}
+    blk["parity"] = {"sequences_checked": C3_SAMPLE,
+                     "max_abs_err_vs_cpu": round(float((got - ref).abs().max()), 6), "tolerance": 2e-3}
+    return blk
 
 
+# ------------------------------------------------------------------------------ C1 quantize+pack
 C1_BYTES = 2 * 8 * 4096 * 128 * 2 + 2 * (8 * 4096 * 64 + 8 * 4096 * 4 + 8 * 4096)   # 21,299,200
 
 
-def bench_quant(torch, ops, args):
-    """Quantize+pack round trip on K, V [1, 8, 4096, 128] fp16 (group 128 = one token row,
-    4 outlier K channels x8): hkv_pack_tokens writes the INT4 block records (codes packed two
-    per byte, fp32 scale and u8 zero point per row); back to fp16 through the Path C route
-    (hkv_unpack_tokens + hkv_dequantize_groups).  Both read or write 21,299,200 algorithmic
-    bytes per K+V call; 16 rotated copies keep the inputs out of the 256 MB Infinity Cache."""
+def leg_c1(torch, ops, args):
+    """Quantize+pack K, V [1, 8, 4096, 128] fp16 (group 128 = one token row, 4 outlier K channels
+    x8): hkv_pack_tokens writes the INT4 block records; back to fp16 by the Path C route
+    (hkv_unpack_tokens + hkv_dequantize_groups).  21,299,200 algorithmic bytes per K+V call;
+    16 rotated copies keep the inputs out of the 256 MB Infinity Cache."""
     from heterokv.kv_compressor import KVCompressor
+    from oracle import torch_ref as tr
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     g = torch.Generator().manual_seed(0)
     K = torch.randn((1, 8, 4096, 128), generator=g)
     K[..., OUTLIERS] *= 8
@@ -282,74 +406,48 @@ def bench_quant(torch, ops, args):
 
     def roundtrip(i):
         for which in (0, 1):
-            c, s, z = ops.unpack_tokens(pools[i % R], bt[0], 4096, which)
-            ops.dequantize_groups(c, s, z)
+            c, s_, z = ops.unpack_tokens(pools[i % R], bt[0], 4096, which)
+            ops.dequantize_groups(c, s_, z)
 
-    def timed(fn, n):
-        for i in range(max(args.warmup, 2 * R)):
-            fn(i)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(n):
-            fn(i)
-        e1.record()
-        e1.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / n
-
-    n = max(args.steps, 64)
-    us_q = timed(quant, n)
-    us_rt = timed(roundtrip, max(n // 4, 16))
+    for i in range(2 * R):
+        quant(i)
+        roundtrip(i)
+    torch.cuda.synchronize()
+    us_q = graph_time_ms(torch, quant, 64, 2, dev) * 1e3
+    us_rt = event_time_ms(torch, roundtrip, 64) * 1e3
     for p_ in pools:
         p_.check_errors()
     comp = KVCompressor(group_size=128, bits=4)
-    rel = {}
-    got = {}
+    rel, got = {}, {}
     for which, name, x in ((0, "k", K16), (1, "v", V16)):
-        c, s, z = ops.unpack_tokens(pools[0], bt[0], 4096, which)
-        got[name] = (c.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy())
-        rel[name] = round(comp.relative_error(x.to(dev), c.view(1, 8, 4096, 128), s, z), 4)
+        c, s_, z = ops.unpack_tokens(pools[0], bt[0], 4096, which)
+        got[name] = (c.cpu(), s_.cpu(), z.cpu())
+        rel[name] = round(comp.relative_error(x.to(dev), c.view(1, 8, 4096, 128), s_, z), 4)
     gbs = C1_BYTES / (us_q * 1e-6) / 1e9
-    cpu = None if args.no_cpu_baseline else cpu_baseline_quant(K16, V16, got, args.cpu_budget)
-    line = {
-        "metric": "INT4 quantize+pack GB/s on the C1 round-trip tensors (K, V [1, 8, 4096, 128] fp16)",
-        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": n, "warmup": args.warmup,
-        "ms_per_step": round(us_q * 1e-3, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp16->int4", "data": "synthetic (seeded N(0,1) K/V, K channels 7, 31, 64, 100 x8)",
-        "config": {"workload": "quantize+pack K and V [1, 8, 4096, 128] fp16 into 256 INT4 block records of 8 kv "
-                               "heads (group 128), then back to fp16 by the Path C route",
-                   "algorithmic_bytes": C1_BYTES, "roundtrip_us": round(us_rt, 3),
-                   "roundtrip_gbs": round(C1_BYTES / (us_rt * 1e-6) / 1e9, 2),
-                   "relative_error_pct": rel},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(line), flush=True)
+    blk = {"workload": "quantize+pack K and V [1, 8, 4096, 128] fp16 into 256 INT4 block records of 8 kv heads "
+                       "(group 128), then back to fp16 by the Path C route",
+           "algorithmic_bytes": C1_BYTES, "value": round(gbs, 2), "unit": "GB/s", "us_per_step": round(us_q, 3),
+           "steps": 64, "launch": "hip graph", "roundtrip_us": round(us_rt, 3), "relative_error_pct": rel,
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+    if args.no_cpu_baseline:
+        return blk
+    n = cpu_threads(torch)
 
+    def step():
+        return tr.compress(K16, 128), tr.compress(V16, 128)
 
-def cpu_baseline_quant(K16, V16, got, budget_s):
-    """The oracle's compress (kv_compressor.py:50-98 restated in C, one thread) on the same
-    K and V, timed on the host; also the number of codes / scales / zero points that differ
-    from the GPU's (reported, expected 0)."""
-    import numpy as np
-    from oracle import compressor as oc
-    t0 = time.perf_counter()
-    reps = 0
+    t, reps, ((kc, kss, kz), (vc, vss, vz)) = time_cpu(step, min(args.cpu_budget, 5.0))
     mism = 0
-    while True:
-        for name, x in (("k", K16), ("v", V16)):
-            c, s, z = oc.compress(x[0].numpy(), 128)
-            if reps == 0:
-                gc, gs, gz = got[name]
-                mism += int((c != gc).sum() + (s.view(np.uint32) != gs.view(np.uint32)).sum() + (z != gz).sum())
-        reps += 1
-        if time.perf_counter() - t0 >= min(budget_s, 5.0) or reps >= 50:
-            break
-    per = (time.perf_counter() - t0) / reps
-    return {"value": round(C1_BYTES / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": "%d full K+V compress pass(es), %.1f ms each; code/scale/zp mismatches vs GPU: %d"
-                      % (reps, per * 1e3, mism)}
+    for (c, s_, z), name in (((kc, kss, kz), "k"), ((vc, vss, vz), "v")):
+        gc, gs, gz = got[name]
+        mism += int((c.view(8, 4096, 128) != gc).sum() + (s_.view(torch.int32) != gs.view(torch.int32)).sum() +
+                    (z != gz).sum())
+    blk["cpu_baseline"] = {"value": round(C1_BYTES / t / 1e9, 4), "unit": "GB/s", "cores": n, "kind": "port",
+                           "sample": "%d float32 torch compress passes of K and V (kv_compressor.py ops), median "
+                                     "%.1f ms" % (reps, t * 1e3)}
+    blk["parity"] = {"code_scale_zp_mismatches_vs_cpu": mism}
+    return blk
 
 
 def bench_scoring(torch, ops, args):
@@ -480,30 +578,24 @@ def _summ(times, stats):
             "stall_fraction": round(stall / (t * 1e3), 4)}
 
 
-def cpu_baseline_tiered(torch, model, budget_s=20.0):
-    """The reference's decode step restated on the host cores for ONE of the 28 layers at
-    the 131072-token shape (Path C: dequantize all 126912 INT4 tokens of the layer to fp16,
-    float64 attention over them plus 64 sink + 4096 recent tokens, 28 q / 4 kv heads) and
-    that layer's projections and MLP in float32 torch; the per-token figure scales the layer
-    time by 28 and adds the final norm + lm_head GEMV."""
-    import numpy as np
-    from oracle import attention as oa
-    from oracle import compressor as oc
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:
-        threads = 1
+def cpu_baseline_c5(torch, model, budget_s):
+    """The reference's decode step restated on the host cores in float32 torch for ONE of the
+    28 layers at the 131072-token shape (Path C: dequantize the layer's 126912 INT4 tokens to
+    fp16, attention over them plus 64 sink + 4096 recent tokens, 28 q / 4 kv heads; the
+    layer's projections and MLP); per token the layer time x 28 plus the final lm_head GEMV."""
+    from oracle import torch_ref as tr
+    n = cpu_threads(torch)
     mid = T_CTX - T_KEEP
-    g = np.random.default_rng(5)
-    kn = g.standard_normal((T_HKV, mid, D), dtype=np.float32).astype(np.float16)
-    vn = g.standard_normal((T_HKV, mid, D), dtype=np.float32).astype(np.float16)
-    kc, ks, kz = oc.compress(kn, 128)
-    vc, vs, vz = oc.compress(vn, 128)
-    hk = g.standard_normal((T_HKV, T_KEEP, D)).astype(np.float16).astype(np.float64)
-    hv = g.standard_normal((T_HKV, T_KEEP, D)).astype(np.float16).astype(np.float64)
+    g = torch.Generator().manual_seed(5)
+    kn = torch.randn((T_HKV, mid, D), generator=g).half()
+    vn = torch.randn((T_HKV, mid, D), generator=g).half()
+    kc, ks, kz = tr.compress(kn, 128)
+    vc, vs, vz = tr.compress(vn, 128)
+    del kn, vn
+    hk = [torch.randn((T_HKV, T_KEEP, D), generator=g).half()]
+    hv = [torch.randn((T_HKV, T_KEEP, D), generator=g).half()]
     layer = model.model.layers[0]
-    w = {n: p.detach().float().cpu() for n, p in layer.named_parameters()}
+    w = {nm: p.detach().float().cpu() for nm, p in layer.named_parameters()}
     lm = model.lm_head.weight.detach().float().cpu()
     x = torch.randn(1, T_HIDDEN)
 
@@ -512,44 +604,34 @@ def cpu_baseline_tiered(torch, model, budget_s=20.0):
         q = h @ w["self_attn.q_proj.weight"].T + w["self_attn.q_proj.bias"]
         h @ w["self_attn.k_proj.weight"].T
         h @ w["self_attn.v_proj.weight"].T
-        kd = oa.dequant_rows(kc, ks.reshape(T_HKV, mid), kz.reshape(T_HKV, mid))
-        vd = oa.dequant_rows(vc, vs.reshape(T_HKV, mid), vz.reshape(T_HKV, mid))
-        a = oa.attend(q.view(T_HQ, 1, D).double().numpy(), np.concatenate([kd, hk], 1), np.concatenate([vd, hv], 1))
-        o = torch.from_numpy(a.reshape(1, T_HQ * D)).float() @ w["self_attn.o_proj.weight"].T
+        a = tr.attend(q.view(T_HQ, 1, D), tr.path_c_keys(kc, ks, kz, hk), tr.path_c_keys(vc, vs, vz, hv))
+        o = a.reshape(1, T_HQ * D) @ w["self_attn.o_proj.weight"].T
         h2 = x + o
         h3 = h2 * torch.rsqrt(h2.pow(2).mean(-1, keepdim=True) + 1e-6) * w["post_attention_layernorm.weight"]
         gte = torch.nn.functional.silu(h3 @ w["mlp.gate_proj.weight"].T) * (h3 @ w["mlp.up_proj.weight"].T)
         return h2 + gte @ w["mlp.down_proj.weight"].T
 
-    t0 = time.perf_counter()
-    n = 0
-    while True:
-        layer_step()
-        n += 1
-        if time.perf_counter() - t0 >= budget_s / 2 or n >= 3:
-            break
-    t_layer = (time.perf_counter() - t0) / n
-    t1 = time.perf_counter()
-    x @ lm.T
-    t_head = time.perf_counter() - t1
+    t_layer, reps, _ = time_cpu(layer_step, budget_s, max_reps=5)
+    t_head, _, _ = time_cpu(lambda: x @ lm.T, 1.0, max_reps=3)
     t_tok = T_LAYERS * t_layer + t_head
-    return dict(value=1.0 / t_tok, unit="tok/s", cores=threads, kind="port",
-                sample="%d timed pass(es) of one decoder layer at 131072 tokens (Path C dequant of 126912 INT4 "
-                       "tokens + float64 attention + fp32 projections/MLP, %.2f s each), x28 + lm_head GEMV"
-                       % (n, t_layer))
+    return {"value": round(1.0 / t_tok, 5), "unit": "tok/s", "cores": n, "kind": "port",
+            "sample": "%d timed pass(es) of one decoder layer at 131072 tokens (float32 torch: Path C dequant "
+                      "of 126912 INT4 tokens + attention + projections/MLP, median %.2f s) x 28 + lm_head GEMV"
+                      % (reps, t_layer)}
 
 
-def bench_tiered(torch, args):
+def leg_c5(torch, args, timed=8, warm=2):
     """End-to-end tiered decode at 131072 tokens: chunked prefill (2048-token chunks, fused
     prefill kernel), then 75% of every layer's INT4 block records moved to pinned host memory;
-    decode with each layer's host records copied on the side stream one layer ahead."""
+    decode with each layer's host records copied on the side stream one layer ahead.  Greedy
+    tokens; every variant decodes `timed` tokens after `warm` untimed ones."""
     from heterokv.engine_wrapper import ChunkedPrefillEngine, DecodeGraph, FusedHeteroCache
+    from oracle import torch_ref as tr
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     t0 = time.perf_counter()
     model = _tiered_model(torch, dev)
     torch.cuda.synchronize()
-    print("[tiered] model ready in %.1f s" % (time.perf_counter() - t0), file=sys.stderr, flush=True)
+    print("[c5] model ready in %.1f s" % (time.perf_counter() - t0), file=sys.stderr, flush=True)
     ids = torch.randint(0, T_VOCAB, (1, T_CTX), generator=torch.Generator().manual_seed(1)).to(dev)
     cache = FusedHeteroCache(num_layers=T_LAYERS, sink_tokens=T_SINK, keep_tail=T_KEEP, chunk_size=T_CHUNK,
                              device=str(dev), fused_prefill=True)
@@ -560,7 +642,7 @@ def bench_tiered(torch, args):
             part = ids[:, :start + 16 * T_CHUNK]
             eng.prefill(part[:, start:], position_ids=torch.arange(start, part.shape[1], device=dev)[None])
             torch.cuda.synchronize()
-            print("[tiered] prefill %d / %d tokens, %.1f s" % (part.shape[1], T_CTX, time.perf_counter() - t0),
+            print("[c5] prefill %d / %d tokens, %.1f s" % (part.shape[1], T_CTX, time.perf_counter() - t0),
                   file=sys.stderr, flush=True)
     prefill_s = time.perf_counter() - t0
     mgr = cache._manager
@@ -568,46 +650,56 @@ def bench_tiered(torch, args):
     out = {}
     with torch.inference_mode():
         tok, pos = ids[:, -1:], T_CTX
-        # all INT4 records resident in HBM
-        tok, pos, _, _ = _decode_tokens(torch, model, cache, tok, pos, args.warmup, dev)
-        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, args.steps, dev)
+        tok, pos, _, _ = _decode_tokens(torch, model, cache, tok, pos, warm, dev)
+        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, timed, dev)
         out["resident"] = _summ(tm, st)
-        print("[tiered] resident: %s" % out["resident"], file=sys.stderr, flush=True)
-        # the same with each decode step captured once in a HIP graph and replayed
-        # (device-stepped zones: no per-token host work besides bookkeeping)
         runner = DecodeGraph(model, cache)
-        tok, pos, _, _ = _decode_tokens_graph(torch, runner, tok, pos, max(args.warmup, 3), dev)
-        tok, pos, tm, st = _decode_tokens_graph(torch, runner, tok, pos, args.steps, dev)
+        tok, pos, _, _ = _decode_tokens_graph(torch, runner, tok, pos, max(warm, 3), dev)
+        tok, pos, tm, st = _decode_tokens_graph(torch, runner, tok, pos, timed, dev)
         out["resident_graph"] = _summ(tm, st)
         runner.close()
         del runner
-        print("[tiered] resident, graph replay: %s" % out["resident_graph"], file=sys.stderr, flush=True)
         moved = cache.offload_to_host(T_HOST_FRAC, seed=0)
         torch.cuda.synchronize()
         host_bytes = mgr.memory_summary()["host_bytes"]
         # full retrieval (Path C): every host record crosses PCIe every token
-        tok, pos, _, _ = _decode_tokens(torch, model, cache, tok, pos, args.warmup, dev)
+        tok, pos, _, _ = _decode_tokens(torch, model, cache, tok, pos, warm, dev)
         b0 = mgr.prefetch_stats()["bytes_h2d"]
-        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, args.steps, dev)
+        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, timed, dev)
         full = _summ(tm, st)
-        full["h2d_bytes_per_token"] = (st[-1]["bytes_h2d"] - b0) // max(args.steps, 1)
+        full["h2d_bytes_per_token"] = (st[-1]["bytes_h2d"] - b0) // max(timed, 1)
         out["full"] = full
-        print("[tiered] full retrieval: %s" % full, file=sys.stderr, flush=True)
-        # the same without look-ahead (copies issued when the layer needs them)
-        mgr.enable_prefetch = False
-        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, max(args.steps // 2, 1), dev)
-        out["full_no_lookahead"] = _summ(tm, st)
-        mgr.enable_prefetch = True
+        # parity: one layer's decode attention over its host-tier records (staged) against the
+        # float32 Path C restatement over the same INT4 codes and zones
+        layer = 5
+        qq = (torch.randn((1, T_HQ, 1, D), generator=torch.Generator().manual_seed(9)) / math.sqrt(D)).half()
+        got = mgr.attend_decode(layer, qq.to(dev)).float().cpu()[0, :, 0]
+        codes = {nm: [] for nm in ("k_data", "k_scales", "k_zps", "v_data", "v_scales", "v_zps")}
+        for key in mgr._layer_chunks(layer):
+            e = mgr.chunk_codes(key)
+            for nm in codes:
+                codes[nm].append(e[nm].cpu())
+        zk, zv = mgr.get_hbm_kv(layer)
+        kcat = torch.cat([c[0] for c in codes["k_data"]], dim=1)
+        vcat = torch.cat([c[0] for c in codes["v_data"]], dim=1)
+        nt = kcat.shape[1]
+        ksc = torch.cat([s_.view(T_HKV, -1) for s_ in codes["k_scales"]], 1).reshape(-1)
+        kzp = torch.cat([z.view(T_HKV, -1) for z in codes["k_zps"]], 1).reshape(-1)
+        vsc = torch.cat([s_.view(T_HKV, -1) for s_ in codes["v_scales"]], 1).reshape(-1)
+        vzp = torch.cat([z.view(T_HKV, -1) for z in codes["v_zps"]], 1).reshape(-1)
+        ref = tr.attend(qq[0].float(), tr.path_c_keys(kcat, ksc, kzp, [zk[0].cpu()]),
+                        tr.path_c_keys(vcat, vsc, vzp, [zv[0].cpu()]))[:, 0]
+        parity = {"layer": layer, "int4_tokens": nt, "fp16_tokens": int(zk.shape[2]),
+                  "max_abs_err_vs_cpu": round(float((got - ref).abs().max()), 6), "tolerance": 2e-3}
         # windowed retrieval (Path A): the top-w_t chunks, w_t from the adaptive controller
         cache.retrieval_window = "adaptive"
-        tok, pos, _, _ = _decode_tokens(torch, model, cache, tok, pos, args.warmup, dev)
+        tok, pos, _, _ = _decode_tokens(torch, model, cache, tok, pos, warm, dev)
         b0 = mgr.prefetch_stats()["bytes_h2d"]
-        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, args.steps, dev)
+        tok, pos, tm, st = _decode_tokens(torch, model, cache, tok, pos, timed, dev)
         win = _summ(tm, st)
-        win["h2d_bytes_per_token"] = (st[-1]["bytes_h2d"] - b0) // max(args.steps, 1)
+        win["h2d_bytes_per_token"] = (st[-1]["bytes_h2d"] - b0) // max(timed, 1)
         win["window_chunks"] = int(mgr._adaptive_controller.stats["current_w"])
         out["windowed"] = win
-        print("[tiered] windowed retrieval: %s" % win, file=sys.stderr, flush=True)
         # host -> HBM copy rate of one layer's records on the side stream
         pf, st0 = mgr._pf, mgr._layers[0]
         rb = st0.n_host * mgr._staging[0].record_bytes
@@ -619,113 +711,60 @@ def bench_tiered(torch, args):
         ev1.record()
         ev1.synchronize()
         h2d_gbs = rb / (ev0.elapsed_time(ev1) * 1e-3) / 1e9
+        cache.check_errors()
+    print("[c5] %s" % json.dumps(out), file=sys.stderr, flush=True)
     weights = sum(p.numel() * p.element_size() for p in model.parameters())
-    kv_hbm = (int4_tokens * T_HKV * 2 * (D // 2 + 5) * (1 - T_HOST_FRAC) + T_KEEP * T_HKV * D * 2 * 2) * T_LAYERS
-    tok_bytes = weights + kv_hbm
-    ms = full["ms_per_token"]
-    gbs = tok_bytes / (ms * 1e-3) / 1e9
-    cpu = None
+    host_per_tok = full["h2d_bytes_per_token"]
+    blk = {"workload": "tiered decode: 28-layer Qwen2-style decoder (hidden 3584, 28 q / 4 kv heads, head_dim 128, "
+                       "MLP 18944, vocab 152064, random-init bf16), 131072-token prompt prefilled in 2048-token "
+                       "chunks, sink 64 + recent 4096 fp16, INT4 middle with 75% of its 16-token blocks in pinned "
+                       "host memory, batch 1, greedy",
+           "full_tok_per_s": full["tok_per_s"], "windowed_tok_per_s": win["tok_per_s"],
+           "full_stall_ms_per_token": full["prefetch_stall_ms_per_token"],
+           "windowed_stall_ms_per_token": win["prefetch_stall_ms_per_token"],
+           "h2d_gbs_one_layer_copy": round(h2d_gbs, 2), "unit": "tok/s", "steps": timed, "warmup": warm,
+           "int4_tokens_per_layer": int4_tokens, "host_records_moved": moved, "host_bytes": host_bytes,
+           "prefill_seconds": round(prefill_s, 1),
+           # the reference's end-to-end figure (results_throughput.csv:42, 2.07 tok/s at 131072 tokens
+           # on its hardware) counts the 128K prefill plus 64 decode tokens in its wall time
+           "wall_tok_per_s_prefill_plus_64_tokens": {
+               k: round(64.0 / (prefill_s + 64 * out[k]["ms_per_token"] * 1e-3), 3)
+               for k in ("full", "windowed", "resident_graph")},
+           "variants": out,
+           # full retrieval moves every host record over PCIe per token: its bound is the link
+           "roofline": {"bound": "pcie", "achieved": round(host_per_tok / (full["ms_per_token"] * 1e-3) / 1e9, 2),
+                        "peak": round(h2d_gbs, 2), "unit": "GB/s",
+                        "frac": round(host_per_tok / (full["ms_per_token"] * 1e-3) / 1e9 / h2d_gbs, 4),
+                        "traffic": None, "weights_bytes": weights},
+           "parity": parity}
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline_tiered(torch, model, args.cpu_budget * 2)
-    line = {
-        "metric": "end-to-end decode tok/s at 131072-token context with 75% of INT4 KV blocks in pinned host "
-                  "DRAM (full retrieval)",
-        "value": full["tok_per_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (random-init weights, seeded random token ids)",
-        "config": {"workload": "tiered decode: 28-layer Qwen2-style decoder (hidden 3584, 28 q / 4 kv heads, "
-                               "head_dim 128, MLP 18944, vocab 152064), 131072-token prompt prefilled in 2048-token "
-                               "chunks, sink 64 + recent 4096 fp16, INT4 middle with 75% of its 16-token blocks "
-                               "in pinned host memory, batch 1, greedy",
-                   "int4_tokens_per_layer": int4_tokens, "host_records_moved": moved, "host_bytes": host_bytes,
-                   "prefill_seconds": round(prefill_s, 1), "h2d_gbs_one_layer_copy": round(h2d_gbs, 2),
-                   # the reference's end-to-end figure counts the 128K prefill plus 64 decode tokens in
-                   # its wall time; the same quantity from this run's prefill and per-token times
-                   "wall_tok_per_s_prefill_plus_64_tokens": {
-                       k: round(64.0 / (prefill_s + 64 * out[k]["ms_per_token"] * 1e-3), 3)
-                       for k in ("full", "windowed", "resident_graph")},
-                   "hbm_bytes_per_token": int(tok_bytes)},
-        "variants": out,
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
-        "cpu_baseline": ({k: (round(v, 5) if isinstance(v, float) else v) for k, v in cpu.items()}
-                         if cpu else None),
-    }
-    print(json.dumps(line), flush=True)
+        blk["cpu_baseline"] = cpu_baseline_c5(torch, model, args.cpu_budget * 2)
+    del model, cache
+    torch.cuda.empty_cache()
+    return blk
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4096)
-    ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--copies", type=int, default=8)
-    ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--deterministic", action="store_true",
-                    help="decode with the fixed block-to-wave schedule (bitwise reproducible)")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged", "scoring", "quant"], default="decode",
-                    help="decode: the headline single-layer decode (default); prefill: the chunked-prefill "
-                         "kernel on a 2048-token chunk over 64 + 131072 INT4 + 4096 tokens (MFMA bound); "
-                         "tiered: end-to-end 28-layer decode at 131072 tokens with 75%% of the INT4 KV in "
-                         "pinned host memory (use small --steps/--warmup, e.g. 8 / 2); paged: batch-16 paged "
-                         "decode, contexts 8K-32K; scoring: heavy-hitter scoring at 32K; quant: quantize+pack "
-                         "of K, V [1, 8, 4096, 128] and the round trip back to fp16")
-    ap.add_argument("--copy-calibration", type=float, default=0.0,
-                    help="run only torch's device copy of this many MB (20 launches) so that rocprofv3 "
-                         "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the decode path would shard by kv head or "
-              "sequence, with no exchange between GPUs); run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-
-    import torch
-
-    if args.copy_calibration > 0:
-        dev = torch.device("cuda:0")
-        n = int(args.copy_calibration * 1e6) // 4
-        src = torch.ones(n, dtype=torch.int32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(20):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_calibration_bytes_read_per_launch": n * 4,
-                          "copy_calibration_bytes_written_per_launch": n * 4, "launches": 20}), flush=True)
-        return
-
-    from heterokv import ops
-
-    if args.workload == "prefill":
-        return bench_prefill(torch, ops, args)
-    if args.workload == "tiered":
-        return bench_tiered(torch, args)
-    if args.workload == "paged":
-        return bench_paged(torch, ops, args)
-    if args.workload == "quant":
-        return bench_quant(torch, ops, args)
-    if args.workload == "scoring":
-        return bench_scoring(torch, ops, args)
-
+# ------------------------------------------------------------------------------ C2 headline
+def leg_c2(torch, ops, args):
+    """The headline: single-layer decode attention at 32K context (one launch per step),
+    replayed from a HIP graph over 8 rotated KV copies."""
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     q, K, V = make_inputs(torch)
     R = args.copies
     copies = [build_copy(torch, ops, q, K, V, dev) for _ in range(R)]
     q_dev = q.to(dev)
     out = torch.empty((B, HQ, D), dtype=torch.float16, device=dev)
     ws = ops.DecodeWorkspace(dev)
+    err = ops.ErrorWord(dev)
 
     def launch(i):
         c = copies[i % R]
-        ops.decode_attention(q_dev, zones=c["zones"], pool=c["pool"], block_table=c["bt"],
-                             int4_max_len=MID, workspace=ws, out=out, deterministic=args.deterministic)
+        ops.decode_attention(q_dev, zones=c["zones"], pool=c["pool"], block_table=c["bt"], int4_max_len=MID,
+                             workspace=ws, out=out, deterministic=args.deterministic, err=err)
 
     for i in range(max(R, 8)):
         launch(i)
     torch.cuda.synchronize()
-
     stream = torch.cuda.Stream(device=dev)
     K_steps, W = args.steps, args.warmup
     graphs = {}
@@ -767,47 +806,112 @@ def main():
     ms_total = ev0.elapsed_time(ev1)
     ms_step = ms_total / K_steps
     gbs = STEP_BYTES * K_steps / (ms_total * 1e-3) / 1e9
-    if ws.error_flag():
-        raise RuntimeError("decode kernel reported an out-of-range block id")
-
+    err.check()
     cpu = None
+    parity = None
     if not args.no_cpu_baseline:
-        import numpy as np
-        ref, cpu = cpu_baseline(q, K, V, args.cpu_budget)
+        ref, cpu = cpu_baseline_c2(torch, q, K, V, args.cpu_budget)
         launch(0)
         torch.cuda.synchronize()
-        err = float(np.abs(out[0].float().cpu().numpy() - ref[:, 0]).max())
-        if not err <= 2e-3:
-            raise RuntimeError("GPU output differs from the oracle by %.3e" % err)
-
-    traffic = read_traffic()
+        e = float((out[0].float().cpu() - ref).abs().max())
+        if not e <= 2e-3:
+            raise RuntimeError("GPU decode output differs from the CPU restatement by %.3e" % e)
+        parity = {"max_abs_err_vs_cpu": round(e, 6), "tolerance": 2e-3}
     line = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": K_steps,
-        "warmup": W,
-        "ms_per_step": round(ms_step, 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": K_steps, "warmup": W,
+        "ms_per_step": round(ms_step, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic (seeded N(0,1) K/V with x8 K outlier channels; INT4 middle packed by the "
-                "build's quantizer)",
-        "config": {"workload": "single-layer INT4-KV decode attention, batch 1, 32 q / 8 kv heads, "
-                               "head_dim 128, ctx 32768 = 64 fp16 sink + 28608 INT4 + 4096 fp16 recent",
+        "data": "synthetic (seeded N(0,1) K/V with x8 K outlier channels; INT4 middle packed by the build's "
+                "quantizer; random-init model weights and seeded token ids for the 128K leg)",
+        "config": {"workload": "single-layer INT4-KV decode attention, batch 1, 32 q / 8 kv heads, head_dim 128, "
+                               "ctx 32768 = 64 fp16 sink + 28608 INT4 + 4096 fp16 recent",
                    "batch": B, "context": CTX, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
                    "int4_tokens": MID, "fp16_tokens": SINK + RECENT, "kv_copies_rotated": R,
                    "launch": "eager" if args.no_graph else "hip graph replay",
                    "schedule": "fixed (deterministic)" if args.deterministic else "on demand",
                    "bytes_per_step": STEP_BYTES},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic},
-        "cpu_baseline": ({k: (round(v, 4) if isinstance(v, float) else v) for k, v in cpu.items()}
-                         if cpu else None),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic()},
+        "cpu_baseline": ({k: (round(v, 4) if isinstance(v, float) else v) for k, v in cpu.items()} if cpu else None),
+        "parity": parity,
     }
+    return line
+
+
+LEGS = ("c1", "c3", "c4", "c5")
+LEG_KEYS = {"c1": "c1_quant", "c3": "c3_paged", "c4": "c4_prefill", "c5": "offload_128k"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4096, help="timed launches of the 32K decode (the headline)")
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--deterministic", action="store_true",
+                    help="decode with the fixed block-to-wave schedule (bitwise reproducible)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU work per baseline")
+    ap.add_argument("--legs", default=",".join(LEGS),
+                    help="nested configuration blocks of the default line: any of c1 (quantize+pack), c3 (batched "
+                         "paged decode), c4 (chunked prefill), c5 (128K tiered decode with 75%% host offload); "
+                         "'none' for the 32K decode alone")
+    ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged", "scoring", "quant"], default=None,
+                    help="run one configuration alone and print its block as the line (for profiling): decode "
+                         "(32K), prefill (C4), tiered (C5), paged (C3), quant (C1), scoring (heavy hitters)")
+    ap.add_argument("--copy-calibration", type=float, default=0.0,
+                    help="run only torch's device copy of this many MB (20 launches) so that rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the decode path would shard by kv head or "
+              "sequence, with no exchange between GPUs); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.copy_calibration > 0:
+        n = int(args.copy_calibration * 1e6) // 4
+        src = torch.ones(n, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read_per_launch": n * 4,
+                          "copy_calibration_bytes_written_per_launch": n * 4, "launches": 20}), flush=True)
+        return
+
+    from heterokv import ops
+
+    single = {"prefill": lambda: leg_c4(torch, ops, args), "paged": lambda: leg_c3(torch, ops, args),
+              "quant": lambda: leg_c1(torch, ops, args), "tiered": lambda: leg_c5(torch, args),
+              "scoring": lambda: bench_scoring(torch, ops, args)}
+    if args.workload in single:
+        blk = single[args.workload]()
+        if blk is not None:
+            print(json.dumps(blk), flush=True)
+        return
+    line = leg_c2(torch, ops, args)
+    legs = [] if args.legs in ("", "none") else [x.strip() for x in args.legs.split(",")]
+    for leg in legs:
+        if leg not in LEGS:
+            raise SystemExit("bench.py: unknown leg %r (choose from %s)" % (leg, ", ".join(LEGS)))
+        print("[bench] leg %s" % leg, file=sys.stderr, flush=True)
+        t0 = time.perf_counter()
+        if leg == "c1":
+            blk = leg_c1(torch, ops, args)
+        elif leg == "c3":
+            blk = leg_c3(torch, ops, args)
+        elif leg == "c4":
+            blk = leg_c4(torch, ops, args)
+        else:
+            blk = leg_c5(torch, args)
+        blk["leg_seconds"] = round(time.perf_counter() - t0, 1)
+        line[LEG_KEYS[leg]] = blk
+        torch.cuda.empty_cache()
     print(json.dumps(line), flush=True)
 
 

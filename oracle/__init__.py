@@ -17,6 +17,10 @@ Modules
                   closed forms and torch SDPA in tests/test_oracle_attention.py.
   pool_format  -- the packed INT4 block-record and fp16-zone layouts of this
                   build, written from their specification in include/heterokv.h.
+  torch_ref    -- the same compress / decompress / Path C / attention in float32 torch
+                  on the CPU, with the reference's own torch operations: the bench's
+                  CPU baseline; pinned bit for bit against the C compressor and against
+                  the float64 attention in tests/test_oracle_torch_ref.py.
   manager      -- HeteroKVManager zone / eviction / gather index arithmetic
                   (src/memory/manager.py:416-674,686-777,779-821,1218-1299);
                   pinned by hand-derived traces in tests/test_oracle_manager.py.
