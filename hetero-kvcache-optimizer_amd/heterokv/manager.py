@@ -202,7 +202,7 @@ class HeteroKVManager:
         # retrieval of the INT4 middle at decode: None = every chunk (decompress_dram_chunks,
         # manager.py:779-821); an int or "adaptive" = the top-w chunks by score
         # (get_dram_chunks_quantized_adaptive, manager.py:931-1056)
-        self.retrieval_window: Any = None
+        self._retrieval_window: Any = None
         self._adaptive_controller = AdaptivePrefetchController()
         self._last_attention_weights: Optional[torch.Tensor] = None
         # device-stepped decode (enable_device_decode): zone decisions and lengths on the GPU
@@ -212,6 +212,19 @@ class HeteroKVManager:
         self._oracle = HeavyHitterOracle(block_size=16, sink_tokens=sink_tokens, local_window=hbm_budget_tokens)
 
     # ---------------------------------------------------------------- helpers
+    @property
+    def retrieval_window(self) -> Any:
+        """None: every INT4 chunk joins decode attention (Path C, manager.py:779-821); an int
+        or "adaptive": the top-w chunks by score (Path A, manager.py:931-1056)."""
+        return self._retrieval_window
+
+    @retrieval_window.setter
+    def retrieval_window(self, w: Any) -> None:
+        # selections made ahead of time by the look-ahead belong to the old window
+        self._selection_of.clear()
+        self._selection_b.clear()
+        self._retrieval_window = w
+
     @property
     def tail_budget(self) -> int:
         return self.hbm_budget_tokens - self.sink_tokens
@@ -885,9 +898,14 @@ class HeteroKVManager:
                     runs.append((k0, k1))
         return runs
 
-    def _submit(self, layer_idx: int, sel) -> Tuple[int, Any, int]:
+    def _submit(self, layer_idx: int, sel, avoid_buf: Optional[int] = None) -> Tuple[int, Any, int]:
+        """Copy the layer's host runs into the next staging buffer (never `avoid_buf`, the one
+        the layer being attended reads: its "free" mark is only recorded after its kernel, so
+        a copy into it would race that kernel)."""
         st = self._layers[layer_idx]
         buf = self._next_buf
+        if buf == avoid_buf:
+            buf = (buf + 1) % len(self._staging)
         self._next_buf = (buf + 1) % len(self._staging)
         prev_slot = self._buf_owner[buf]
         prev = prev_slot // 2 if prev_slot >= 0 else -1
@@ -905,7 +923,7 @@ class HeteroKVManager:
         self._pending[layer_idx] = (buf, sel, slot)
         return self._pending[layer_idx]
 
-    def _prefetch_after(self, layer_idx: int) -> None:
+    def _prefetch_after(self, layer_idx: int, avoid_buf: Optional[int] = None) -> None:
         """Submit the copies of the next layer (cyclically) that holds host records."""
         L = len(self._layers)
         for d in range(1, L):
@@ -916,7 +934,7 @@ class HeteroKVManager:
             sel = self._selection(j)
             p = self._pending.get(j)
             if p is None or p[1] != sel:
-                self._submit(j, sel)
+                self._submit(j, sel, avoid_buf)
             return
 
     def prefetch_stats(self, reset: bool = True) -> Dict[str, Any]:
@@ -984,7 +1002,7 @@ class HeteroKVManager:
                 p = self._submit(layer_idx, sel)
             buf, _, slot = p
         if self._pf is not None and self.enable_prefetch:
-            self._prefetch_after(layer_idx)
+            self._prefetch_after(layer_idx, buf)
         if staged:
             self._pf.wait(slot)
         q = query_states

@@ -283,3 +283,46 @@ def test_dram_storage_manager_and_async_prefetcher():
     assert torch.equal(rk, comp.decompress(qk, sk, zk).to(torch.bfloat16))
     assert torch.equal(rv, comp.decompress(qv, sv, zv).to(torch.bfloat16))
     assert pf.fetch_if_ready("l0_e0") is None
+
+
+def test_out_of_order_attends_with_host_tier():
+    """attend_decode calls in any layer order (a caller re-attending a layer, skipping one)
+    stay bit-identical to an all-resident twin: the look-ahead copy never lands in the
+    staging buffer of the layer being attended."""
+    print("case: out-of-order attend_decode with a host tier", flush=True)
+    from heterokv.manager import HeteroKVManager
+    L, B, H, HQ = 4, 1, 4, 16
+    K, V = _kv(21, B, H, 2600)
+    a = HeteroKVManager(L, sink_tokens=64, hbm_budget_tokens=576, device=DEV)
+    b = HeteroKVManager(L, sink_tokens=64, hbm_budget_tokens=576, device=DEV)
+    a.deterministic_decode = b.deterministic_decode = True
+    pos = _feed([a, b], K, V, L, [1024, 1024, 500])
+    a.offload_to_host(0.75, seed=5)
+    g = torch.Generator().manual_seed(22)
+    order = [0, 1, 2, 3, 0, 0, 1, 3, 2, 1, 2, 3, 0, 2, 1, 0, 3, 3, 1]
+    for li in order:
+        q = (torch.randn((B, HQ, 1, 128), generator=g) / math.sqrt(128)).half().to(DEV)
+        assert torch.equal(a.attend_decode(li, q), b.attend_decode(li, q)), li
+    a.check_errors()
+
+
+def test_window_change_after_lookahead():
+    """Switching retrieval_window after full-retrieval steps whose look-ahead already chose
+    the next layers' chunks: every later attend uses the new window, as on an all-resident
+    twin (which never looks ahead)."""
+    print("case: retrieval_window change after look-ahead", flush=True)
+    from heterokv.manager import HeteroKVManager
+    L, B, H, HQ = 3, 1, 4, 16
+    K, V = _kv(23, B, H, 2600)
+    a = HeteroKVManager(L, sink_tokens=64, hbm_budget_tokens=576, device=DEV)
+    b = HeteroKVManager(L, sink_tokens=64, hbm_budget_tokens=576, device=DEV)
+    a.deterministic_decode = b.deterministic_decode = True
+    _feed([a, b], K, V, L, [1024, 1024, 500])
+    a.offload_to_host(0.75, seed=6)
+    g = torch.Generator().manual_seed(24)
+    for window in (None, 2, None, "adaptive", 1):
+        a.retrieval_window = b.retrieval_window = window
+        for li in [0, 1, 2, 0, 1, 2]:
+            q = (torch.randn((B, HQ, 1, 128), generator=g) / math.sqrt(128)).half().to(DEV)
+            assert torch.equal(a.attend_decode(li, q), b.attend_decode(li, q)), (window, li)
+    a.check_errors()
