@@ -33,9 +33,9 @@
 // ticket and L1-bypassing loads.  Otherwise (or with HKV_DECODE_AGENT_HANDOFF) it
 // goes through memory with agent-scope (sc1) accesses.  The placement is checked
 // on every launch: each workgroup ORs its XCD bit into a device-scope mask of its
-// pair as its first memory operation and reads the old mask back before its
-// ticket; a foreign bit (or a ticket beyond the range count, left by such a
-// launch) sets HKV_ERR_BIT_PLACEMENT.  The merging workgroup clears the mask.
+// pair when its streaming ends and reads the old mask back at its ticket; a foreign
+// bit (or a ticket beyond the range count, left by such a launch) sets
+// HKV_ERR_BIT_PLACEMENT.  The merging workgroup clears the mask.
 #include "hkv_internal.h"
 #include "nibble_decode.h"
 
@@ -518,14 +518,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const int c = lane & 15, g = lane >> 4;
     const int kzsh = 8 * (c & 3);
     const int nrep = p.nrep;
-    // XCD-local hand-off: OR this workgroup's XCD bit (HW_REG_XCC_ID) into the pair's
-    // device-scope mask first; the old mask is only examined before the ticket, so the
-    // round trip overlaps the streaming
-    unsigned owner_old = 0u, owner_bit = 0u;
-    if (p.xcc_local && threadIdx.x == 0) {
-        owner_bit = 1u << (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
-        owner_old = __hip_atomic_fetch_or(&p.owners[bh], owner_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    unsigned owner_old = 0u, owner_bit = 0u;   // placement check (below, after the streaming)
 
     const int len4 = p.int4_lens ? min(max(p.int4_lens[b], 0), p.int4_max_len) : p.int4_max_len;
     int lenz[HKV_MAX_F16_ZONES];
@@ -717,6 +710,17 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             __syncthreads();   // every wave is done with this window's ids and counter
             if (kDynamic && threadIdx.x == 0) sm_ctr[0] = kPrefetch * kWaves;
         }
+    }
+
+    // XCD-local hand-off: OR this workgroup's XCD bit (HW_REG_XCC_ID) into the pair's
+    // device-scope mask; the old mask is examined at the ticket.  Issued here, its round
+    // trip overlaps the merge below.  (At the start of the kernel it cost ~1.7 us on the
+    // 32K decode: the pair's 32 atomics serialize on one address, and loads issued after
+    // one complete after it.)  Of any two workgroups of a pair on different XCDs, the
+    // later OR returns the other's bit, so a split placement is always reported.
+    if (p.xcc_local && threadIdx.x == 0) {
+        owner_bit = 1u << (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
+        owner_old = __hip_atomic_fetch_or(&p.owners[bh], owner_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // ---- merge the waves of this workgroup through LDS

@@ -184,6 +184,21 @@ def test_schedules_agree_on_long_windows():
     _check(c, splits=1)
 
 
+def test_long_ragged_contexts():
+    """Long and short sequences in one batch: 140000 INT4 tokens (8750 blocks, many id
+    windows per range) beside 33 (an odd block count), one kv head."""
+    print("case: B=2 1/4 heads, 140000 and 33 INT4 tokens", flush=True)
+    c = Case(14, 2, 4, 1, 16, [140000, 33], [64, 1])
+    _check(c)
+
+
+def test_very_long_context():
+    """270000 INT4 tokens (16875 blocks) in one sequence."""
+    print("case: B=1 4/1 heads, 270000 INT4 tokens", flush=True)
+    c = Case(15, 1, 4, 1, 16, [270000], [64])
+    _check(c)
+
+
 @pytest.mark.parametrize("seed", range(int(os.environ.get("HKV_DECODE_RANDOM_CASES", "24"))))
 def test_random_geometries(seed):
     """Seeded random geometries against the float64 oracle in both schedules: batch 1-4,
