@@ -11,6 +11,7 @@
 * `AdaptivePrefetchController` mirrors src/policy/adaptive_prefetch_controller.py:33-143
   (window size w_t from attention volatility and miss rate).
 """
+import collections
 import ctypes
 import math
 from typing import Any, Dict, List, Optional, Tuple
@@ -318,37 +319,40 @@ class AdaptivePrefetchController:
         self.alpha, self.beta = alpha, beta
         self.delta_max, self.ema_decay = delta_max, ema_decay
         self.miss_window_size = miss_window_size
-        self._current_w = float(w_min)
-        self._sigma_ref = 0.0
-        self._sigma_ref_initialized = False
-        self._miss_history: List[bool] = []
-        self._step = 0
+        self._window = float(w_min)                      # the last window handed out
+        self._ema_sigma: Optional[float] = None          # None until the first weights arrive
+        self._misses = collections.deque(maxlen=max(1, miss_window_size))
+        self._calls = 0
+
+    def _miss_rate(self) -> float:
+        return sum(self._misses) / len(self._misses) if self._misses else 0.0
+
+    def _volatility(self, attention_weights: Optional[torch.Tensor]) -> float:
+        """Clipped relative deviation of this step's weight spread from its running mean."""
+        if attention_weights is None or attention_weights.numel() <= 1:
+            return 0.0
+        sigma = float(attention_weights.detach().cpu().std())
+        if self._ema_sigma is None:
+            self._ema_sigma = sigma
+        else:
+            self._ema_sigma = self.ema_decay * self._ema_sigma + (1.0 - self.ema_decay) * sigma
+        rel = sigma / self._ema_sigma - 1.0 if self._ema_sigma > 1e-8 else 0.0
+        return min(self.delta_max, max(-self.delta_max, rel * self.alpha))
 
     def compute_window(self, attention_weights: Optional[torch.Tensor] = None, cache_miss: bool = False) -> int:
-        self._step += 1
-        self._miss_history.append(cache_miss)
-        if len(self._miss_history) > self.miss_window_size:
-            self._miss_history.pop(0)
-        miss_rate = sum(self._miss_history) / len(self._miss_history) if self._miss_history else 0.0
-        vol = 0.0
-        if attention_weights is not None and attention_weights.numel() > 1:
-            sigma_t = float(attention_weights.detach().cpu().std())
-            if not self._sigma_ref_initialized:
-                self._sigma_ref = sigma_t
-                self._sigma_ref_initialized = True
-            else:
-                self._sigma_ref = self.ema_decay * self._sigma_ref + (1 - self.ema_decay) * sigma_t
-            dev = (sigma_t / self._sigma_ref - 1.0) if self._sigma_ref > 1e-8 else 0.0
-            vol = max(-self.delta_max, min(self.delta_max, dev * self.alpha))
-        raw = self.w_min + vol + self.beta * miss_rate * self.w_max
-        w = max(self.w_min, min(self.w_max, round(raw)))
-        if abs(w - self._current_w) > 1:
-            w = int(self._current_w + math.copysign(1, w - self._current_w))
-        self._current_w = float(w)
+        self._calls += 1
+        self._misses.append(bool(cache_miss))
+        target = self.w_min + self._volatility(attention_weights) + self.beta * self._miss_rate() * self.w_max
+        w = min(self.w_max, max(self.w_min, round(target)))
+        # the window moves by at most one per step
+        step = w - self._window
+        if abs(step) > 1:
+            w = int(self._window + (1 if step > 0 else -1))
+        self._window = float(w)
         return int(w)
 
     @property
     def stats(self) -> Dict[str, float]:
-        miss_rate = sum(self._miss_history) / len(self._miss_history) if self._miss_history else 0.0
-        return {"current_w": self._current_w, "sigma_ref": self._sigma_ref, "miss_rate": miss_rate,
-                "step": self._step}
+        """The reference's report keys: current window, reference spread, miss rate, steps."""
+        return {"current_w": self._window, "sigma_ref": self._ema_sigma if self._ema_sigma is not None else 0.0,
+                "miss_rate": self._miss_rate(), "step": self._calls}
