@@ -11,6 +11,9 @@ namespace {
 // --------------------------------------------------------------------------
 // Reference layout: one wavefront per group of `G` flattened elements; the last
 // group is zero-padded (kv_compressor.py:70-74), so padding takes part in min/max.
+// min/max are IEEE minimum/maximum (v_minimum3/v_maximum3), which propagate NaN as
+// torch's min/max do: a group holding a NaN gets a NaN scale, and its zero point
+// and codes are 0 (NaN clamps to 0 here; torch's .to(uint8) gives 0).
 __global__ __launch_bounds__(256) void quantize_groups_kernel(
     const void* __restrict__ x, int dtype, int64_t n, int G, int64_t ngroups,
     uint8_t* __restrict__ codes, float* __restrict__ scales, uint8_t* __restrict__ zps) {
@@ -23,13 +26,13 @@ __global__ __launch_bounds__(256) void quantize_groups_kernel(
         for (int i = lane; i < G; i += 64) {
             const int64_t idx = base + i;
             const float v = idx < n ? load_as_float(x, dtype, idx) : 0.0f;
-            mn = fminf(mn, v);
-            mx = fmaxf(mx, v);
+            mn = __builtin_elementwise_minimum(mn, v);
+            mx = __builtin_elementwise_maximum(mx, v);
         }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) {
-            mn = fminf(mn, __shfl_xor(mn, off));
-            mx = fmaxf(mx, __shfl_xor(mx, off));
+            mn = __builtin_elementwise_minimum(mn, __shfl_xor(mn, off));
+            mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, off));
         }
         const QParams q = qparams_from_minmax(mn, mx);
         if (lane == 0) {
@@ -200,14 +203,14 @@ __global__ __launch_bounds__(256) void pack_tokens_kernel(PackParams p) {
         load16(kv ? p.v : p.k, p.dtype, off, p.vec_ok, vals);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            mn = fminf(mn, vals[i]);
-            mx = fmaxf(mx, vals[i]);
+            mn = __builtin_elementwise_minimum(mn, vals[i]);
+            mx = __builtin_elementwise_maximum(mx, vals[i]);
         }
     }
 #pragma unroll
     for (int off = 1; off < 8; off <<= 1) {
-        mn = fminf(mn, __shfl_xor(mn, off));
-        mx = fmaxf(mx, __shfl_xor(mx, off));
+        mn = __builtin_elementwise_minimum(mn, __shfl_xor(mn, off));
+        mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, off));
     }
     if (active) {
         const QParams q = qparams_from_minmax(mn, mx);

@@ -88,7 +88,7 @@ void hkvo_group_params(float mn, float mx, float* scale, uint8_t* zp) {
     float s = (mx - mn) / 15.0f;
     if (s < 1e-8f) s = 1e-8f;
     float z = rintf(-mn / s);
-    if (z < 0.0f) z = 0.0f;
+    if (!(z >= 0.0f)) z = 0.0f; /* NaN converts to 0, as torch's .to(uint8) does */
     if (z > 15.0f) z = 15.0f;
     *scale = s;
     *zp = (uint8_t)z;
@@ -99,7 +99,7 @@ uint8_t hkvo_quant_code(float x, float scale, uint8_t zp) {
     float t = x / scale;
     t = t + (float)zp;
     t = rintf(t);
-    if (t < 0.0f) t = 0.0f;
+    if (!(t >= 0.0f)) t = 0.0f; /* NaN as above */
     if (t > 15.0f) t = 15.0f;
     return (uint8_t)t;
 }
@@ -115,8 +115,13 @@ int64_t hkvo_compress(const void* x, int dtype, int64_t n, int32_t group_size, u
         for (int32_t i = 0; i < group_size; ++i) {
             const int64_t idx = base + i;
             const float v = idx < n ? load_elem(x, dtype, idx) : 0.0f; /* zero padding */
-            if (v < mn) mn = v;
-            if (v > mx) mx = v;
+            /* torch's min/max propagate NaN: one NaN makes the group's scale NaN,
+               and its zero point and codes then convert to 0 */
+            if (v != v || mn != mn) mn = mx = NAN;
+            else {
+                if (v < mn) mn = v;
+                if (v > mx) mx = v;
+            }
         }
         float s;
         uint8_t z;

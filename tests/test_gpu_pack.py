@@ -73,6 +73,33 @@ def test_pack_tokens_bytes(H, T, start):
         assert np.array_equal(zps.reshape(H, -1)[:, start:].cpu().numpy().reshape(-1), ref[2])
 
 
+def test_pack_tokens_nan_and_inf_tokens():
+    """A token row holding a NaN gets a NaN scale and zero codes/zp, as torch's min/max
+    propagate NaN; rows with infinities follow the same float32 steps as the oracle."""
+    print("case: pack_tokens NaN / inf rows", flush=True)
+    from heterokv import ops
+    H, T = 2, 20
+    k, v = _rand_kv(77, H, T)
+    k[0, 0, 3, 17] = float("nan")
+    k[0, 1, 16, :] = float("nan")
+    v[0, 0, 5, 0] = float("inf")
+    v[0, 1, 19, 100] = float("-inf")
+    k[0, 1, 2, 1], k[0, 1, 2, 2] = float("inf"), float("-inf")
+    perm = torch.tensor([1, 0], dtype=torch.int32)
+    pool = ops.Int4Pool(3, H, DEV)
+    ops.pack_tokens(pool, k.to(DEV), v.to(DEV), torch.tensor([0], dtype=torch.int32), perm[None])
+    pool.check_errors()
+    for which, x in ((0, k), (1, v)):
+        rc, rs, rz = oc.compress(x[0].numpy(), 128)
+        codes, scales, zps = ops.unpack_tokens(pool, perm, T, which)
+        got_s = scales.cpu().numpy().reshape(-1)
+        assert np.array_equal(codes.cpu().numpy(), rc)
+        assert np.array_equal(np.isnan(got_s), np.isnan(rs))
+        assert np.array_equal(got_s[~np.isnan(rs)].view(np.uint32), rs[~np.isnan(rs)].view(np.uint32))
+        assert np.array_equal(zps.cpu().numpy().reshape(-1), rz)
+    assert np.isnan(ops.unpack_tokens(pool, perm, T, 0)[1].cpu().numpy().reshape(H, T)[[0, 1], [3, 16]]).all()
+
+
 def test_incremental_append_equals_one_shot():
     print("case: pack in pieces 37 + 1 + 1 + 90 vs one shot", flush=True)
     from heterokv import ops

@@ -92,6 +92,38 @@ def test_edge_rows():
     assert list(oc_codes[2, :6]) == [0, 15, 8, 2, 4, 10]
 
 
+def _same_f32(a, b):
+    """Bit-equal float32 arrays, except that NaN matches any NaN."""
+    na, nb = np.isnan(a), np.isnan(b)
+    return np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+def test_nan_and_inf_rows():
+    """torch's min/max propagate NaN: a NaN group has a NaN scale and zero codes/zp."""
+    print("case: NaN / inf rows (compress, decompress)", flush=True)
+    from heterokv import KVCompressor
+    rows = np.zeros((7, 128), np.float32)
+    rows[0, 5] = np.nan
+    rows[1] = np.linspace(-3, 3, 128)
+    rows[1, 127] = np.nan
+    rows[2, 0] = np.inf
+    rows[3, 9] = -np.inf
+    rows[4, 1], rows[4, 2] = np.inf, -np.inf
+    rows[5] = np.nan
+    rows[6] = np.linspace(-3, 3, 128)
+    for dt in (torch.float32, torch.float16):
+        x = torch.from_numpy(rows).to(dt)
+        comp = KVCompressor()
+        codes, scales, zps = comp.compress(x.to(DEV))
+        oc_codes, oc_scales, oc_zps = oc.compress(x.numpy(), 128)
+        assert np.isnan(oc_scales[[0, 1, 5]]).all() and not np.isnan(oc_scales[[2, 3, 4, 6]]).any()
+        assert np.array_equal(codes.cpu().numpy(), oc_codes), dt
+        assert _same_f32(scales.cpu().numpy(), oc_scales), dt
+        assert np.array_equal(zps.cpu().numpy(), oc_zps), dt
+        deq = comp.decompress(codes, scales, zps, target_dtype=torch.float32).cpu().numpy()
+        assert _same_f32(deq, oc.decompress(oc_codes, oc_scales, oc_zps, 128, out_dtype=np.float32)), dt
+
+
 def test_division_edge_rows_and_random_fp32():
     """The per-element x / scale is computed from RN(1/scale) with one fma correction; rows
     that exercise it: infinite values (the plain-division path), values whose residual

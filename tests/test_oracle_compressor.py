@@ -135,6 +135,40 @@ def test_matches_torch_cpu_ops_random():
         assert np.array_equal(codes.reshape(-1), q.numpy())
 
 
+def test_nan_and_inf_rows_match_torch_ops():
+    """torch's min/max propagate NaN (kv_compressor.py:76-77): a group holding a NaN gets
+    a NaN scale, and its zero point and codes convert to 0 (torch's NaN -> uint8 is 0 on
+    the CPU, checked here too).  Infinite values go through the same float32 steps."""
+    assert torch.tensor([float("nan")]).to(torch.uint8).item() == 0
+    rows = np.zeros((6, 128), np.float32)
+    rows[0, 5] = np.nan
+    rows[1] = np.linspace(-3, 3, 128)
+    rows[1, 127] = np.nan
+    rows[2, 0] = np.inf
+    rows[3, 9] = -np.inf
+    rows[4, 1], rows[4, 2] = np.inf, -np.inf
+    rows[5] = np.nan
+    codes, scales, zps = oc.compress(rows, 128)
+    t = torch.from_numpy(rows)
+    s = torch.clamp((t.max(-1, keepdim=True).values - t.min(-1, keepdim=True).values) / 15, min=1e-8)
+    z = torch.clamp(torch.round(-t.min(-1, keepdim=True).values / s), 0, 15).to(torch.uint8)
+    q = torch.clamp(torch.round(t / s + z.float()), 0, 15).to(torch.uint8)
+    sr = s.reshape(-1).numpy()
+    assert np.array_equal(np.isnan(scales), np.isnan(sr))
+    assert np.array_equal(scales[~np.isnan(sr)], sr[~np.isnan(sr)])
+    assert list(np.isnan(scales)) == [True, True, False, False, False, True]
+    assert np.array_equal(zps, z.reshape(-1).numpy())
+    assert np.array_equal(codes, q.numpy())
+    assert not codes[[0, 1, 5]].any() and not zps[[0, 1, 5]].any()
+    # decompress (kv_compressor.py:131): (q - zp) * scale, so a NaN group comes back
+    # all NaN, and so does every 0-code element of a group with an infinite scale
+    deq = oc.decompress(codes, scales, zps, 128, out_dtype=np.float32)
+    ref = ((q.float() - z.float()) * s).numpy()
+    assert np.array_equal(np.isnan(deq), np.isnan(ref))
+    assert np.array_equal(deq[~np.isnan(ref)], ref[~np.isnan(ref)])
+    assert np.isnan(deq[[0, 1, 5]]).all()
+
+
 def test_bf16_input():
     rng = np.random.default_rng(2)
     x32 = rng.standard_normal(512).astype(np.float32)
