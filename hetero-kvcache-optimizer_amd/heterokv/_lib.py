@@ -13,7 +13,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libheterokv.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_U8 = 0, 1, 2, 3
 MAX_F16_ZONES = 3
 DECODE_DETERMINISTIC = 1   # HKV_DECODE_DETERMINISTIC
@@ -123,7 +123,8 @@ class PrefillArgs(ctypes.Structure):
                 ("chunk_stride_b", i64), ("chunk_stride_h", i64), ("chunk_stride_t", i64),
                 ("out", vp), ("out_stride_b", i64), ("out_stride_h", i64), ("out_stride_t", i64),
                 ("err_flag", vp), ("staging", vp), ("staging_blocks", i64),
-                ("q_dtype", i32), ("chunk_dtype", i32), ("out_dtype", i32)]
+                ("q_dtype", i32), ("chunk_dtype", i32), ("out_dtype", i32),
+                ("workspace", vp), ("workspace_bytes", ctypes.c_size_t)]
 
 
 class CopyDesc(ctypes.Structure):
@@ -152,6 +153,7 @@ SYMBOLS = [
     ("hkv_decode_workspace_bytes", ctypes.c_size_t, [i32, i32, i32, i32, i32, vp, i32]),
     ("hkv_decode_attn", ctypes.c_int, [ctypes.POINTER(DecodeArgs), vp]),
     ("hkv_decode_attn_noalloc", ctypes.c_int, [ctypes.POINTER(DecodeArgs), vp]),
+    ("hkv_prefill_workspace_bytes", ctypes.c_size_t, [i32, i32, i32]),
     ("hkv_prefill_attn", ctypes.c_int, [ctypes.POINTER(PrefillArgs), vp]),
     ("hkv_pf_create", ctypes.c_int, [i32, ctypes.c_size_t, i32, ctypes.POINTER(vp)]),
     ("hkv_pf_destroy", ctypes.c_int, [vp]),

@@ -581,16 +581,32 @@ def eviction_candidates(token_scores, seq_len, block_size, sink_tokens, local_wi
 
 
 # ----------------------------------------------------------------------- prefill attention
+_PREFILL_WS = {}
+
+
+def _prefill_workspace(dev, nbytes):
+    """Per-device scratch for the zone kernel's softmax state (no zero fill needed); grown on
+    demand.  Calls that share it are ordered on the device's current stream."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    buf = _PREFILL_WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 4096), dtype=torch.uint8, device=dev)
+        _PREFILL_WS[key] = buf
+    return buf
+
+
 def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, int4_max_len=0,
                       chunk_k=None, chunk_v=None, sm_scale=None, out=None, staging=None, err=None,
-                      out_dtype=None):
+                      out_dtype=None, workspace=None):
     """Chunked-prefill attention (hkv_prefill_attn).
 
     q: [B, Hq, Sq, 128] fp16 or bf16.  Every query attends to all fp16-zone tokens and all
     INT4 tokens, plus -- when chunk_k/chunk_v [B, Hkv, Sq, 128] (fp16 or bf16) are given --
     causally to the chunk itself.  bf16 inputs are range-checked into the error word
     (err: ErrorWord; default: the INT4 pool's).  Returns [B, Hq, Sq, 128] in out_dtype
-    (default q's dtype).
+    (default q's dtype).  workspace: a uint8 device tensor of at least
+    hkv_prefill_workspace_bytes(B, Hq, Sq) bytes, used when there are INT4 and zone or
+    chunk keys (default: a cached per-device buffer, for calls ordered on one stream).
     """
     _require_gpu(q, chunk_k, chunk_v)
     if q.dtype not in _F16_OR_BF16 or q.dim() != 4 or q.shape[-1] != HEAD_DIM:
@@ -661,5 +677,12 @@ def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, 
         a.err_flag = err.ptr()
     else:
         a.err_flag = pool_err.data_ptr() if pool_err is not None else 0
+    zone_keys = chunk_k is not None or any(int(mx) > 0 for (_, _, mx) in zones)
+    if zone_keys and int4_max_len > 0:
+        need = load().hkv_prefill_workspace_bytes(B, Hq, Sq)
+        ws = workspace if workspace is not None else _prefill_workspace(dev, need)
+        if ws.device != dev or ws.dtype != torch.uint8 or ws.numel() < need:
+            raise HeteroKVError(-1, "prefill_attention: workspace must be a uint8 tensor of %d bytes on %s" % (need, dev))
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     check(load().hkv_prefill_attn(ctypes.byref(a), stream_ptr(dev)), "hkv_prefill_attn")
     return out

@@ -78,7 +78,7 @@
 extern "C" {
 #endif
 
-#define HKV_ABI_VERSION 6
+#define HKV_ABI_VERSION 7
 
 /* dtype codes */
 #define HKV_DTYPE_F16  0
@@ -388,8 +388,14 @@ typedef struct HkvPrefillArgs {
     int32_t q_dtype;               /* F16 or BF16 */
     int32_t chunk_dtype;           /* F16 or BF16 */
     int32_t out_dtype;             /* F16 or BF16 */
+    /* Needed when there are INT4 tokens and zone or chunk tokens: the zone kernel leaves
+     * each query row's partial softmax state here for the INT4 kernel.  16-byte aligned,
+     * hkv_prefill_workspace_bytes() bytes; no zero fill needed.  NULL otherwise. */
+    void* workspace;
+    size_t workspace_bytes;
 } HkvPrefillArgs;
 
+size_t hkv_prefill_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_queries);
 int hkv_prefill_attn(const HkvPrefillArgs* args, void* stream);
 
 /*
