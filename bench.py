@@ -185,8 +185,9 @@ P_ROWS = list(range(0, 32)) + list(range(P_SQ - 32, P_SQ))   # CPU sample / pari
 
 
 def leg_c4(torch, ops, args):
-    """Chunked prefill (one hkv_prefill_attn launch): 2048 fp16 queries, 32 q / 8 kv heads, over
-    64 fp16 sink + 131072 INT4 + 4096 fp16 recent tokens plus the chunk itself, causally."""
+    """Chunked prefill (one hkv_prefill_attn call: the INT4 kernel, then the zone kernel): 2048 fp16
+    queries, 32 q / 8 kv heads, over 64 fp16 sink + 131072 INT4 + 4096 fp16 recent tokens plus the
+    chunk itself, causally."""
     from oracle import torch_ref as tr
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(4)
@@ -222,7 +223,7 @@ def leg_c4(torch, ops, args):
     tflops = P_FLOPS / (ms * 1e-3) / 1e12
     got = out[0][:, P_ROWS].float().cpu()
     blk = {"workload": "chunked prefill: 2048 fp16 queries, 32 q / 8 kv heads, head_dim 128, over 64 fp16 sink "
-                       "+ 131072 INT4 + 4096 fp16 recent + the chunk causally (one launch)",
+                       "+ 131072 INT4 + 4096 fp16 recent + the chunk causally (one hkv_prefill_attn call, two kernels)",
            "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "steps": 10,
            "flops_per_step": P_FLOPS,
            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
