@@ -19,6 +19,7 @@
 
 #include <math.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace hkv {
@@ -36,17 +37,22 @@ constexpr int kQ = kPfQ;          // query rows per wave
 constexpr int kT = kPfT;          // tokens per tile
 // One LDS tile buffer: K rows (64 tokens, 256 bytes of fp16 each, rows padded to
 // 272 bytes), V^T rows (128 dims, 64 tokens of fp16 each, padded to 144 bytes), then
-// per token the K factor (K scale x sm_scale x log2 e), the V scale and the score bias
-// (0, or -inf past the valid length), fp32.  INT4 tiles hold exact (code - zero point)
-// values and the scales are applied to the scores and the probabilities; fp16 tiles
-// hold K and V with factors (sm_scale x log2 e, 1).  The padding keeps the 16-byte
-// operand reads of 8 consecutive lanes on distinct banks, and each lane reads all its
-// operands of a tile at immediate offsets from one address.
+// per token the score bias (0, or -inf past the valid length), fp32.  K rows hold
+// (code - zero point) x K scale x sm_scale x log2 e and V^T rows (code - zero point) x
+// V scale, in fp16, so the scores come out of the MFMAs in the log2 domain (the fp16
+// rounding of each dequantized element is the one fp16 dequantization makes).  Tokens
+// past the valid length get K and V scale 0, so whatever their record slots hold, their
+// scores are 0 until the bias masks them, and their V^T rows are 0.  The padding keeps the
+// 16-byte operand reads of 8 consecutive lanes on distinct banks, and each lane reads
+// all its operands of a tile at immediate offsets from one address.
 constexpr int kKRow = kHeadDim * 2 + 16;
 constexpr int kVRow = kT * 2 + 16;
 constexpr int kVOff = kT * kKRow;
-constexpr int kSkOff = kVOff + kHeadDim * kVRow, kSvOff = kSkOff + kT * 4, kSbOff = kSvOff + kT * 4;
-constexpr int kBufBytes = kSbOff + kT * 4;
+constexpr int kDataBytes = kVOff + kHeadDim * kVRow;   // K rows + V^T rows of one tile
+// The per-token biases of the tile buffers sit together at the start of LDS, so every
+// bias read is an immediate offset from one address (offsets stop at 65535).
+constexpr int kSbOff = 0;
+constexpr int kFacBytes = kT * 4;
 
 // LDS addresses (bytes) inside a tile buffer.  K: 16-byte chunk `chunk` (dims
 // 8 chunk .. +8) of token `tok`.  V^T rows hold the tile's 64 tokens in 8-byte units
@@ -72,13 +78,14 @@ __device__ __forceinline__ int vt_pair_addr(int dim, int gr, int hh) { return kV
 //   phase X:  team 0: PV(t-1), QK(t), stage K of tile t+1     team 1: SM(t-1)
 //   phase Y:  team 0: SM(t)     team 1: PV(t-1), QK(t), stage V of tile t+1
 // with a workgroup barrier after each phase.  Three LDS tile buffers rotate: tile t-1
-// (its V and factors still read), tile t, and tile t+1 being staged.  The staging of a
-// tile is split between the teams (team 0 the K rows and K factors, team 1 V^T and the
-// V scales), so every wave dequantizes an eighth of each tile.
+// (its V^T and biases still read), tile t, and tile t+1 being staged.  The staging of
+// a tile is split between the teams (team 0 the K rows and the token biases, team 1 the
+// V^T rows), so every wave dequantizes an eighth of each tile.
 constexpr int kTeamWaves = 4;
 constexpr int kThreadsPP = 2 * kTeamWaves * 64;
 constexpr int kQB = 2 * kQ;                  // query rows per workgroup
 constexpr int kNumBufs = 3;
+constexpr int kLdsBytes = kNumBufs * (kFacBytes + kDataBytes);
 constexpr int kRing4 = 3;                    // INT4 half-tiles per thread: one staged, two in flight
 
 // Staging of INT4 tile x: wave w of a team handles block w of the tile (4 blocks of 16
@@ -105,13 +112,15 @@ __device__ __forceinline__ int block_id4(const PrefillParams& p, int nb, int b, 
     return p.bt[(int64_t)b * p.bt_stride + lb];
 }
 // Buffer resource over this wave's head part of record `id` (an out-of-range id is
-// reported and replaced by a valid record).
+// reported and replaced by a valid record).  The range check is a 32-bit unsigned
+// compare of a wave-uniform value, and the id used is read back from lane 0, so it and
+// the resource stay in scalar registers (a resource the compiler takes for divergent
+// wraps every load in a readfirstlane loop).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const PrefillParams& p, int h, int id_v) {
-    int phys = __builtin_amdgcn_readfirstlane(id_v);
-    if (phys >= 0 ? (int64_t)phys >= p.pool_blocks : (int64_t)(~phys) >= p.staging_blocks) {
-        if (p.err && (threadIdx.x & 63) == 0) atomicOr(p.err, 1);
-        phys = p.fallback_id;
-    }
+    const int id = __builtin_amdgcn_readfirstlane(id_v);
+    const bool ok = id >= 0 ? (uint32_t)id < p.pool_blocks : (uint32_t)(~id) < p.staging_blocks;
+    const int phys = __builtin_amdgcn_readfirstlane(ok ? id : p.fallback_id);
+    if (!ok && p.err && (threadIdx.x & 63) == 0) atomicOr(p.err, 1);
     const int64_t rb = (int64_t)p.Hkv * kHeadPartBytes;
     const uint8_t* part = (phys >= 0 ? p.pool + (int64_t)phys * rb : p.staging + (int64_t)(~phys) * rb) +
                           RecordLayout::part(h);
@@ -137,41 +146,46 @@ __device__ __forceinline__ void load_v4(const PrefillParams& p, int h, int id, i
     s.vs = __builtin_bit_cast(f4, bld16(r, kPartVs + g * 16));
     s.vz = bld4(r, kPartVz + g * 4);
 }
-// Writes a staged block into LDS buffer `lds` as exact fp16 (code - zero point) values
-// with its per-token factors; `valid` = valid tokens of the block.  Tokens past it hold
-// finite values (their block is a valid record) and are masked by the bias.
-__device__ __forceinline__ void store_k4(const SlotK& s, uint8_t* lds, float scale_log2, int wt, int lane, int valid) {
+// Writes a staged block into LDS buffer `lds`: K as (code - zero point) x K scale x
+// sm_scale x log2 e with the per-token biases, V as (code - zero point) x V scale;
+// `valid` = valid tokens of the block.  Tokens past it get scale 0 (their codes are
+// finite, their scales may be anything) and bias -inf.
+__device__ __forceinline__ void store_k4(const SlotK& s, uint8_t* lds, uint8_t* fac, float scale_log2, int wt, int lane,
+                                         int valid) {
     const int rr = lane >> 2, pt = lane & 3;
     const int tok = wt * 16 + rr;
     const uint32_t kz = s.kz & 0xFFu;
     const h2 kz1024 = zp1024(kz, kz), kz64 = zp64(kz, kz);
+    const _Float16 f = (_Float16)(rr < valid ? s.ks * scale_log2 : 0.0f);
+    const h2 f2 = {f, f};
     const uint32_t w4[4] = {s.w.x, s.w.y, s.w.z, s.w.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {          // word j: dims 32pt + 8j .. +8
         const NibPairs a = unpack_word(w4[j], kz1024, kz64);
         *(u4*)(lds + k_addr(tok, pt * 4 + j)) =
-            u4{__builtin_bit_cast(uint32_t, a.p0), __builtin_bit_cast(uint32_t, a.p1),
-               __builtin_bit_cast(uint32_t, a.p2), __builtin_bit_cast(uint32_t, a.p3)};
+            u4{__builtin_bit_cast(uint32_t, a.p0 * f2), __builtin_bit_cast(uint32_t, a.p1 * f2),
+               __builtin_bit_cast(uint32_t, a.p2 * f2), __builtin_bit_cast(uint32_t, a.p3 * f2)};
     }
-    if (pt == 0) {
-        ((float*)(lds + kSkOff))[tok] = s.ks * scale_log2;
-        ((float*)(lds + kSbOff))[tok] = rr < valid ? 0.0f : -INFINITY;
-    }
+    if (pt == 0) ((float*)(fac + kSbOff))[tok] = rr < valid ? 0.0f : -INFINITY;
 }
-__device__ __forceinline__ void store_v4(const SlotV& s, uint8_t* lds, int wt, int lane) {
+__device__ __forceinline__ void store_v4(const SlotV& s, uint8_t* lds, int wt, int lane, int valid) {
     // V word 4 lane + mm: x0..x3 = tokens 4g..4g+3 at dim c+32mm, x4..x7 at +16
     const int g = lane >> 4, c = lane & 15;
     const h2 z01 = zp1024(s.vz & 0xFFu, (s.vz >> 8) & 0xFFu), z23 = zp64((s.vz >> 16) & 0xFFu, s.vz >> 24);
+    const int t0 = 4 * g;
+    const h2 vs01 = {(_Float16)(t0 < valid ? s.vs.x : 0.f), (_Float16)(t0 + 1 < valid ? s.vs.y : 0.f)};
+    const h2 vs23 = {(_Float16)(t0 + 2 < valid ? s.vs.z : 0.f), (_Float16)(t0 + 3 < valid ? s.vs.w : 0.f)};
     const uint32_t v4[4] = {s.w.x, s.w.y, s.w.z, s.w.w};
     const int unit = wt * 4 + g;
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
         const NibPairs a = unpack_word(v4[mm], z01, z23);
         const int d1 = c + 32 * mm, d2 = d1 + 16;
-        *(u2*)(lds + vt_addr(d1, unit)) = u2{__builtin_bit_cast(uint32_t, a.p0), __builtin_bit_cast(uint32_t, a.p1)};
-        *(u2*)(lds + vt_addr(d2, unit)) = u2{__builtin_bit_cast(uint32_t, a.p2), __builtin_bit_cast(uint32_t, a.p3)};
+        *(u2*)(lds + vt_addr(d1, unit)) =
+            u2{__builtin_bit_cast(uint32_t, a.p0 * vs01), __builtin_bit_cast(uint32_t, a.p1 * vs23)};
+        *(u2*)(lds + vt_addr(d2, unit)) =
+            u2{__builtin_bit_cast(uint32_t, a.p2 * vs01), __builtin_bit_cast(uint32_t, a.p3 * vs23)};
     }
-    if (c == 0) *(f4*)(lds + kSvOff + (wt * 16 + 4 * g) * 4) = s.vs;
 }
 
 // QK(t): S^T[64 tok x 32 q] = K . Q^T for this wave's 32 query rows.  The two token
@@ -203,37 +217,35 @@ __device__ __forceinline__ void qk_tile(const uint8_t* cur, int n, int hh, const
     }
 }
 
-// SM(t): masked online softmax of S; P = exp2(S - m) x V scale as the P^T operands
-// (P[2 tb + u]: tokens tb*32 + 16u + 4hh .. +3 and +8 .. +11).  Lane (n, hh) holds
-// tokens tb*32 + 8j + 4hh + i for r = 4j + i: four consecutive tokens per j, whose
-// factors are one 16-byte LDS read.  The tile's bias masks tokens past its valid
-// length; kCausal also masks token t for query row qrow unless t < tvalid and
-// causal_base + t <= qrow (a zone tile passes a causal_base far below any row).
-template <bool kCausal>
-__device__ __forceinline__ void softmax_tile(const uint8_t* cur, int tvalid, int causal_base, int hh, int qrow,
-                                             f16v (&S)[2], f16v (&acc)[4], float& m, float& l, h8 (&P)[4]) {
-    float mt = -INFINITY;
+// SM(t): masked online softmax of S; P = exp2(S - m) as the P^T operands (P[2 tb + u]:
+// tokens tb*32 + 16u + 4hh .. +3 and +8 .. +11) in fp16, and the row sum adds those
+// fp16 values (two per v_dot2), the same numbers the P.V product weighs.  Lane (n, hh)
+// holds tokens tb*32 + 8j + 4hh + i for r = 4j + i: four consecutive tokens per j, whose
+// biases are one 16-byte LDS read.  `tvalid` (wave-uniform) is the tile's count of
+// valid tokens; only a sequence's last INT4 tile and the empty tiles have fewer than 64,
+// and only they add the per-token bias (-inf past the valid length).
+__device__ __forceinline__ void softmax_tile(const uint8_t* fac, int tvalid, int hh, f16v (&S)[2], f16v (&acc)[4],
+                                             float& m, float& l, h8 (&P)[4]) {
+    if (tvalid < kT) {
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
+        for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            // factors of tokens tb*32 + 8j + 4hh .. +3, one group at a time (registers)
-            const f4 fk = *(const f4*)(cur + kSkOff + (tb * 32 + 8 * j + 4 * hh) * 4);
-            const f4 fb = *(const f4*)(cur + kSbOff + (tb * 32 + 8 * j + 4 * hh) * 4);
+            for (int j = 0; j < 4; ++j) {
+                const f4 fb = *(const f4*)(fac + kSbOff + (tb * 32 + 8 * j + 4 * hh) * 4);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 4 * j + i;
-                S[tb][r] = __builtin_fmaf(S[tb][r], fk[i], fb[i]);
-                if constexpr (kCausal) {
-                    const int tok = tb * 32 + 8 * j + 4 * hh + i;
-                    if (!(tok < tvalid && causal_base + tok <= qrow)) S[tb][r] = -INFINITY;
-                }
-                mt = fmaxf(mt, S[tb][r]);
+                for (int i = 0; i < 4; ++i) S[tb][4 * j + i] += fb[i];
             }
-        }
-        __builtin_amdgcn_sched_barrier(0);
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    // four independent max chains, so the reduction is not one 16-deep dependency chain
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx[r & 3] = fmaxf(mx[r & 3], S[tb][r]);
+    float mt = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+    // the other half of the row (lanes n and n + 32) by a lane swap, not an LDS permute
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+    mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
     if (__ballot(mt > m)) {
         const float m_new = fmaxf(m, mt);
         const float alpha = (m_new > m) ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
@@ -251,16 +263,21 @@ __device__ __forceinline__ void softmax_tile(const uint8_t* cur, int tvalid, int
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
                 const int j = 2 * u + jj;
-                const f4 fv = *(const f4*)(cur + kSvOff + (tb * 32 + 8 * j + 4 * hh) * 4);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float pv = __builtin_amdgcn_exp2f(S[tb][4 * j + i] - msafe);
-                    l += pv;
-                    P[2 * tb + u][jj * 4 + i] = (_Float16)(pv * fv[i]);
-                }
+                for (int i = 0; i < 4; ++i)
+                    P[2 * tb + u][jj * 4 + i] = (_Float16)__builtin_amdgcn_exp2f(S[tb][4 * j + i] - msafe);
             }
         __builtin_amdgcn_sched_barrier(0);
     }
+    const h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+    float ls[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        ls[k] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ls[k] = __builtin_amdgcn_fdot2(h2{P[k][2 * e], P[k][2 * e + 1]}, one2, ls[k], false);
+    }
+    l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 }
 
 // PV(t): O^T[128 d x 32 q] += V^T . P^T: four independent accumulator chains (dim
@@ -293,7 +310,8 @@ __device__ __forceinline__ void phase_end() {
 struct WaveCtx {
     int b, h, wt, lane, n, hh, qrow;
 };
-#define HKV_BUF(i) (lds + (i) * kBufBytes)
+#define HKV_BUF(i) (lds + kNumBufs * kFacBytes + (i) * kDataBytes)
+#define HKV_FAC(i) (lds + (i) * kFacBytes)
 
 // INT4 tiles 0 .. n4-1 for one team; iteration t (0 .. n4) runs phases X and Y.  The
 // loop is unrolled by 3 from multiples of 3, so tile t's LDS buffer (t % 3) and staging
@@ -309,13 +327,14 @@ __device__ __forceinline__ void int4_tiles(const PrefillParams& p, const TileMap
         const int lbt = x * 4 + w.wt;
         return (x < n4 && lbt < nb4) ? min(kBlockTokens, tm.len4 - lbt * kBlockTokens) : 0;
     };
+    auto tvalid_of = [&](int x) { return (x >= 0 && x < n4) ? min(kT, tm.len4 - x * kT) : 0; };
     auto load = [&](int id, Slot& sl) {
         if constexpr (kTeam == 0) load_k4(p, w.h, id, w.lane, sl);
         else load_v4(p, w.h, id, w.lane, sl);
     };
-    auto store = [&](const Slot& sl, uint8_t* dst, int x) {
-        if constexpr (kTeam == 0) store_k4(sl, dst, p.scale_log2, w.wt, w.lane, valid_of(x));
-        else store_v4(sl, dst, w.wt, w.lane);
+    auto store = [&](const Slot& sl, uint8_t* dst, uint8_t* fac, int x) {
+        if constexpr (kTeam == 0) store_k4(sl, dst, fac, p.scale_log2, w.wt, w.lane, valid_of(x));
+        else store_v4(sl, dst, w.wt, w.lane, valid_of(x));
     };
     Slot ring[kRing4];
     int idn[kRing4];   // block id of tile x + kRing4 for the slot holding tile x
@@ -324,7 +343,7 @@ __device__ __forceinline__ void int4_tiles(const PrefillParams& p, const TileMap
         load(block_id4(p, nb4, w.b, x, w.wt), ring[x]);
         idn[x] = block_id4(p, nb4, w.b, x + kRing4, w.wt);
     }
-    store(ring[0], HKV_BUF(0), 0);
+    store(ring[0], HKV_BUF(0), HKV_FAC(0), 0);
     load(idn[0], ring[0]);
     idn[0] = block_id4(p, nb4, w.b, 2 * kRing4, w.wt);
     phase_end();
@@ -339,6 +358,9 @@ __device__ __forceinline__ void int4_tiles(const PrefillParams& p, const TileMap
             uint8_t* const prv = HKV_BUF((uu + kNumBufs - 1) % kNumBufs);
             uint8_t* const cur = HKV_BUF(uu);
             uint8_t* const nxt = HKV_BUF((uu + 1) % kNumBufs);
+            uint8_t* const prv_f = HKV_FAC((uu + kNumBufs - 1) % kNumBufs);
+            uint8_t* const cur_f = HKV_FAC(uu);
+            uint8_t* const nxt_f = HKV_FAC((uu + 1) % kNumBufs);
             // A team's MFMA phase also stages its half of tile t+1 (buffer (t+1) % 3 held
             // tile t-2, whose last reads ended in the previous iteration) and issues the
             // loads of tile t+1+kRing4: that VALU and LDS work runs while its MFMAs
@@ -347,22 +369,22 @@ __device__ __forceinline__ void int4_tiles(const PrefillParams& p, const TileMap
                 // X: PV(t-1), QK(t), stage tile t+1
                 pv_tile(prv, w.n, w.hh, P, acc);
                 qk_tile(cur, w.n, w.hh, qf, S);
-                store(ring[ks], nxt, t + 1);
+                store(ring[ks], nxt, nxt_f, t + 1);
                 __builtin_amdgcn_sched_barrier(0);
                 load(idn[ks], ring[ks]);
                 idn[ks] = block_id4(p, nb4, w.b, t + 1 + 2 * kRing4, w.wt);
                 phase_end();
                 // Y: SM(t)
-                softmax_tile<false>(cur, kT, -1, w.hh, w.qrow, S, acc, m, l, P);
+                softmax_tile(cur_f, tvalid_of(t), w.hh, S, acc, m, l, P);
                 phase_end();
             } else {
                 // X: SM(t-1)
-                softmax_tile<false>(prv, kT, -1, w.hh, w.qrow, S, acc, m, l, P);
+                softmax_tile(prv_f, tvalid_of(t - 1), w.hh, S, acc, m, l, P);
                 phase_end();
                 // Y: PV(t-1), QK(t), stage tile t+1
                 pv_tile(prv, w.n, w.hh, P, acc);
                 qk_tile(cur, w.n, w.hh, qf, S);
-                store(ring[ks], nxt, t + 1);
+                store(ring[ks], nxt, nxt_f, t + 1);
                 __builtin_amdgcn_sched_barrier(0);
                 load(idn[ks], ring[ks]);
                 idn[ks] = block_id4(p, nb4, w.b, t + 1 + 2 * kRing4, w.wt);
@@ -373,6 +395,7 @@ __device__ __forceinline__ void int4_tiles(const PrefillParams& p, const TileMap
 }
 
 #undef HKV_BUF
+#undef HKV_FAC
 
 // One workgroup per CU, 8 waves (two per SIMD), up to 256 registers per wave.
 __global__ __launch_bounds__(kThreadsPP, 1) void prefill_attn_kernel(PrefillParams p) {
@@ -427,10 +450,10 @@ __global__ __launch_bounds__(kThreadsPP, 1) void prefill_attn_kernel(PrefillPara
     for (int u = 0; u < 4; ++u)
 #pragma unroll
         for (int i = 0; i < 8; ++i) P[u][i] = (_Float16)0.f;
-    for (int o = threadIdx.x * 16; o < kBufBytes; o += kThreadsPP * 16)
-        *(u4*)(lds_raw + 2 * kBufBytes + o) = u4{0u, 0u, 0u, 0u};
+    for (int o = threadIdx.x * 16; o < kDataBytes; o += kThreadsPP * 16)
+        *(u4*)(lds_raw + kNumBufs * kFacBytes + 2 * kDataBytes + o) = u4{0u, 0u, 0u, 0u};
     __syncthreads();
-    if (threadIdx.x < kT) ((float*)(lds_raw + 2 * kBufBytes + kSbOff))[threadIdx.x] = -INFINITY;
+    if (threadIdx.x < kT) ((float*)(lds_raw + 2 * kFacBytes + kSbOff))[threadIdx.x] = -INFINITY;
     // The teams run mirrored loops (team 0 is half an iteration ahead); they meet at
     // every phase barrier.
     const WaveCtx wc{b, h, wt, lane, n, hh, qrow};
@@ -540,9 +563,9 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
         p.z[i].lens = on ? a->f16[i].lens : nullptr;
     }
     p.pool = a->pool;
-    p.pool_blocks = a->pool ? a->pool_blocks : 0;
+    p.pool_blocks = a->pool ? (uint32_t)std::min<int64_t>(a->pool_blocks, 1ll << 31) : 0u;
     p.staging = a->staging;
-    p.staging_blocks = a->staging ? a->staging_blocks : 0;
+    p.staging_blocks = a->staging ? (uint32_t)std::min<int64_t>(a->staging_blocks, 1ll << 31) : 0u;
     p.fallback_id = p.pool_blocks > 0 ? 0 : -1;
     p.bt = a->block_table;
     p.bt_stride = a->bt_stride;
@@ -581,10 +604,10 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
         static bool raised = false;   // three tile buffers exceed the 64 KB default
         if (!raised) {
             HKV_HIP_CHECK(hipFuncSetAttribute((const void*)prefill_attn_kernel,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, kNumBufs * kBufBytes));
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
             raised = true;
         }
-        hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kThreadsPP), kNumBufs * kBufBytes, (hipStream_t)stream, p);
+        hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kThreadsPP), kLdsBytes, (hipStream_t)stream, p);
         HKV_LAUNCH_CHECK("prefill_attn_kernel");
     }
     return HKV_OK;

@@ -40,9 +40,9 @@ struct PrefillParams {
     int nz;
     PfZone z[HKV_MAX_F16_ZONES];
     const uint8_t* pool;
-    int64_t pool_blocks;
-    const uint8_t* staging;      // records addressed by negative block ids
-    int64_t staging_blocks;
+    uint32_t pool_blocks;        // record counts capped at 2^31 (block ids are int32), so the
+    const uint8_t* staging;      // range check is a 32-bit scalar compare; staging records are
+    uint32_t staging_blocks;     // addressed by negative block ids
     int fallback_id;             // id substituted for an out-of-range one (a valid record)
     const int32_t* bt;
     int bt_stride;

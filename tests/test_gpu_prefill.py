@@ -15,7 +15,27 @@ DEV = "cuda:0"
 TOL = 2e-3
 
 
-def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0):
+def _poison_tails(pool, bt, mids, Hkv):
+    """Writes NaN / inf scales and zero point 255 into the unused token slots of each
+    sequence's last INT4 block (slots past its length), which the kernels must ignore."""
+    from oracle import pool_format as pf
+    data = pool.data.cpu().numpy()
+    f32 = np.array([np.nan, np.inf, -np.inf], dtype=np.float32).view(np.uint8).reshape(3, 4)
+    for b, m in enumerate(mids):
+        if m % 16 == 0:
+            continue
+        rec = data[int(bt[b, (m - 1) // 16])]
+        for h in range(Hkv):
+            o = pf.offsets(h)
+            for t in range(m % 16, 16):
+                rec[o["ks"] + 4 * t:o["ks"] + 4 * t + 4] = f32[t % 3]
+                rec[o["vs"] + 4 * t:o["vs"] + 4 * t + 4] = f32[(t + 1) % 3]
+                rec[o["kz"] + t] = 255
+                rec[o["vz"] + t] = 255
+    pool.data.copy_(torch.from_numpy(data))
+
+
+def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0, poison=False):
     from heterokv import ops
     g = torch.Generator().manual_seed(seed)
     hist = sink + max(mids) + max(recents)
@@ -54,6 +74,8 @@ def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0):
         if mids[b]:
             ops.pack_tokens(pool, K[b:b + 1, :, sink:sink + mids[b]].to(DEV), V[b:b + 1, :, sink:sink + mids[b]].to(DEV),
                             [0], bt[b:b + 1])
+    if poison:
+        _poison_tails(pool, bt, mids, Hkv)
     out = ops.prefill_attention(q.to(DEV), zones=zones, pool=pool, block_table=bt.to(DEV),
                                 int4_lens=torch.tensor(mids, dtype=torch.int32).to(DEV), int4_max_len=max(mids),
                                 chunk_k=CK.to(DEV) if causal else None, chunk_v=CV.to(DEV) if causal else None)
@@ -107,6 +129,12 @@ def test_causal_only_sharp():
 def test_ragged_batch():
     print("case: prefill B=2 ragged", flush=True)
     _case(5, 2, 8, 2, 64, 64, [1000, 17], [200, 3])
+
+
+def test_garbage_in_unused_tail_slots():
+    print("case: prefill with NaN/inf scales and zero point 255 in the slots past each INT4 length", flush=True)
+    _case(9, 2, 8, 2, 40, 16, [150, 33], [20, 5], poison=True)
+    _case(10, 1, 4, 4, 20, 0, [7], [0], causal=False, poison=True)
 
 
 def test_medium_c4_like():
