@@ -1,21 +1,18 @@
 // Chunked-prefill attention over [INT4 pool | fp16 zones | causal chunk] on MFMA: the
-// entry point, and the INT4 kernel (the zone kernel is prefill_zones.hip).
+// entry point, and the INT4 kernel (the zone kernel is prefill_zones.hip; the tile loop
+// both run is prefill_flat.h).
 //
 // Math (fused_dequant_attn.py:242-247,385-390; kernels/fused_dequant_attn.py:371-435
 // is the reference entry point): out[q] = softmax_t(q . K_t * sm_scale) V_t over every
-// INT4 token (dequantized as (code - zero point) x scale in fp32), every fp16 zone token
-// and the chunk's own tokens t <= q (causal), GQA q head i -> kv head i / n_rep.  The
-// INT4 operands are the exact integers code - zero point; the K scale multiplies the
-// score and the V scale the probability, in fp32.
+// INT4 token (dequantized as (code - zero point) x scale), every fp16 zone token and the
+// chunk's own tokens t <= q (causal), GQA q head i -> kv head i / n_rep.
 //
-// INT4 kernel.  Per wave and 64-token tile, with v_mfma_f32_32x32x16_f16:
-//   S^T[64 tok x 32 q] = K[tok][d] . Q^T      (2 token blocks x 8 k-steps)
-//   O^T[128 d x 32 q] += V^T[d][tok] . P^T    (4 dim blocks x 4 token steps)
-// The S^T accumulator of lane (query n, half h) holds tokens 8j + 4h + i, exactly the
-// 8-token k-slices the P^T operand needs, so P never leaves registers.  The workgroup
-// schedule (two teams in ping-pong) is described below.
+// INT4 tiles are staged into LDS as fp16 K rows (code - zero point) x K scale x sm_scale
+// x log2 e and V^T rows (code - zero point) x V scale, so the scores come out of the
+// MFMAs in the log2 domain; each element takes the one fp16 rounding that dequantizing
+// to fp16 takes.
 #include "nibble_decode.h"
-#include "prefill_common.h"
+#include "prefill_flat.h"
 
 #include <math.h>
 
@@ -25,74 +22,16 @@
 namespace hkv {
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef float f16v __attribute__((ext_vector_type(16)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef pu4 u4;
+typedef pf4 f4;
+typedef pu2 u2;
+typedef fh2 h2;
 
-typedef PfZone ZoneP;
-constexpr int kQ = kPfQ;          // query rows per wave
-constexpr int kT = kPfT;          // tokens per tile
-// One LDS tile buffer: K rows (64 tokens, 256 bytes of fp16 each, rows padded to
-// 272 bytes), V^T rows (128 dims, 64 tokens of fp16 each, padded to 144 bytes), then
-// per token the score bias (0, or -inf past the valid length), fp32.  K rows hold
-// (code - zero point) x K scale x sm_scale x log2 e and V^T rows (code - zero point) x
-// V scale, in fp16, so the scores come out of the MFMAs in the log2 domain (the fp16
-// rounding of each dequantized element is the one fp16 dequantization makes).  Tokens
-// past the valid length get K and V scale 0, so whatever their record slots hold, their
-// scores are 0 until the bias masks them, and their V^T rows are 0.  The padding keeps the
-// 16-byte operand reads of 8 consecutive lanes on distinct banks, and each lane reads
-// all its operands of a tile at immediate offsets from one address.
-constexpr int kKRow = kHeadDim * 2 + 16;
-constexpr int kVRow = kT * 2 + 16;
-constexpr int kVOff = kT * kKRow;
-constexpr int kDataBytes = kVOff + kHeadDim * kVRow;   // K rows + V^T rows of one tile
-// The per-token biases of the tile buffers sit together at the start of LDS, so every
-// bias read is an immediate offset from one address (offsets stop at 65535).
-constexpr int kSbOff = 0;
-constexpr int kFacBytes = kT * 4;
-
-// LDS addresses (bytes) inside a tile buffer.  K: 16-byte chunk `chunk` (dims
-// 8 chunk .. +8) of token `tok`.  V^T rows hold the tile's 64 tokens in 8-byte units
-// of 4 tokens; within each 16-token group the units are stored in the order 0, 2, 1,
-// 3, so that the 8 tokens one lane feeds to a P.V product (tokens 4hh..4hh+3 and
-// 8+4hh..8+4hh+3 of a group) are one 16-byte read.  vt_addr takes the natural unit
-// index (token / 4).
-__device__ __forceinline__ int k_addr(int tok, int chunk) { return tok * kKRow + chunk * 16; }
-__device__ __forceinline__ int vt_unit(int unit) { return (unit & ~3) | ((unit & 1) << 1) | ((unit >> 1) & 1); }
-__device__ __forceinline__ int vt_addr(int dim, int unit) { return kVOff + dim * kVRow + vt_unit(unit) * 8; }
-// The 16 bytes holding natural units 4gr + hh and 4gr + 2 + hh (gr = 16-token group).
-__device__ __forceinline__ int vt_pair_addr(int dim, int gr, int hh) { return kVOff + dim * kVRow + (2 * gr + hh) * 16; }
-
-// ---- Ping-pong schedule.  A workgroup = 8 waves = two teams of 4 waves over the same
-// kv head: team 0 takes query rows q0 .. q0 + 31, team 1 rows q0 + 32 .. q0 + 63, and
-// wave w of a team takes query head 4 grp + w of the GQA group.  Waves w and w + 4 share
-// a SIMD.  Per 64-token tile t, each team runs
-//   QK(t): S^T = K . Q^T      (16 MFMAs)
-//   SM(t): scale, mask, online softmax, P = exp2(S - m) x V scale   (VALU)
-//   PV(t): O^T += V^T . P^T   (16 MFMAs)
-// and the teams are half an iteration apart, so one team's MFMAs run beside the
-// other's VALU work on every SIMD:
-//   phase X:  team 0: PV(t-1), QK(t), stage K of tile t+1     team 1: SM(t-1)
-//   phase Y:  team 0: SM(t)     team 1: PV(t-1), QK(t), stage V of tile t+1
-// with a workgroup barrier after each phase.  Three LDS tile buffers rotate: tile t-1
-// (its V^T and biases still read), tile t, and tile t+1 being staged.  The staging of
-// a tile is split between the teams (team 0 the K rows and the token biases, team 1 the
-// V^T rows), so every wave dequantizes an eighth of each tile.
-constexpr int kTeamWaves = 4;
-constexpr int kThreadsPP = 2 * kTeamWaves * 64;
-constexpr int kQB = 2 * kQ;                  // query rows per workgroup
-constexpr int kNumBufs = 3;
-constexpr int kLdsBytes = kNumBufs * (kFacBytes + kDataBytes);
-constexpr int kRing4 = 3;                    // INT4 half-tiles per thread: one staged, two in flight
-
-// Staging of INT4 tile x: wave w of a team handles block w of the tile (4 blocks of 16
-// tokens), so the block id and record address are wave-uniform (scalar registers,
-// one buffer resource per block).  Team 0 lane i: K codes of token i/4, dims
-// 32(i%4)..+32, with that row's scale and zero point.  Team 1 lane i: V word 4i..4i+3,
-// with the V scales and zero points of tokens 4g..4g+3, g = i/16.
+// Staging of INT4 tile x: wave wt of a team handles block wt of the tile (4 blocks of
+// 16 tokens), so the block id and record address are wave-uniform (scalar registers,
+// one buffer resource per block).  Waves 0-3 lane i: K codes of token i/4, dims
+// 32(i%4)..+32, with that row's scale and zero point.  Waves 4-7 lane i: V word
+// 4i..4i+3, with the V scales and zero points of tokens 4g..4g+3, g = i/16.
 struct SlotK {
     u4 w;
     float ks;
@@ -105,8 +44,8 @@ struct SlotV {
 };
 
 // Block id of this wave's block of INT4 tile x (clamped to the last block), the same in
-// every lane.  It stays a vector register until it is used, kRing4 tiles later, so no
-// wait for this load sits behind the record loads issued before it.
+// every lane.  It stays a vector register until it is used two tiles later, so no wait
+// for this load sits behind the record loads issued before it.
 __device__ __forceinline__ int block_id4(const PrefillParams& p, int nb, int b, int x, int wt) {
     const int lb = min(x * 4 + wt, nb - 1);
     return p.bt[(int64_t)b * p.bt_stride + lb];
@@ -146,12 +85,12 @@ __device__ __forceinline__ void load_v4(const PrefillParams& p, int h, int id, i
     s.vs = __builtin_bit_cast(f4, bld16(r, kPartVs + g * 16));
     s.vz = bld4(r, kPartVz + g * 4);
 }
-// Writes a staged block into LDS buffer `lds`: K as (code - zero point) x K scale x
-// sm_scale x log2 e with the per-token biases, V as (code - zero point) x V scale;
-// `valid` = valid tokens of the block.  Tokens past it get scale 0 (their codes are
-// finite, their scales may be anything) and bias -inf.
-__device__ __forceinline__ void store_k4(const SlotK& s, uint8_t* lds, uint8_t* fac, float scale_log2, int wt, int lane,
-                                         int valid) {
+// Writes a staged block into LDS: K as (code - zero point) x K scale x sm_scale x log2 e
+// with the per-token biases, V as (code - zero point) x V scale; `valid` = valid tokens
+// of the block.  Tokens past it get scale 0 (their codes are finite, their scales may be
+// anything) and bias -inf.
+__device__ __forceinline__ void store_k4(const SlotK& s, uint8_t* lds, uint8_t* bias, float scale_log2, int wt,
+                                         int lane, int valid) {
     const int rr = lane >> 2, pt = lane & 3;
     const int tok = wt * 16 + rr;
     const uint32_t kz = s.kz & 0xFFu;
@@ -166,7 +105,7 @@ __device__ __forceinline__ void store_k4(const SlotK& s, uint8_t* lds, uint8_t* 
             u4{__builtin_bit_cast(uint32_t, a.p0 * f2), __builtin_bit_cast(uint32_t, a.p1 * f2),
                __builtin_bit_cast(uint32_t, a.p2 * f2), __builtin_bit_cast(uint32_t, a.p3 * f2)};
     }
-    if (pt == 0) ((float*)(fac + kSbOff))[tok] = rr < valid ? 0.0f : -INFINITY;
+    if (pt == 0) ((float*)bias)[tok] = rr < valid ? 0.0f : -INFINITY;
 }
 __device__ __forceinline__ void store_v4(const SlotV& s, uint8_t* lds, int wt, int lane, int valid) {
     // V word 4 lane + mm: x0..x3 = tokens 4g..4g+3 at dim c+32mm, x4..x7 at +16
@@ -188,277 +127,90 @@ __device__ __forceinline__ void store_v4(const SlotV& s, uint8_t* lds, int wt, i
     }
 }
 
-// QK(t): S^T[64 tok x 32 q] = K . Q^T for this wave's 32 query rows.  The two token
-// blocks' accumulators form two independent MFMA chains, issued alternately, and each
-// step's K operands are read two steps ahead, so neither the chain's result latency
-// nor the LDS latency stalls the MFMA pipe.  (Scheduling barriers keep this order.)
-__device__ __forceinline__ void qk_tile(const uint8_t* cur, int n, int hh, const h8 (&qf)[8], f16v (&S)[2]) {
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) S[tb][r] = 0.f;
-    const uint8_t* k0 = cur + k_addr(n, hh);          // token n, chunk hh; step s adds 32 s bytes
-    const uint8_t* k1 = cur + k_addr(32 + n, hh);
-    h8 a0[3], a1[3];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        a0[s] = __builtin_bit_cast(h8, *(const u4*)(k0 + 32 * s));
-        a1[s] = __builtin_bit_cast(h8, *(const u4*)(k1 + 32 * s));
-    }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        if (s + 2 < 8) {
-            a0[(s + 2) % 3] = __builtin_bit_cast(h8, *(const u4*)(k0 + 32 * (s + 2)));
-            a1[(s + 2) % 3] = __builtin_bit_cast(h8, *(const u4*)(k1 + 32 * (s + 2)));
-        }
-        S[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0[s % 3], qf[s], S[0], 0, 0, 0);
-        S[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[s % 3], qf[s], S[1], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-// SM(t): masked online softmax of S; P = exp2(S - m) as the P^T operands (P[2 tb + u]:
-// tokens tb*32 + 16u + 4hh .. +3 and +8 .. +11) in fp16, and the row sum adds those
-// fp16 values (two per v_dot2), the same numbers the P.V product weighs.  Lane (n, hh)
-// holds tokens tb*32 + 8j + 4hh + i for r = 4j + i: four consecutive tokens per j, whose
-// biases are one 16-byte LDS read.  `tvalid` (wave-uniform) is the tile's count of
-// valid tokens; only a sequence's last INT4 tile and the empty tiles have fewer than 64,
-// and only they add the per-token bias (-inf past the valid length).
-__device__ __forceinline__ void softmax_tile(const uint8_t* fac, int tvalid, int hh, f16v (&S)[2], f16v (&acc)[4],
-                                             float& m, float& l, h8 (&P)[4]) {
-    if (tvalid < kT) {
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f4 fb = *(const f4*)(fac + kSbOff + (tb * 32 + 8 * j + 4 * hh) * 4);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) S[tb][4 * j + i] += fb[i];
-            }
-    }
-    // four independent max chains, so the reduction is not one 16-deep dependency chain
-    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx[r & 3] = fmaxf(mx[r & 3], S[tb][r]);
-    float mt = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
-    // the other half of the row (lanes n and n + 32) by a lane swap, not an LDS permute
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-    mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    if (__ballot(mt > m)) {
-        const float m_new = fmaxf(m, mt);
-        const float alpha = (m_new > m) ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-        l *= alpha;
-        m = m_new;
-    }
-    const float msafe = (m == -INFINITY) ? 0.f : m;
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                const int j = 2 * u + jj;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    P[2 * tb + u][jj * 4 + i] = (_Float16)__builtin_amdgcn_exp2f(S[tb][4 * j + i] - msafe);
-            }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    const h2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
-    float ls[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        ls[k] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ls[k] = __builtin_amdgcn_fdot2(h2{P[k][2 * e], P[k][2 * e + 1]}, one2, ls[k], false);
-    }
-    l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-}
-
-// PV(t): O^T[128 d x 32 q] += V^T . P^T: four independent accumulator chains (dim
-// blocks); each token group's V^T operands are read one group ahead.
-__device__ __forceinline__ void pv_tile(const uint8_t* cur, int n, int hh, const h8 (&P)[4], f16v (&acc)[4]) {
-    h8 a[2][4];
-#pragma unroll
-    for (int db = 0; db < 4; ++db) a[0][db] = __builtin_bit_cast(h8, *(const u4*)(cur + vt_pair_addr(32 * db + n, 0, hh)));
-#pragma unroll
-    for (int gr = 0; gr < 4; ++gr) {
-        if (gr + 1 < 4) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-                a[(gr + 1) & 1][db] = __builtin_bit_cast(h8, *(const u4*)(cur + vt_pair_addr(32 * db + n, gr + 1, hh)));
-        }
-#pragma unroll
-        for (int db = 0; db < 4; ++db) acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[gr & 1][db], P[gr], acc[db], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-// One ping-pong iteration boundary.  The scheduling barrier keeps each phase's work on
-// its side of the workgroup barrier.
-__device__ __forceinline__ void phase_end() {
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-struct WaveCtx {
-    int b, h, wt, lane, n, hh, qrow;
-};
-#define HKV_BUF(i) (lds + kNumBufs * kFacBytes + (i) * kDataBytes)
-#define HKV_FAC(i) (lds + (i) * kFacBytes)
-
-// INT4 tiles 0 .. n4-1 for one team; iteration t (0 .. n4) runs phases X and Y.  The
-// loop is unrolled by 3 from multiples of 3, so tile t's LDS buffer (t % 3) and staging
-// slot are compile-time.  Both teams execute the same number of barriers.
+// The INT4 staging policy of the tile loop: two register slots per wave (the records
+// of tiles t+2 and t+3 in flight while tile t is attended), block ids fetched one slot
+// cycle ahead of their records.
 template <int kTeam>
-__device__ __forceinline__ void int4_tiles(const PrefillParams& p, const TileMap& tm, const WaveCtx& w, uint8_t* lds,
-                                           const h8 (&qf)[8], f16v (&acc)[4], float& m, float& l, f16v (&S)[2],
-                                           h8 (&P)[4]) {
+struct Int4Stage {
+    static constexpr int kRing = 2;
     typedef typename std::conditional<kTeam == 0, SlotK, SlotV>::type Slot;
-    const int n4 = tm.n4;
-    const int nb4 = (tm.len4 + kBlockTokens - 1) / kBlockTokens;
-    auto valid_of = [&](int x) {
-        const int lbt = x * 4 + w.wt;
-        return (x < n4 && lbt < nb4) ? min(kBlockTokens, tm.len4 - lbt * kBlockTokens) : 0;
-    };
-    auto tvalid_of = [&](int x) { return (x >= 0 && x < n4) ? min(kT, tm.len4 - x * kT) : 0; };
-    auto load = [&](int id, Slot& sl) {
+    const PrefillParams& p;
+    const TileMap& tm;
+    const FlatWave& w;
+    int nb4;
+    Slot ring[kRing];
+    int idn[kRing];   // block id of the tile next loaded into each slot
+
+    __device__ Int4Stage(const PrefillParams& p_, const TileMap& tm_, const FlatWave& w_)
+        : p(p_), tm(tm_), w(w_), nb4((tm_.len4 + kBlockTokens - 1) / kBlockTokens) {}
+    // valid tokens of this wave's block of tile x and of tile x, branch-free (0 past the end)
+    __device__ int valid(int x) const { return min(kBlockTokens, max(0, tm.len4 - (x * 4 + w.wt) * kBlockTokens)); }
+    __device__ int tvalid(int x) const { return min(kPfT, max(0, tm.len4 - x * kPfT)); }
+    __device__ void load(int id, Slot& sl) const {
         if constexpr (kTeam == 0) load_k4(p, w.h, id, w.lane, sl);
         else load_v4(p, w.h, id, w.lane, sl);
-    };
-    auto store = [&](const Slot& sl, uint8_t* dst, uint8_t* fac, int x) {
-        if constexpr (kTeam == 0) store_k4(sl, dst, fac, p.scale_log2, w.wt, w.lane, valid_of(x));
-        else store_v4(sl, dst, w.wt, w.lane, valid_of(x));
-    };
-    Slot ring[kRing4];
-    int idn[kRing4];   // block id of tile x + kRing4 for the slot holding tile x
-#pragma unroll
-    for (int x = 0; x < kRing4; ++x) {
-        load(block_id4(p, nb4, w.b, x, w.wt), ring[x]);
-        idn[x] = block_id4(p, nb4, w.b, x + kRing4, w.wt);
     }
-    store(ring[0], HKV_BUF(0), HKV_FAC(0), 0);
-    load(idn[0], ring[0]);
-    idn[0] = block_id4(p, nb4, w.b, 2 * kRing4, w.wt);
-    phase_end();
-    // Every iteration does the same work: the first reads the empty tile -1 (buffer 2),
-    // and iterations past the last tile read empty tiles (re-read records, no valid
-    // token), so no MFMA or accumulator update sits behind a branch.
-    for (int t0 = 0; t0 <= n4; t0 += kNumBufs) {
+    __device__ void stage(int s, uint8_t* buf, uint8_t* bias, int x) const {
+        if constexpr (kTeam == 0) store_k4(ring[s], buf, bias, p.scale_log2, w.wt, w.lane, valid(x));
+        else store_v4(ring[s], buf, w.wt, w.lane, valid(x));
+    }
+    __device__ void refill(int s, int x) {   // tile x just staged from slot s
+        load(idn[s], ring[s]);
+        idn[s] = block_id4(p, nb4, w.b, x + 2 * kRing, w.wt);
+    }
+    __device__ void start(uint8_t* lds) {
 #pragma unroll
-        for (int uu = 0; uu < kNumBufs; ++uu) {
-            const int t = t0 + uu;
-            const int ks = (uu + 1) % kRing4;   // slot of tile t + 1
-            uint8_t* const prv = HKV_BUF((uu + kNumBufs - 1) % kNumBufs);
-            uint8_t* const cur = HKV_BUF(uu);
-            uint8_t* const nxt = HKV_BUF((uu + 1) % kNumBufs);
-            uint8_t* const prv_f = HKV_FAC((uu + kNumBufs - 1) % kNumBufs);
-            uint8_t* const cur_f = HKV_FAC(uu);
-            uint8_t* const nxt_f = HKV_FAC((uu + 1) % kNumBufs);
-            // A team's MFMA phase also stages its half of tile t+1 (buffer (t+1) % 3 held
-            // tile t-2, whose last reads ended in the previous iteration) and issues the
-            // loads of tile t+1+kRing4: that VALU and LDS work runs while its MFMAs
-            // execute, and the other phase is the softmax alone.
-            if constexpr (kTeam == 0) {
-                // X: PV(t-1), QK(t), stage tile t+1
-                pv_tile(prv, w.n, w.hh, P, acc);
-                qk_tile(cur, w.n, w.hh, qf, S);
-                store(ring[ks], nxt, nxt_f, t + 1);
-                __builtin_amdgcn_sched_barrier(0);
-                load(idn[ks], ring[ks]);
-                idn[ks] = block_id4(p, nb4, w.b, t + 1 + 2 * kRing4, w.wt);
-                phase_end();
-                // Y: SM(t)
-                softmax_tile(cur_f, tvalid_of(t), w.hh, S, acc, m, l, P);
-                phase_end();
-            } else {
-                // X: SM(t-1)
-                softmax_tile(prv_f, tvalid_of(t - 1), w.hh, S, acc, m, l, P);
-                phase_end();
-                // Y: PV(t-1), QK(t), stage tile t+1
-                pv_tile(prv, w.n, w.hh, P, acc);
-                qk_tile(cur, w.n, w.hh, qf, S);
-                store(ring[ks], nxt, nxt_f, t + 1);
-                __builtin_amdgcn_sched_barrier(0);
-                load(idn[ks], ring[ks]);
-                idn[ks] = block_id4(p, nb4, w.b, t + 1 + 2 * kRing4, w.wt);
-                phase_end();
-            }
+        for (int x = 0; x < kRing; ++x) {
+            load(block_id4(p, nb4, w.b, x, w.wt), ring[x]);
+            idn[x] = block_id4(p, nb4, w.b, x + kRing, w.wt);
+        }
+#pragma unroll
+        for (int x = 0; x < kRing; ++x) {
+            stage(x, flat_buf(lds, x), flat_bias(lds, x), x);
+            refill(x, x);
         }
     }
-}
+    __device__ void mask(int, pf16v (&)[2]) const {}
+};
 
-#undef HKV_BUF
-#undef HKV_FAC
-
-// One workgroup per CU, 8 waves (two per SIMD), up to 256 registers per wave.
-__global__ __launch_bounds__(kThreadsPP, 1) void prefill_attn_kernel(PrefillParams p) {
+// One workgroup per CU: 8 waves (two per SIMD), up to 256 registers per wave, over one
+// kv head and 64 query rows; waves 0-3 stage K, waves 4-7 stage V^T.
+__global__ __launch_bounds__(kFlatThreads, 1) void prefill_attn_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     const int b = blockIdx.z;
-    const int ngrp = (p.nrep + kTeamWaves - 1) / kTeamWaves;
+    const int ngrp = (p.nrep + 3) / 4;
     const int h = blockIdx.y / ngrp, grp = blockIdx.y % ngrp;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int team = wave >> 2, wt = wave & 3;
-    const int q0 = blockIdx.x * kQB + team * kQ;
     const int n = lane & 31, hh = lane >> 5;
-    const int rep = grp * kTeamWaves + wt;
+    const int rep = grp * 4 + wt;
     const bool head_ok = rep < p.nrep;
     const int qh = h * p.nrep + (head_ok ? rep : 0);
-    const int qrow = q0 + n;
+    const int qrow = (int)blockIdx.x * kFlatQ + team * kPfQ + n;
 
     TileMap tm;
-    make_tile_map(p, b, (int)blockIdx.x * kQB + kQB, tm);
+    make_tile_map(p, b, (int)blockIdx.x * kFlatQ + kFlatQ, tm);
     // a sequence with no INT4 token was finished by the zone kernel
     if (tm.n4 == 0) return;
 
-    // Q^T fragments: lane (query n, half hh) step s -> q[qrow][16s + 8hh .. +8]
-    h8 qf[8];
-    {
-        const bool ok = head_ok && qrow < p.Sq;
-        const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)qh * p.q_sh + (int64_t)(ok ? qrow : 0) * p.q_st + 8 * hh;
-        bool over = false;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            u4 w = ok ? *(const u4*)(qp + 16 * s) : u4{0u, 0u, 0u, 0u};
-            if (p.q_bf16) w = bf16x8_to_f16(w, over);
-            qf[s] = __builtin_bit_cast(h8, w);
-        }
-        if (__ballot(over) && lane == 0 && p.err) atomicOr(p.err, HKV_ERR_BIT_RANGE);
-    }
-    f16v acc[4];
+    ph8 qf[8];
+    flat_load_q(p, b, qh, head_ok && qrow < p.Sq, qrow, hh, 1.0f, qf);
+    pf16v acc[4];
     float m = -INFINITY, l = 0.f;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
-    // S and P start at zero and LDS buffer 2 as an empty tile (finite values, every token
-    // masked): the first iteration's softmax and P.V of tile -1 then change nothing.
-    f16v S[2];
-    h8 P[4];
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) S[tb][r] = 0.f;
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) P[u][i] = (_Float16)0.f;
-    for (int o = threadIdx.x * 16; o < kDataBytes; o += kThreadsPP * 16)
-        *(u4*)(lds_raw + kNumBufs * kFacBytes + 2 * kDataBytes + o) = u4{0u, 0u, 0u, 0u};
-    __syncthreads();
-    if (threadIdx.x < kT) ((float*)(lds_raw + 2 * kFacBytes + kSbOff))[threadIdx.x] = -INFINITY;
-    // The teams run mirrored loops (team 0 is half an iteration ahead); they meet at
-    // every phase barrier.
-    const WaveCtx wc{b, h, wt, lane, n, hh, qrow};
-    if (team == 0) int4_tiles<0>(p, tm, wc, lds_raw, qf, acc, m, l, S, P);
-    else int4_tiles<1>(p, tm, wc, lds_raw, qf, acc, m, l, S, P);
+    const FlatWave fw{b, h, wt, lane, n, hh, qrow};
+    const int T = (tm.n4 + kFlatBufs - 1) / kFlatBufs * kFlatBufs;
+    if (team == 0) {
+        Int4Stage<0> pol(p, tm, fw);
+        flat_tiles(pol, fw, lds_raw, qf, acc, m, l, T);
+    } else {
+        Int4Stage<1> pol(p, tm, fw);
+        flat_tiles(pol, fw, lds_raw, qf, acc, m, l, T);
+    }
 
     l += __shfl_xor(l, 32);
     if (!(head_ok && qrow < p.Sq)) return;
@@ -537,7 +289,7 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
                         "hkv_prefill_attn: zone %d k/v null or misaligned", i);
     }
     const int nrep = a->num_q_heads / a->num_kv_heads;
-    const int ngrp = (nrep + kTeamWaves - 1) / kTeamWaves;
+    const int ngrp = (nrep + 3) / 4;
     HKV_REQUIRE((int64_t)a->num_kv_heads * ngrp < 65536 && a->batch < 65536, HKV_ERR_ARG,
                 "hkv_prefill_attn: grid too large");
     PrefillParams p;
@@ -581,39 +333,77 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
     p.o_sh = a->out_stride_h;
     p.o_st = a->out_stride_t;
     p.err = a->err_flag;
-    p.state = (float*)a->workspace;
     // Which kernels run: the zone kernel whenever a sequence may have zone or chunk keys
     // or no INT4 token (it then writes the output), the INT4 kernel whenever there are
     // INT4 tokens; with both kinds of keys the zone kernel's state crosses the workspace.
+    // The workspace holds that state, then the chunk's K/V in the zone layout (K rows,
+    // 16-token V tiles), written by the zone writer before the zone kernel runs.
     bool zone_keys = a->chunk_k != nullptr;
     for (int i = 0; i < a->num_f16_zones; ++i) zone_keys = zone_keys || a->f16[i].max_len > 0;
     const bool int4_keys = a->int4_max_len > 0;
     const bool run_zones = zone_keys || !int4_keys || a->int4_lens != nullptr;
-    if (zone_keys && int4_keys) {
+    const size_t state_bytes = (size_t)a->batch * a->num_q_heads * a->num_queries * kStateFloats * sizeof(float);
+    const int ccap = (a->num_queries + kBlockTokens - 1) / kBlockTokens * kBlockTokens;
+    const size_t chunk_bytes = (size_t)a->batch * a->num_kv_heads * ccap * kHeadDim * 2;
+    if (a->chunk_k != nullptr || (zone_keys && int4_keys)) {
         const size_t need = hkv_prefill_workspace_bytes(a->batch, a->num_q_heads, a->num_queries);
         HKV_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= need && (((uintptr_t)a->workspace) & 15) == 0,
-                    HKV_ERR_ARG, "hkv_prefill_attn: INT4 and zone/chunk keys need a 16-byte aligned workspace of "
-                    "%zu bytes (hkv_prefill_workspace_bytes), got %zu", need, a->workspace ? a->workspace_bytes : 0);
+                    HKV_ERR_ARG, "hkv_prefill_attn: a causal chunk, or INT4 and zone keys, need a 16-byte aligned "
+                    "workspace of %zu bytes (hkv_prefill_workspace_bytes), got %zu", need,
+                    a->workspace ? a->workspace_bytes : 0);
+    }
+    p.state = (float*)a->workspace;
+    p.czk = nullptr;
+    p.czv = nullptr;
+    p.ccap = ccap;
+    if (a->chunk_k != nullptr) {
+        uint8_t* ws = (uint8_t*)a->workspace + state_bytes;
+        p.czk = (const uint16_t*)ws;
+        p.czv = (const uint16_t*)(ws + chunk_bytes);
+        HkvZoneWriteArgs zw = {};
+        zw.k = a->chunk_k;
+        zw.v = a->chunk_v;
+        zw.src_stride_b = a->chunk_stride_b;
+        zw.src_stride_h = a->chunk_stride_h;
+        zw.src_stride_t = a->chunk_stride_t;
+        zw.batch = a->batch;
+        zw.num_kv_heads = a->num_kv_heads;
+        zw.head_dim = kHeadDim;
+        zw.num_tokens = a->num_queries;
+        zw.slot_start = nullptr;
+        zw.capacity = ccap;
+        zw.ring = 0;
+        zw.zone_k = (uint16_t*)ws;
+        zw.zone_v = (uint16_t*)(ws + chunk_bytes);
+        zw.slot_base = 0;
+        zw.dtype = a->chunk_dtype;
+        zw.err_flag = a->err_flag;
+        const int rc = hkv_zone_write(&zw, stream);
+        if (rc != HKV_OK) return rc;
     }
     if (run_zones) {
         const int rc = launch_prefill_zones(p, ngrp, (hipStream_t)stream);
         if (rc != HKV_OK) return rc;
     }
     if (int4_keys) {
-        const dim3 grid((a->num_queries + kQB - 1) / kQB, a->num_kv_heads * ngrp, a->batch);
-        static bool raised = false;   // three tile buffers exceed the 64 KB default
+        const dim3 grid((a->num_queries + kFlatQ - 1) / kFlatQ, a->num_kv_heads * ngrp, a->batch);
+        static bool raised = false;   // four tile buffers exceed the 64 KB default
         if (!raised) {
             HKV_HIP_CHECK(hipFuncSetAttribute((const void*)prefill_attn_kernel,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes));
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, kFlatLdsBytes));
             raised = true;
         }
-        hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kThreadsPP), kLdsBytes, (hipStream_t)stream, p);
+        hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kFlatThreads), kFlatLdsBytes, (hipStream_t)stream, p);
         HKV_LAUNCH_CHECK("prefill_attn_kernel");
     }
     return HKV_OK;
 }
 
+// The state of every (sequence, query head, query row), then the causal chunk's K rows
+// and V tiles in the zone layout (sized with the query heads, which bound the kv heads).
 extern "C" size_t hkv_prefill_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_queries) {
     if (batch <= 0 || num_q_heads <= 0 || num_queries <= 0) return 0;
-    return (size_t)batch * (size_t)num_q_heads * (size_t)num_queries * kStateFloats * sizeof(float);
+    const size_t ccap = ((size_t)num_queries + kBlockTokens - 1) / kBlockTokens * kBlockTokens;
+    return (size_t)batch * (size_t)num_q_heads * (size_t)num_queries * kStateFloats * sizeof(float) +
+           2 * (size_t)batch * (size_t)num_q_heads * ccap * kHeadDim * 2;
 }

@@ -55,6 +55,9 @@ struct PrefillParams {
     int64_t o_sb, o_sh, o_st;
     int* err;
     float* state;                // [B][Hq][Sq][kStateFloats] zone-kernel state (may be null)
+    const uint16_t* czk;         // the causal chunk in the zone layout: K rows [B*Hkv][ccap][128]
+    const uint16_t* czv;         // and V tiles [B*Hkv][ccap/16][16 x 128] (null without a chunk)
+    int ccap;
 };
 
 // Tile counts of one sequence: INT4 tiles, each zone's tiles, and the causal chunk's

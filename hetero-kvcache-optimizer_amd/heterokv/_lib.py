@@ -13,7 +13,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libheterokv.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_U8 = 0, 1, 2, 3
 MAX_F16_ZONES = 3
 DECODE_DETERMINISTIC = 1   # HKV_DECODE_DETERMINISTIC

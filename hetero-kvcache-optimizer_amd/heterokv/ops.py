@@ -585,8 +585,9 @@ _PREFILL_WS = {}
 
 
 def _prefill_workspace(dev, nbytes):
-    """Per-device scratch for the zone kernel's softmax state (no zero fill needed); grown on
-    demand.  Calls that share it are ordered on the device's current stream."""
+    """Per-device scratch for the chunk in the zone layout and the zone kernel's softmax
+    state (no zero fill needed); grown on demand.  Calls that share it are ordered on the
+    device's current stream."""
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     buf = _PREFILL_WS.get(key)
     if buf is None or buf.numel() < nbytes:
@@ -605,8 +606,8 @@ def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, 
     causally to the chunk itself.  bf16 inputs are range-checked into the error word
     (err: ErrorWord; default: the INT4 pool's).  Returns [B, Hq, Sq, 128] in out_dtype
     (default q's dtype).  workspace: a uint8 device tensor of at least
-    hkv_prefill_workspace_bytes(B, Hq, Sq) bytes, used when there are INT4 and zone or
-    chunk keys (default: a cached per-device buffer, for calls ordered on one stream).
+    hkv_prefill_workspace_bytes(B, Hq, Sq) bytes, used with a causal chunk or with INT4 and
+    zone keys (default: a cached per-device buffer, for calls ordered on one stream).
     """
     _require_gpu(q, chunk_k, chunk_v)
     if q.dtype not in _F16_OR_BF16 or q.dim() != 4 or q.shape[-1] != HEAD_DIM:
@@ -678,7 +679,7 @@ def prefill_attention(q, zones=(), pool=None, block_table=None, int4_lens=None, 
     else:
         a.err_flag = pool_err.data_ptr() if pool_err is not None else 0
     zone_keys = chunk_k is not None or any(int(mx) > 0 for (_, _, mx) in zones)
-    if zone_keys and int4_max_len > 0:
+    if chunk_k is not None or (zone_keys and int4_max_len > 0):
         need = load().hkv_prefill_workspace_bytes(B, Hq, Sq)
         ws = workspace if workspace is not None else _prefill_workspace(dev, need)
         if ws.device != dev or ws.dtype != torch.uint8 or ws.numel() < need:

@@ -78,7 +78,7 @@
 extern "C" {
 #endif
 
-#define HKV_ABI_VERSION 7
+#define HKV_ABI_VERSION 8
 
 /* dtype codes */
 #define HKV_DTYPE_F16  0
@@ -388,8 +388,9 @@ typedef struct HkvPrefillArgs {
     int32_t q_dtype;               /* F16 or BF16 */
     int32_t chunk_dtype;           /* F16 or BF16 */
     int32_t out_dtype;             /* F16 or BF16 */
-    /* Needed when there are INT4 tokens and zone or chunk tokens: the zone kernel leaves
-     * each query row's partial softmax state here for the INT4 kernel.  16-byte aligned,
+    /* Needed with a causal chunk, or with INT4 tokens and zone tokens: the chunk's K/V
+     * are rewritten here in the zone layout, and the zone kernel leaves each query row's
+     * partial softmax state here for the INT4 kernel.  16-byte aligned,
      * hkv_prefill_workspace_bytes() bytes; no zero fill needed.  NULL otherwise. */
     void* workspace;
     size_t workspace_bytes;

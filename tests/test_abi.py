@@ -32,7 +32,7 @@ def test_header_symbols_exported(lib):
 
 
 def test_version_and_record_size(lib):
-    assert lib.hkv_abi_version() == 7
+    assert lib.hkv_abi_version() == 8
     assert lib.hkv_block_bytes(8, 128) == 17664
     assert lib.hkv_block_bytes(4, 128) == 8832
     assert lib.hkv_block_bytes(8, 64) == -1
@@ -201,11 +201,16 @@ def test_prefill_argument_errors(lib):
     a.f16[0] = _lib.F16Zone(k=4100, v=4096, capacity=64, max_len=64, lens=None)
     _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"misaligned")
     # INT4 and zone keys: the zone kernel's state needs a workspace of the documented size
+    # (state rows, then the chunk's K rows and V tiles at 16-token capacity)
     a.f16[0] = _lib.F16Zone(k=4096, v=4096, capacity=64, max_len=64, lens=None)
     need = lib.hkv_prefill_workspace_bytes(1, 32, 4)
-    assert need == 1 * 32 * 4 * 132 * 4 and lib.hkv_prefill_workspace_bytes(0, 32, 4) == 0
+    assert need == 1 * 32 * 4 * 132 * 4 + 2 * 32 * 16 * 128 * 2 and lib.hkv_prefill_workspace_bytes(0, 32, 4) == 0
     _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"workspace")
     a.workspace, a.workspace_bytes = 1 << 20, need - 1
+    _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"workspace")
+    # a causal chunk alone needs it too (its K/V are rewritten in the zone layout)
+    a.num_f16_zones, a.int4_max_len, a.workspace, a.workspace_bytes = 0, 0, None, 0
+    a.chunk_k, a.chunk_v = 16384, 16384
     _err(lib, lib.hkv_prefill_attn(ctypes.byref(a), None), -1, b"workspace")
 
 
