@@ -208,8 +208,12 @@ __global__ __launch_bounds__(kFlatThreads, 1) void prefill_attn_kernel(PrefillPa
         Int4Stage<0> pol(p, tm, fw);
         flat_tiles(pol, fw, lds_raw, qf, acc, m, l, T);
     } else {
+        // waves 4-7 (the V^T staging, the larger share of VALU work) win issue ties
+        // against the older waves 0-3 on their SIMDs
+        __builtin_amdgcn_s_setprio(1);
         Int4Stage<1> pol(p, tm, fw);
         flat_tiles(pol, fw, lds_raw, qf, acc, m, l, T);
+        __builtin_amdgcn_s_setprio(0);
     }
 
     l += __shfl_xor(l, 32);
