@@ -35,7 +35,7 @@ def _poison_tails(pool, bt, mids, Hkv):
     pool.data.copy_(torch.from_numpy(data))
 
 
-def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0, poison=False):
+def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0, poison=False, io_dtype=torch.float16):
     from heterokv import ops
     g = torch.Generator().manual_seed(seed)
     hist = sink + max(mids) + max(recents)
@@ -43,9 +43,10 @@ def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0, p
     K[..., [7, 31, 64, 100]] *= 8
     K = K.half()
     V = torch.randn((B, Hkv, hist, 128), generator=g).half()
-    CK = torch.randn((B, Hkv, Sq, 128), generator=g).half()
-    CV = torch.randn((B, Hkv, Sq, 128), generator=g).half()
-    q = (torch.randn((B, Hq, Sq, 128), generator=g) * q_scale / math.sqrt(128)).half()
+    # q, the chunk and the output in io_dtype (bf16 q/chunk values are exact in fp16 here)
+    CK = torch.randn((B, Hkv, Sq, 128), generator=g).to(io_dtype)
+    CV = torch.randn((B, Hkv, Sq, 128), generator=g).to(io_dtype)
+    q = (torch.randn((B, Hq, Sq, 128), generator=g) * q_scale / math.sqrt(128)).to(io_dtype)
     zones = []
     if sink:
         zs = ops.F16Zone(B, Hkv, sink, DEV)
@@ -100,10 +101,12 @@ def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0, p
             vs.append(CV[b].double().numpy())
             mask = np.concatenate([mask, np.tril(np.ones((Sq, Sq), dtype=bool))], axis=1)
         ref = oa.attend(q[b].double().numpy(), np.concatenate(ks, 1), np.concatenate(vs, 1), mask=mask)
-        err = np.abs(got[b] - ref).max()
-        print("  b=%d max abs err %.3e" % (b, err), flush=True)
+        # a bf16 output adds its own rounding: half an ulp, 2^-9 of the value
+        tol = TOL + (np.abs(ref) * 2.0 ** -9 if io_dtype == torch.bfloat16 else 0.0)
+        err = np.abs(got[b] - ref)
+        print("  b=%d max abs err %.3e" % (b, err.max()), flush=True)
         assert np.all(np.isfinite(got[b]))
-        assert err <= TOL
+        assert np.all(err <= tol)
 
 
 def test_small_all_sources():
@@ -135,6 +138,12 @@ def test_garbage_in_unused_tail_slots():
     print("case: prefill with NaN/inf scales and zero point 255 in the slots past each INT4 length", flush=True)
     _case(9, 2, 8, 2, 40, 16, [150, 33], [20, 5], poison=True)
     _case(10, 1, 4, 4, 20, 0, [7], [0], causal=False, poison=True)
+
+
+def test_bf16_query_chunk_and_output():
+    print("case: prefill with bf16 q, chunk and output, 16/4 Sq=100, sink 64 + INT4 300 + recent 50", flush=True)
+    _case(11, 1, 16, 4, 100, 64, [300], [50], io_dtype=torch.bfloat16)
+    _case(12, 2, 8, 8, 37, 0, [0, 70], [20, 0], io_dtype=torch.bfloat16)
 
 
 def test_medium_c4_like():
