@@ -227,7 +227,8 @@ def leg_c4(torch, ops, args):
            "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "steps": 10,
            "flops_per_step": P_FLOPS,
            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                        "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                        "traffic": read_profile("prefill_attn_c4_traffic.txt", "traffic_bytes_per_call"),
                         "mfma_busy_frac": read_profile("prefill_attn_c4_mfma_busy.txt", "mfma_busy_fraction")}}
     del pool, sink, rec, qd, ckd, cvd
     if args.no_cpu_baseline:
