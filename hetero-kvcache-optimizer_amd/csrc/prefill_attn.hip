@@ -178,8 +178,9 @@ struct Int4Stage {
 __global__ __launch_bounds__(kFlatThreads, 1) void prefill_attn_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     const int b = blockIdx.z;
+    const FlatBlock blk = flat_block();
     const int ngrp = (p.nrep + 3) / 4;
-    const int h = blockIdx.y / ngrp, grp = blockIdx.y % ngrp;
+    const int h = blk.hg / ngrp, grp = blk.hg % ngrp;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int team = wave >> 2, wt = wave & 3;
@@ -187,10 +188,10 @@ __global__ __launch_bounds__(kFlatThreads, 1) void prefill_attn_kernel(PrefillPa
     const int rep = grp * 4 + wt;
     const bool head_ok = rep < p.nrep;
     const int qh = h * p.nrep + (head_ok ? rep : 0);
-    const int qrow = (int)blockIdx.x * kFlatQ + team * kPfQ + n;
+    const int qrow = blk.qb * kFlatQ + team * kPfQ + n;
 
     TileMap tm;
-    make_tile_map(p, b, (int)blockIdx.x * kFlatQ + kFlatQ, tm);
+    make_tile_map(p, b, blk.qb * kFlatQ + kFlatQ, tm);
     // a sequence with no INT4 token was finished by the zone kernel
     if (tm.n4 == 0) return;
 
@@ -202,7 +203,7 @@ __global__ __launch_bounds__(kFlatThreads, 1) void prefill_attn_kernel(PrefillPa
     for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
-    const FlatWave fw{b, h, wt, lane, n, hh, qrow};
+    const FlatWave fw{b, h, wt, lane, n, hh, qrow, blk.qb};
     const int T = (tm.n4 + kFlatBufs - 1) / kFlatBufs * kFlatBufs;
     if (team == 0) {
         Int4Stage<0> pol(p, tm, fw);

@@ -66,8 +66,20 @@ __device__ __forceinline__ void flat_barrier() {
 }
 
 struct FlatWave {
-    int b, h, wt, lane, n, hh, qrow;
+    int b, h, wt, lane, n, hh, qrow, qb;
 };
+
+// The workgroup's query block and (kv head, GQA group) index.  Dispatch goes round-robin
+// over the 8 XCDs by linear workgroup id, so with qb = lin / HG and hg = lin % HG (HG =
+// gridDim.y, the head-group count) every workgroup of one head group runs on the same XCD
+// when HG is a multiple of 8, and the query blocks reading that head's tiles share an L2.
+struct FlatBlock {
+    int qb, hg;
+};
+__device__ __forceinline__ FlatBlock flat_block() {
+    const int lin = (int)blockIdx.x + (int)gridDim.x * (int)blockIdx.y;
+    return FlatBlock{lin / (int)gridDim.y, lin % (int)gridDim.y};
+}
 
 // QK: S^T[64 tok x 32 q] = K . Q^T.  The two token blocks' accumulators are two
 // independent MFMA chains; each step's K operands are read two steps ahead.

@@ -36,7 +36,7 @@ struct F16Stage {
     __device__ F16Stage(const PrefillParams& p_, const TileMap& tm_, const FlatWave& w_)
         : p(p_), tm(tm_), w(w_) {
         zone_tiles = tm.nz_t[0] + tm.nz_t[1] + tm.nz_t[2];
-        diag = tm.nc > 0 ? zone_tiles + (int)blockIdx.x : -1;
+        diag = tm.nc > 0 ? zone_tiles + w.qb : -1;
     }
     // Source of tile x: K rows, V tiles, capacity, valid length, tile index in the source
     __device__ void source(int x, const uint16_t*& k, const uint16_t*& v, int& cap, int& len, int& xl) const {
@@ -149,8 +149,9 @@ struct F16Stage {
 __global__ __launch_bounds__(kFlatThreads, 1) void prefill_zones_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     const int b = blockIdx.z;
+    const FlatBlock blk = flat_block();
     const int ngrp = (p.nrep + 3) / 4;
-    const int h = blockIdx.y / ngrp, grp = blockIdx.y % ngrp;
+    const int h = blk.hg / ngrp, grp = blk.hg % ngrp;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int team = wave >> 2, wt = wave & 3;
@@ -158,10 +159,10 @@ __global__ __launch_bounds__(kFlatThreads, 1) void prefill_zones_kernel(PrefillP
     const int rep = grp * 4 + wt;
     const bool head_ok = rep < p.nrep;
     const int qh = h * p.nrep + (head_ok ? rep : 0);
-    const int qrow = (int)blockIdx.x * kFlatQ + team * kPfQ + n;
+    const int qrow = blk.qb * kFlatQ + team * kPfQ + n;
 
     TileMap tm;
-    make_tile_map(p, b, (int)blockIdx.x * kFlatQ + kFlatQ, tm);
+    make_tile_map(p, b, blk.qb * kFlatQ + kFlatQ, tm);
     const int nf = tm.nf();
     // Sequences with INT4 tokens and no zone or chunk tile: the INT4 kernel starts at zero
     if (tm.n4 > 0 && nf == 0) return;
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(kFlatThreads, 1) void prefill_zones_kernel(PrefillP
     for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
-    const FlatWave fw{b, h, wt, lane, n, hh, qrow};
+    const FlatWave fw{b, h, wt, lane, n, hh, qrow, blk.qb};
     const int T = (nf + kFlatBufs - 1) / kFlatBufs * kFlatBufs;
     if (team == 0) {
         F16Stage<0> pol(p, tm, fw);
