@@ -431,7 +431,8 @@ def leg_c1(torch, ops, args):
            "algorithmic_bytes": C1_BYTES, "value": round(gbs, 2), "unit": "GB/s", "us_per_step": round(us_q, 3),
            "steps": 64, "launch": "hip graph", "roundtrip_us": round(us_rt, 3), "relative_error_pct": rel,
            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+                        "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "traffic": read_profile("pack_tokens_c1_traffic.txt", "traffic_bytes_per_call")}}
     if args.no_cpu_baseline:
         return blk
     n = cpu_threads(torch)
