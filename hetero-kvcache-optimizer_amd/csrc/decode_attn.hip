@@ -912,15 +912,14 @@ constexpr size_t kWsHeader = 256;
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int num_cus() {
-    static int cached = 0;
-    if (cached > 0) return cached;
+    static std::atomic<int> cached[64];   // per device (partition modes can differ)
     int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-        cached = n;
-    else
-        n = 256;
-    return cached > 0 ? cached : n;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    const int c = cached[dev & 63].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+    cached[dev & 63].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 // Ranges per (sequence, kv head): about one 8-wave workgroup per CU for the
@@ -985,17 +984,18 @@ void ws_forget(const void* ws) {
 // XCDs that workgroups are dispatched over round-robin: gfx950 has 32 CUs per
 // XCD, so a partition with N CUs spans N / 32 of them.
 int num_xcc() {
-    static int cached = 0;
-    if (cached > 0) return cached;
+    static std::atomic<int> cached[64];   // per device (partition modes can differ)
     int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1;
+    const int c = cached[dev & 63].load(std::memory_order_relaxed);
+    if (c > 0) return c;
     hipDeviceProp_t prop;
     int n = 1;
-    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess &&
-        strncmp(prop.gcnArchName, "gfx950", 6) == 0 && prop.multiProcessorCount % 32 == 0 &&
-        prop.multiProcessorCount >= 32)
+    if (hipGetDeviceProperties(&prop, dev) == hipSuccess && strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
+        prop.multiProcessorCount % 32 == 0 && prop.multiProcessorCount >= 32)
         n = prop.multiProcessorCount / 32;
-    cached = n;
-    return cached;
+    cached[dev & 63].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 size_t lds_bytes(int nrep) {
@@ -1145,11 +1145,8 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
                                        (const void*)decode_attn_kernel<true, false>,
                                        (const void*)decode_attn_kernel<false, true>,
                                        (const void*)decode_attn_kernel<true, true>};
-    static bool raised[4] = {false, false, false, false};   // the merge area plus the static id window can exceed 64 KB
-    if (!raised[var]) {
-        HKV_HIP_CHECK(hipFuncSetAttribute(fns[var], hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
-        raised[var] = true;
-    }
+    static std::atomic<uint64_t> raised[4];   // the merge area plus the static id window can exceed 64 KB
+    HKV_RAISE_LDS(fns[var], 96 * 1024, raised[var]);
     if (ws_needs_clear(wsp, BH)) {
         const int64_t words = (int64_t)(ticket_area_end((size_t)BH) - kWsHeader) / 4;
         hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024)),

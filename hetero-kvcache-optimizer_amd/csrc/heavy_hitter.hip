@@ -173,7 +173,7 @@ size_t evict_workspace(const EvictPlan& e) {
     return (size_t)e.nblocks * 8 + (e.nchunks > 1 ? (size_t)e.nchunks * e.k * 8 : 0);
 }
 
-bool sort_lds_raised = false;
+std::atomic<uint64_t> sort_lds_raised{0};
 
 }  // namespace
 }  // namespace hkv
@@ -240,11 +240,7 @@ extern "C" int hkv_eviction_candidates(const float* token_scores, int64_t seq_le
     HKV_REQUIRE(nchunks == 1 || nchunks * e.k <= kSortMax, HKV_ERR_UNSUPPORTED,
                 "hkv_eviction_candidates: %lld blocks with %d candidates exceed one merge pass",
                 (long long)e.nblocks, e.k);
-    if (!sort_lds_raised) {
-        HKV_HIP_CHECK(hipFuncSetAttribute((const void*)sort_take_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          kSortMax * 8));
-        sort_lds_raised = true;
-    }
+    HKV_RAISE_LDS(sort_take_kernel, kSortMax * 8, sort_lds_raised);
     uint64_t* keys = (uint64_t*)workspace;
     hipLaunchKernelGGL(block_keys_kernel, dim3((unsigned)((e.nblocks + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, token_scores, seq_len, (int)block_size, e.nblocks, e.prot_lo, e.prot_hi,

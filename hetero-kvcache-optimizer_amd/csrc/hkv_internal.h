@@ -6,6 +6,7 @@
 #include <stdint.h>
 #include <stdio.h>
 #include <stdarg.h>
+#include <atomic>
 
 #include "../../include/heterokv.h"
 
@@ -40,6 +41,21 @@ void clear_error();
             ::hkv::set_error("launch of %s failed: %s", name, hipGetErrorString(_e)); \
             return HKV_ERR_HIP;                                                    \
         }                                                                          \
+    } while (0)
+
+// Raises kernel fn's dynamic LDS limit to `bytes` on the current device, once per device
+// (the attribute is held per device); `done` is the kernel's bitmask of devices already
+// raised.  Safe to call from several host threads.
+#define HKV_RAISE_LDS(fn, bytes, done)                                                        \
+    do {                                                                                      \
+        int _dev = 0;                                                                         \
+        HKV_HIP_CHECK(hipGetDevice(&_dev));                                                   \
+        const uint64_t _bit = 1ull << (_dev & 63);                                            \
+        if (!((done).load(std::memory_order_acquire) & _bit)) {                               \
+            HKV_HIP_CHECK(hipFuncSetAttribute((const void*)(fn),                              \
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (bytes))); \
+            (done).fetch_or(_bit, std::memory_order_release);                                 \
+        }                                                                                     \
     } while (0)
 
 constexpr int kHeadDim = 128;

@@ -392,12 +392,8 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
     }
     if (int4_keys) {
         const dim3 grid((a->num_queries + kFlatQ - 1) / kFlatQ, a->num_kv_heads * ngrp, a->batch);
-        static bool raised = false;   // four tile buffers exceed the 64 KB default
-        if (!raised) {
-            HKV_HIP_CHECK(hipFuncSetAttribute((const void*)prefill_attn_kernel,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, kFlatLdsBytes));
-            raised = true;
-        }
+        static std::atomic<uint64_t> raised{0};   // four tile buffers exceed the 64 KB default
+        HKV_RAISE_LDS(prefill_attn_kernel, kFlatLdsBytes, raised);
         hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(kFlatThreads), kFlatLdsBytes, (hipStream_t)stream, p);
         HKV_LAUNCH_CHECK("prefill_attn_kernel");
     }

@@ -212,12 +212,8 @@ __global__ __launch_bounds__(kFlatThreads, 1) void prefill_zones_kernel(PrefillP
 
 int launch_prefill_zones(const PrefillParams& p, int ngrp, hipStream_t stream) {
     const dim3 grid((p.Sq + kFlatQ - 1) / kFlatQ, p.Hkv * ngrp, p.B);
-    static bool raised = false;   // four tile buffers exceed the 64 KB default
-    if (!raised) {
-        HKV_HIP_CHECK(hipFuncSetAttribute((const void*)prefill_zones_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          kFlatLdsBytes));
-        raised = true;
-    }
+    static std::atomic<uint64_t> raised{0};   // four tile buffers exceed the 64 KB default
+    HKV_RAISE_LDS(prefill_zones_kernel, kFlatLdsBytes, raised);
     hipLaunchKernelGGL(prefill_zones_kernel, grid, dim3(kFlatThreads), kFlatLdsBytes, stream, p);
     HKV_LAUNCH_CHECK("prefill_zones_kernel");
     return HKV_OK;
