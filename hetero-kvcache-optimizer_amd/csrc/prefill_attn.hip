@@ -295,8 +295,11 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
     }
     const int nrep = a->num_q_heads / a->num_kv_heads;
     const int ngrp = (nrep + 3) / 4;
-    HKV_REQUIRE((int64_t)a->num_kv_heads * ngrp < 65536 && a->batch < 65536, HKV_ERR_ARG,
-                "hkv_prefill_attn: grid too large");
+    // the kernels' linear workgroup id (query block, head group) is a 32-bit int
+    const int64_t qblocks = ((int64_t)a->num_queries + kFlatQ - 1) / kFlatQ;
+    HKV_REQUIRE((int64_t)a->num_kv_heads * ngrp < 65536 && a->batch < 65536 &&
+                    qblocks * a->num_kv_heads * ngrp < (1ll << 31),
+                HKV_ERR_ARG, "hkv_prefill_attn: grid too large");
     PrefillParams p;
     p.B = a->batch;
     p.Hkv = a->num_kv_heads;
