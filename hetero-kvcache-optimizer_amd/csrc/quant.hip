@@ -93,8 +93,10 @@ __device__ __forceinline__ void load16(const void* src, int dtype, int64_t off, 
                                        float (&vals)[16]) {
     const uint16_t* p = (const uint16_t*)src + off;
     if (vec_ok) {
-        const uint4 a = *(const uint4*)p;
-        const uint4 b = *(const uint4*)(p + 8);
+        // read once: non-temporal loads (on the 8x4096-token K+V pack, 8.8 vs 9.0 us)
+        typedef unsigned int nv4 __attribute__((ext_vector_type(4)));
+        const nv4 a = __builtin_nontemporal_load((const nv4*)p);
+        const nv4 b = __builtin_nontemporal_load((const nv4*)(p + 8));
         const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
