@@ -149,6 +149,17 @@ __device__ __forceinline__ uint32_t quant_code(float x, const QParams& q) {
     return (uint32_t)t;
 }
 
+// quant_code before its rounding: x / scale + zp clamped to [0, 15].  Clamping first
+// and rounding after gives the same code for integer bounds (a NaN clamps to 0);
+// code_into() rounds to nearest even, as rintf does, with v_cvt_pk_u8_f32, which also
+// writes the code into byte `sel` (0..3) of `word`.
+__device__ __forceinline__ float quant_unrounded(float x, const QParams& q) {
+    return fminf(fmaxf(div_by_scale(x, q) + q.zpf, 0.0f), 15.0f);
+}
+__device__ __forceinline__ uint32_t code_into(float t, uint32_t sel, uint32_t word) {
+    return __builtin_amdgcn_cvt_pk_u8_f32(t, sel, word);
+}
+
 // Position of logical code k (0..7) inside a packed 32-bit word.
 __host__ __device__ constexpr int nib_shift(int k) { return (k & 1) * 16 + (k >> 1) * 4; }
 

@@ -216,25 +216,34 @@ __global__ __launch_bounds__(256) void pack_tokens_kernel(PackParams p) {
     }
     if (active) {
         const QParams q = qparams_from_minmax(mn, mx);
-        uint32_t cw[16];
+        float tv[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) cw[i] = quant_code(vals[i], q);
+        for (int i = 0; i < 16; ++i) tv[i] = quant_unrounded(vals[i], q);
         if (kv == 0) {
-            // this lane's 16 K codes are K words 2 part and 2 part + 1 of the row: packed
-            // here and written to the record directly
-            uint32_t w0 = 0, w1 = 0;
+            // this lane's 16 K codes are K words 2 part and 2 part + 1 of the row: codes
+            // 2j and 2j + 1 of a word go to bytes 0 and 2 of x[j], and the word is
+            // x0 | x1 << 4 | x2 << 8 | x3 << 12 (nib_shift order)
+            uint32_t kw[2];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                w0 |= cw[k] << nib_shift(k);
-                w1 |= cw[8 + k] << nib_shift(k);
+            for (int hw = 0; hw < 2; ++hw) {
+                uint32_t x[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    x[j] = code_into(tv[8 * hw + 2 * j + 1], 2u, code_into(tv[8 * hw + 2 * j], 0u, 0u));
+                kw[hw] = x[0] | (x[1] << 4) | (x[2] << 8) | (x[3] << 12);
             }
-            *(uint2*)(rec + L.kc(h) + slot * kCodeRowBytes + part * 8) = make_uint2(w0, w1);
+            *(uint2*)(rec + L.kc(h) + slot * kCodeRowBytes + part * 8) = make_uint2(kw[0], kw[1]);
         } else {
-            // V words mix four tokens: the codes go through LDS, one 16-byte write
+            // V words mix four tokens: the codes go through LDS (one byte each), one
+            // 16-byte write
             uint32_t b4[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                b4[i] = cw[4 * i] | (cw[4 * i + 1] << 8) | (cw[4 * i + 2] << 16) | (cw[4 * i + 3] << 24);
+            for (int i = 0; i < 4; ++i) {
+                uint32_t w = 0u;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w = code_into(tv[4 * i + e], (uint32_t)e, w);
+                b4[i] = w;
+            }
             *(uint4*)&codes[1][slot][part * 16] = make_uint4(b4[0], b4[1], b4[2], b4[3]);
         }
         if (part == 0) {
