@@ -73,6 +73,44 @@ def test_pack_tokens_bytes(H, T, start):
         assert np.array_equal(zps.reshape(H, -1)[:, start:].cpu().numpy().reshape(-1), ref[2])
 
 
+def test_pack_tokens_bf16_rows():
+    """bf16 K/V: the values widen to float32 exactly, so the records equal the oracle's
+    compression of those float32 values."""
+    print("case: pack_tokens bf16 H=4 T=77 start=3", flush=True)
+    from heterokv import ops
+    k, v = _rand_kv(4077, 4, 77)
+    kb, vb = k.float().bfloat16(), v.float().bfloat16()
+    start, nlb = 3, (3 + 77 + 15) // 16
+    bt = torch.arange(nlb, dtype=torch.int32)
+    pool = ops.Int4Pool(nlb, 4, DEV)
+    ops.pack_tokens(pool, kb.to(DEV), vb.to(DEV), torch.tensor([start], dtype=torch.int32), bt[None])
+    exp, _, _ = _expected_pool(kb[0].float().numpy(), vb[0].float().numpy(), start, bt.numpy(), nlb)
+    assert np.array_equal(pool.data.cpu().numpy(), exp)
+    pool.check_errors()
+
+
+def test_pack_tokens_strided_rows_match_contiguous():
+    """Rows 129 elements apart (no 16-byte alignment: the per-element load path) pack to
+    the same bytes as the contiguous copy (the 16-byte load path)."""
+    print("case: pack_tokens strided rows H=8 T=50 start=9", flush=True)
+    from heterokv import ops
+    g = torch.Generator().manual_seed(129)
+    big_k = torch.randn((1, 8, 50, 129), generator=g).half().to(DEV)
+    big_v = torch.randn((1, 8, 50, 129), generator=g).half().to(DEV)
+    k, v = big_k[..., :128], big_v[..., :128]
+    assert k.stride(2) == 129
+    start, nlb = 9, (9 + 50 + 15) // 16
+    bt = torch.arange(nlb, dtype=torch.int32)[None]
+    sp = torch.tensor([start], dtype=torch.int32)
+    p1, p2 = ops.Int4Pool(nlb, 8, DEV), ops.Int4Pool(nlb, 8, DEV)
+    ops.pack_tokens(p1, k, v, sp, bt)
+    ops.pack_tokens(p2, k.contiguous(), v.contiguous(), sp, bt)
+    assert torch.equal(p1.data, p2.data)
+    exp, _, _ = _expected_pool(k[0].cpu().numpy(), v[0].cpu().numpy(), start, bt[0].numpy(), nlb)
+    assert np.array_equal(p1.data.cpu().numpy(), exp)
+    p1.check_errors()
+
+
 def test_pack_tokens_nan_and_inf_tokens():
     """A token row holding a NaN gets a NaN scale and zero codes/zp, as torch's min/max
     propagate NaN; rows with infinities follow the same float32 steps as the oracle."""
