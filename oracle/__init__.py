@@ -2,9 +2,9 @@
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import anything from this package, and
-only as the checker (or, for the bench, as the timed CPU baseline).  The
-product path (the ``heterokv`` package) never imports it and fails loudly when
-its HIP library is missing.
+only as the reference results that GPU outputs are compared with (or, for the
+bench, as the timed CPU baseline).  The product path (the ``heterokv`` package)
+never imports it and fails loudly when its HIP library is missing.
 
 Modules
   compressor   -- KVCompressor.compress/decompress/relative_error

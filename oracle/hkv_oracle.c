@@ -1,7 +1,7 @@
 /*
  * CPU restatement of the reference INT4 group quantizer -- TEST INFRASTRUCTURE ONLY.
  *
- * This file is the checker for the HIP kernels.  Only tests/, the smoke test and
+ * The HIP kernels are compared with this file's results.  Only tests/, the smoke test and
  * the bench's cpu_baseline leg load it; the product path never does.
  *
  * It follows src/quantization/kv_compressor.py of kldxg123/Hetero-KVCache-Optimizer:
