@@ -868,7 +868,7 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the decode path would shard by kv head or "
+        print("bench.py: this benchmark measures one GPU only (the decode path would shard by kv head or "
               "sequence, with no exchange between GPUs); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 

@@ -152,7 +152,7 @@ __global__ __launch_bounds__(128) void zone_read_kernel(const uint16_t* __restri
 }
 
 // ---- device-stepped decode update: the decision of the manager's decode step
-// (manager.py:588-674 as this build keeps it) taken on the GPU from `state`, so the
+// (manager.py:588-674 as this library keeps it) taken on the GPU from `state`, so the
 // step can be replayed from a captured graph.
 struct ZoneStepParams {
     const uint16_t* k;

@@ -159,7 +159,7 @@ class HeteroKVManager:
             raise HeteroKVError(-4, "HeteroKVManager stores one INT4 group per 128-value token row "
                                     "(group_size=128, bits=4); got group_size=%d bits=%d" % (group_size, bits))
         if enable_method_d:
-            raise HeteroKVError(-4, "query-aware retrieval (Method D) is not part of this build")
+            raise HeteroKVError(-4, "query-aware retrieval (Method D) is not part of this library")
         self.num_layers = num_layers
         self.sink_tokens = sink_tokens
         self.hbm_budget_tokens = hbm_budget_tokens
@@ -397,7 +397,7 @@ class HeteroKVManager:
         return kk.to(k.dtype), vv.to(v.dtype)
 
     def _decode_host(self, st, seq_offset, k, v, launch):
-        """The decode step's zone decision (manager.py:588-674 as this build keeps it), with
+        """The decode step's zone decision (manager.py:588-674 as this library keeps it), with
         its kernels when `launch` (device-stepped decode takes the same decision on the GPU)."""
         pos = seq_offset
         if st.tail_len < self.tail_budget:
@@ -1086,7 +1086,7 @@ class HeteroKVManager:
 
     # ---------------------------------------------------------------- summaries
     def memory_summary(self) -> Dict[str, Any]:
-        """manager.py:387-401.  dram_bytes counts this build's packed INT4 storage (HBM and
+        """manager.py:387-401.  dram_bytes counts this library's packed INT4 storage (HBM and
         host records alike); host_bytes the part in the pinned host arena."""
         hbm = sum((st.sink_len + st.tail_len + st.hh_len) for st in self._layers if st is not None)
         dram_bytes = 0

@@ -239,7 +239,7 @@ int hkv_zone_copy(const uint16_t* src_k, const uint16_t* src_v, int32_t src_capa
 
 /*
  * Device-stepped decode update of the recent-window ring and the heavy-hitter zone:
- * the manager's decode step (src/memory/manager.py:588-674 as this build keeps it)
+ * the manager's decode step (src/memory/manager.py:588-674 as this library keeps it)
  * with its decision taken on the GPU from `state`, so that a captured graph can
  * replay it.  state = device int32 [4]: ring head, ring length, heavy-hitter length,
  * dropped tokens.  If the ring is not full the new token goes to slot
