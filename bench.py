@@ -57,14 +57,17 @@ def make_inputs(torch, seed=2):
     return q.half(), K.half(), V.half()
 
 
-def build_copy(torch, ops, q, K, V, dev):
+def build_copy(torch, ops, q, K, V, dev, bt=None):
+    """One KV copy of the 32K decode workload; `bt` is a block table to share between
+    copies (the layers of a decode step read one table)."""
     sink = ops.F16Zone(B, HKV, SINK, dev)
     sink.write(K[:, :, :SINK].to(dev), V[:, :, :SINK].to(dev), [0])
     rec = ops.F16Zone(B, HKV, RECENT, dev)
     rec.write(K[:, :, SINK + MID:].to(dev), V[:, :, SINK + MID:].to(dev), [0])
     nb = (MID + 15) // 16
     pool = ops.Int4Pool(nb, HKV, dev)
-    bt = torch.arange(nb, dtype=torch.int32, device=dev)[None]
+    if bt is None:
+        bt = torch.arange(nb, dtype=torch.int32, device=dev)[None]
     ops.pack_tokens(pool, K[:, :, SINK:SINK + MID].to(dev), V[:, :, SINK:SINK + MID].to(dev),
                     torch.zeros(1, dtype=torch.int32, device=dev), bt)
     pool.check_errors()
@@ -519,6 +522,72 @@ def bench_scoring(torch, ops, args):
     print(json.dumps(line), flush=True)
 
 
+PROBE_LIB = os.path.join(ROOT, "hetero-kvcache-optimizer_amd", "heterokv", "libhkvprobe.so")
+# (pattern, workgroups, waves per workgroup, units in flight per wave): 8 and 16 waves per
+# CU at 1x and 2x the decode's 256-workgroup grid, plus the INT4 pool's head-part pattern
+PROBE_SHAPES = ("contig:256:8:2,contig:256:8:4,contig:256:8:8,contig:256:16:2,contig:256:16:4,"
+                "contig:512:4:4,contig:512:4:8,contig:512:8:2,contig:512:8:4,contig:1024:8:2,"
+                "parts:256:8:2,parts:256:8:4,parts:256:16:2,parts:512:8:2")
+
+
+def bench_probe(torch, args):
+    """Streaming-read probes at the 32K decode's size: how fast one launch of a given shape
+    reads 48,638,976 bytes (contiguous) or the INT4 pool's 2208-byte head parts of 1788
+    records of 8 heads (31,583,232 bytes), with no compute.  Eight rotated copies defeat
+    the Infinity Cache; launches are replayed from a HIP graph, HIP events on its stream."""
+    import ctypes
+    dev = torch.device("cuda:0")
+    lib = ctypes.CDLL(PROBE_LIB)
+    lib.hkv_probe_stream.restype = ctypes.c_int
+    lib.hkv_probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                     ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint32,
+                                     ctypes.c_void_p, ctypes.c_void_p]
+    R = args.copies
+    parts_bytes = HKV * 2208 * ((MID + 15) // 16)
+    bufs = [torch.randint(0, 1 << 30, (STEP_BYTES // 4,), dtype=torch.int32, device=dev) for _ in range(R)]
+    sink = torch.zeros(1024 * 16 * 64, dtype=torch.int32, device=dev)
+    n = max(args.steps, 64)
+    n -= n % R
+    shapes = [s for s in (args.probe_shapes or PROBE_SHAPES).split(",") if s]
+    rows = []
+    for sh in shapes:
+        pat, grid, waves, depth = sh.split(":")
+        grid, waves, depth = int(grid), int(waves), int(depth)
+        pattern = {"contig": 0, "parts": 1}[pat]
+        nbytes = STEP_BYTES if pattern == 0 else parts_bytes
+
+        def launch(i):
+            st = torch.cuda.current_stream(dev).cuda_stream   # the capturing stream under graph capture
+            rc = lib.hkv_probe_stream(bufs[i % R].data_ptr(), nbytes, pattern, grid, waves, depth, HKV, 2208,
+                                      0x9E3779B9, sink.data_ptr(), ctypes.c_void_p(st))
+            if rc != 0:
+                raise RuntimeError("hkv_probe_stream(%s) returned %d" % (sh, rc))
+
+        if args.no_graph:
+            for i in range(R):
+                launch(i)
+            ms = event_time_ms(torch, launch, n)
+        else:
+            ms = graph_time_ms(torch, launch, n, 2, dev)
+        rows.append({"shape": sh, "waves_per_cu": waves * grid // 256, "bytes": nbytes, "us": round(ms * 1e3, 3),
+                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        print("[probe] %-18s %6.2f us  %7.1f GB/s" % (sh, rows[-1]["us"], rows[-1]["gbs"]), file=sys.stderr, flush=True)
+    best = max((r for r in rows if r["bytes"] == STEP_BYTES), key=lambda r: r["gbs"], default=None)
+    line = {
+        "metric": "streaming-read probe GB/s at the 32K decode's byte count",
+        "value": best["gbs"] if best else None, "unit": "GB/s", "n_gpus": 1, "steps": n, "warmup": 2,
+        "ms_per_step": round(best["us"] * 1e-3, 6) if best else None, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u8", "data": "synthetic (random int32 words, 8 rotated copies)",
+        "config": {"workload": "read-only streaming probe (no compute), 48,638,976 bytes contiguous or the "
+                               "31,583,232-byte INT4 head-part pattern; %d launches per shape from a HIP graph" % n,
+                   "shapes": rows},
+        "roofline": {"bound": "hbm", "achieved": best["gbs"] if best else None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": best["frac"] if best else None, "traffic": None},
+        "cpu_baseline": None,
+    }
+    return line
+
+
 T_LAYERS, T_HQ, T_HKV, T_HIDDEN, T_INTER, T_VOCAB = 28, 28, 4, 3584, 18944, 152064
 T_CTX, T_CHUNK, T_SINK, T_KEEP, T_HOST_FRAC = 131072, 2048, 64, 4160, 0.75
 
@@ -750,11 +819,15 @@ def leg_c5(torch, args, timed=8, warm=2):
 # ------------------------------------------------------------------------------ C2 headline
 def leg_c2(torch, ops, args):
     """The headline: single-layer decode attention at 32K context (one launch per step),
-    replayed from a HIP graph over 8 rotated KV copies."""
+    replayed from HIP graphs over 8 rotated KV copies (the copies play the layers of a
+    decode step: each has its own K/V, all share one block table).  The W warm-up
+    launches and the K timed launches are each captured in one graph, so the timed
+    region is K launches and one graph launch."""
     dev = torch.device("cuda:0")
     q, K, V = make_inputs(torch)
     R = args.copies
-    copies = [build_copy(torch, ops, q, K, V, dev) for _ in range(R)]
+    bt = torch.arange((MID + 15) // 16, dtype=torch.int32, device=dev)[None]
+    copies = [build_copy(torch, ops, q, K, V, dev, bt) for _ in range(R)]
     q_dev = q.to(dev)
     out = torch.empty((B, HQ, D), dtype=torch.float16, device=dev)
     ws = ops.DecodeWorkspace(dev)
@@ -778,31 +851,26 @@ def leg_c2(torch, ops, args):
                 for i in range(n):
                     launch(i)
             return g
-        graphs["full"] = capture(R)
-        if K_steps % R:
-            graphs["rem"] = capture(K_steps % R)
-        if W % R:
-            graphs["wrem"] = capture(W % R)
+        graphs["timed"] = capture(K_steps)
+        if W > 0:
+            graphs["warm"] = capture(W)
 
-    def run(n, rem_key):
+    def run(n, key):
         if args.no_graph:
             with torch.cuda.stream(stream):
                 for i in range(n):
                     launch(i)
-            return
-        for _ in range(n // R):
-            graphs["full"].replay()
-        if n % R:
-            graphs[rem_key].replay()
+        elif n > 0:
+            graphs[key].replay()
 
     with torch.cuda.stream(stream):
-        run(W, "wrem")
+        run(W, "warm")
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         ev0.record(stream)
-        run(K_steps, "rem")
+        run(K_steps, "timed")
         ev1.record(stream)
     ev1.synchronize()
     torch.cuda.synchronize()
@@ -860,9 +928,13 @@ def main():
                     help="nested configuration blocks of the default line: any of c1 (quantize+pack), c3 (batched "
                          "paged decode), c4 (chunked prefill), c5 (128K tiered decode with 75%% host offload); "
                          "'none' for the 32K decode alone")
-    ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged", "scoring", "quant"], default=None,
+    ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged", "scoring", "quant", "probe"],
+                    default=None,
                     help="run one configuration alone and print its block as the line (for profiling): decode "
-                         "(32K), prefill (C4), tiered (C5), paged (C3), quant (C1), scoring (heavy hitters)")
+                         "(32K), prefill (C4), tiered (C5), paged (C3), quant (C1), scoring (heavy hitters), probe "
+                         "(streaming-read probes at the decode's byte count)")
+    ap.add_argument("--probe-shapes", default=None,
+                    help="probe shapes pattern:workgroups:waves:depth, comma-separated (pattern contig or parts)")
     ap.add_argument("--copy-calibration", type=float, default=0.0,
                     help="run only torch's device copy of this many MB (20 launches) so that rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE can be scaled against a known byte count")
@@ -891,7 +963,7 @@ def main():
 
     single = {"prefill": lambda: leg_c4(torch, ops, args), "paged": lambda: leg_c3(torch, ops, args),
               "quant": lambda: leg_c1(torch, ops, args), "tiered": lambda: leg_c5(torch, args),
-              "scoring": lambda: bench_scoring(torch, ops, args)}
+              "scoring": lambda: bench_scoring(torch, ops, args), "probe": lambda: bench_probe(torch, args)}
     if args.workload in single:
         blk = single[args.workload]()
         if blk is not None:

@@ -5,7 +5,8 @@
 Compiles every csrc/*.hip file with hipcc for gfx950 into
 heterokv/libheterokv.so.  Correctly rounded fp32 division/sqrt stay on (the
 quantizer is bit-exact with an IEEE reference) and packed-fp32 instructions are
-disabled for device code.
+disabled for device code.  The streaming-read probes (csrc/probe/*.hip, used by
+bench.py's probe workload only) go into heterokv/libhkvprobe.so.
 """
 import os
 import shutil
@@ -15,6 +16,7 @@ import sys
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 OUT = os.path.join(PKG_DIR, "heterokv", "libheterokv.so")
+PROBE_OUT = os.path.join(PKG_DIR, "heterokv", "libhkvprobe.so")
 
 HIPCC_FLAGS = [
     "-O3",
@@ -26,6 +28,11 @@ HIPCC_FLAGS = [
     "-fno-fast-math",
     "-ffp-contract=on",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # The AMDGPU atomic optimizer turns a single-lane atomic whose result is used later
+    # (the decode kernel's placement-mask OR) into a wave-aggregated one that waits for
+    # the result at once, which puts an L2 round trip in front of the workgroup merge.
+    # Every other atomic in the library is a single-lane error-bit OR on a rare path.
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wno-unused-command-line-argument",
 ]
 
@@ -43,9 +50,8 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def build(verbose=True):
-    srcs = sources()
-    tmp = OUT + ".tmp"
+def _compile(srcs, out_path, verbose):
+    tmp = out_path + ".tmp"
     cmd = [hipcc_path()] + HIPCC_FLAGS + ["-o", tmp] + srcs
     if verbose:
         print("[heterokv] " + " ".join(cmd), flush=True)
@@ -58,7 +64,14 @@ def build(verbose=True):
         raise RuntimeError("hipcc failed with exit code %d" % res.returncode)
     if verbose and lines:
         print("\n".join(lines), flush=True)
-    os.replace(tmp, OUT)
+    os.replace(tmp, out_path)
+
+
+def build(verbose=True):
+    _compile(sources(), OUT, verbose)
+    probe_dir = os.path.join(CSRC, "probe")
+    _compile(sorted(os.path.join(probe_dir, f) for f in os.listdir(probe_dir) if f.endswith(".hip")), PROBE_OUT,
+             verbose)
     return OUT
 
 

@@ -50,12 +50,14 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 8;                 // waves per workgroup
 constexpr int kThreads = kWaves * 64;
 constexpr int kPartStride = kHeadDim + 4;  // o[128], m, l, 2 pad (16-byte rows)
+static_assert((kHeadDim * 4) % 8 == 0 && (kPartStride * 4) % 16 == 0, "m, l load as one aligned 8-byte pair");
 #ifndef HKV_DECODE_PREFETCH
 #define HKV_DECODE_PREFETCH 2
 #endif
@@ -138,6 +140,9 @@ __device__ __forceinline__ float ld_l2(__amdgpu_buffer_rsrc_t r, int byte_off) {
 }
 __device__ __forceinline__ f4 ld_l2_f4(__amdgpu_buffer_rsrc_t r, int byte_off) {
     return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 1));
+}
+__device__ __forceinline__ f2 ld_l2_f2(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    return __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 1));
 }
 
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
@@ -494,8 +499,9 @@ __device__ __forceinline__ void load_partials(__amdgpu_buffer_rsrc_t prs, const 
         const int sj = s0 + j * K;
         const int off = min(sj, nsplit - 1) * (nrep * kPartStride) + hd * kPartStride;
         if constexpr (kL2) {
-            ms[j] = sj < nsplit ? ld_l2(prs, (off + kHeadDim) * 4) : -INFINITY;
-            ls[j] = ld_l2(prs, (off + kHeadDim + 1) * 4);
+            const f2 ml = ld_l2_f2(prs, (off + kHeadDim) * 4);   // m, l side by side (8-byte aligned)
+            ms[j] = sj < nsplit ? ml.x : -INFINITY;
+            ls[j] = ml.y;
             os[j] = ld_l2_f4(prs, (off + d4) * 4);
         } else {
             const float* ps = parts + off;
@@ -939,46 +945,23 @@ int choose_splits(int BH, int int4_max_len, const int32_t* f16_max_lens, int nz,
 
 // Workspace: [header (error word) | agent tickets | XCD masks | XCD-local tickets
 // (256 B each) | partial states, one 256-byte aligned block per (sequence, kv head)].
-// The ticket area [kWsHeader, partials) must be zero at a launch; it depends only on
-// the pair count.
+// The ticket area holds kHandoffPairs slots of each kind at fixed offsets, whatever the
+// launch geometry, so the partial states of one launch never overlap the tickets of
+// another launch on the same workspace: the kernels leave every ticket at zero, and a
+// workspace (or a graph replaying launches on it) stays valid across geometries with
+// no clearing between launches.  A launch that splits more pairs than that is
+// rejected.
+constexpr int64_t kHandoffPairs = 1024;
+
 size_t pair_part_bytes(int nrep, int nsplit) { return align256((size_t)nsplit * nrep * kPartStride * sizeof(float)); }
 
-size_t ticket_area_end(size_t BH) { return kWsHeader + 2 * align256(BH * sizeof(int)) + BH * 256; }
+constexpr size_t kTicketAreaEnd = kWsHeader + 2 * kHandoffPairs * sizeof(int) + kHandoffPairs * 256;
+static_assert(kTicketAreaEnd % 256 == 0, "partial states start 256-byte aligned");
 
 size_t workspace_bytes(int B, int Hq, int Hkv, int nsplit) {
     const size_t BH = (size_t)B * Hkv;
     const int nrep = Hq / Hkv;
-    return ticket_area_end(BH) + BH * pair_part_bytes(nrep, nsplit);
-}
-
-// Pair count of the last launch on each workspace address.  A launch with another
-// pair count moves the ticket area over bytes that held partial states, so the area
-// is cleared first (one small kernel on the launch's stream).
-struct WsGeom {
-    const void* ws;
-    int64_t bh;
-};
-std::mutex g_ws_mu;
-WsGeom g_ws[64];
-int g_ws_next = 0;
-
-bool ws_needs_clear(const void* ws, int64_t bh) {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    for (auto& e : g_ws)
-        if (e.ws == ws) {
-            const bool changed = e.bh != bh;
-            e.bh = bh;
-            return changed;
-        }
-    g_ws[g_ws_next] = WsGeom{ws, bh};
-    g_ws_next = (g_ws_next + 1) % 64;
-    return true;
-}
-
-void ws_forget(const void* ws) {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    for (auto& e : g_ws)
-        if (e.ws == ws) e = WsGeom{nullptr, 0};
+    return kTicketAreaEnd + BH * pair_part_bytes(nrep, nsplit);
 }
 
 // XCDs that workgroups are dispatched over round-robin: gfx950 has 32 CUs per
@@ -1080,6 +1063,9 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
     const int64_t BH = (int64_t)a->batch * a->num_kv_heads;
     HKV_REQUIRE(BH < 65536, HKV_ERR_ARG, "hkv_decode_attn: batch x kv heads too large");
     const int ms = choose_splits((int)BH, a->int4_max_len, zl, a->num_f16_zones, a->splits_hint);
+    HKV_REQUIRE(ms == 1 || BH <= kHandoffPairs, HKV_ERR_CAPACITY,
+                "hkv_decode_attn: %d ranges per pair for %lld (sequence, kv head) pairs; a split launch hands off "
+                "at most %lld pairs", ms, (long long)BH, (long long)kHandoffPairs);
     const size_t need = workspace_bytes(a->batch, a->num_q_heads, a->num_kv_heads, ms);
     HKV_REQUIRE(ws_bytes >= need, HKV_ERR_CAPACITY, "hkv_decode_attn: workspace %zu bytes, need %zu", ws_bytes, need);
     HKV_REQUIRE((((uintptr_t)wsp) & 255) == 0, HKV_ERR_ARG, "hkv_decode_attn: workspace must be 256-byte aligned");
@@ -1118,9 +1104,9 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
     char* ws = (char*)wsp;
     p.err = a->err_flag ? (int*)a->err_flag : (int*)ws;
     p.counters = (int*)(ws + kWsHeader);
-    p.owners = (unsigned*)(ws + kWsHeader + align256((size_t)BH * sizeof(int)));
-    p.counters_l2 = (int*)(ws + kWsHeader + 2 * align256((size_t)BH * sizeof(int)));
-    p.partials = (float*)(ws + ticket_area_end((size_t)BH));
+    p.owners = (unsigned*)(ws + kWsHeader + kHandoffPairs * sizeof(int));
+    p.counters_l2 = (int*)(ws + kWsHeader + 2 * kHandoffPairs * sizeof(int));
+    p.partials = (float*)(ws + kTicketAreaEnd);
     p.part_pair_stride = (int64_t)(pair_part_bytes(nrep, ms) / sizeof(float));
     p.nxcc = num_xcc();
     // one range per pair needs no hand-off (and must not leave a mask bit behind)
@@ -1147,15 +1133,6 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
                                        (const void*)decode_attn_kernel<true, true>};
     static std::atomic<uint64_t> raised[4];   // the merge area plus the static id window can exceed 64 KB
     HKV_RAISE_LDS(fns[var], 96 * 1024, raised[var]);
-    if (ws_needs_clear(wsp, BH)) {
-        const int64_t words = (int64_t)(ticket_area_end((size_t)BH) - kWsHeader) / 4;
-        hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024)),
-                           dim3(256), 0, (hipStream_t)stream, (int*)(ws + kWsHeader), words);
-        if (hipGetLastError() != hipSuccess) {
-            ws_forget(wsp);
-            HKV_REQUIRE(false, HKV_ERR_HIP, "hkv_decode_attn: launch of the ticket clear failed");
-        }
-    }
     const dim3 grid((unsigned)(BH * ms)), block(kThreads);
     switch (var) {
         case 0: hipLaunchKernelGGL((decode_attn_kernel<false, false>), grid, block, lds, (hipStream_t)stream, p); break;
@@ -1200,6 +1177,12 @@ extern "C" int hkv_decode_attn_noalloc(const HkvDecodeArgs* a, void* stream) {
             void* p = nullptr;
             HKV_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
             HKV_REQUIRE(p != nullptr, HKV_ERR_HIP, "hkv_decode_attn_noalloc: no scratch address on device %d", dev);
+            // the ticket area starts at zero, like a new workspace (a fill kernel, not a memset,
+            // so that a first call made under graph capture records nothing a replay mishandles)
+            const int64_t words = (int64_t)(kTicketAreaEnd - kWsHeader) / 4;
+            hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                               (hipStream_t)stream, (int*)((char*)p + kWsHeader), words);
+            HKV_LAUNCH_CHECK("clear_words_kernel");
             g_scratch_ptr[dev] = p;
         }
         ptr = g_scratch_ptr[dev];

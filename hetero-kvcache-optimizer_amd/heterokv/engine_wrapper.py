@@ -446,13 +446,27 @@ class DecodeGraph:
             with torch.cuda.graph(g):
                 self._logits = self._forward(self._ids, self._pos)
             g.replay()
+            mgr._errword().post()
             self.graph = g
             out = self._logits
         else:
+            # The kernels of a replay report into the manager's error word like eager steps
+            # do; the word is read back here, at the next step, without blocking.  A step
+            # that reported an error had its flags fixed at capture, so the graph is
+            # dropped and a later step captures again (after a placement failure the
+            # workspace has switched to the device-scope hand-off by then).
+            err = mgr._errword()
+            try:
+                err.poll()
+            except HeteroKVError:
+                self.graph = None
+                self._logits = None
+                raise
             self._ids.copy_(input_ids)
             self._pos.copy_(position_ids)
             self._advance_host(mgr)
             self.graph.replay()
+            err.post()
             out = self._logits
         self.steps += 1
         return out

@@ -339,7 +339,8 @@ def decode_workspace_bytes(batch, num_q_heads, num_kv_heads, int4_max_len, f16_m
 
 class DecodeWorkspace:
     """Zero-initialised scratch for hkv_decode_attn; grows on demand (re-zeroed when it
-    grows; the library clears its ticket area itself when the geometry changes).
+    grows).  Its ticket area has the same offsets for every geometry and the kernels leave
+    it zero, so it serves launches of any geometry in any order, graph replays included.
 
     agent_handoff: launches on this workspace combine their ranges through device-scope
     memory (HKV_DECODE_AGENT_HANDOFF).  It is switched on by placement_failed(), which

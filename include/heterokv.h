@@ -331,11 +331,13 @@ typedef struct HkvDecodeArgs {
  * device-scope atomic per workgroup and reports a violation as HKV_ERR_BIT_PLACEMENT. */
 #define HKV_DECODE_AGENT_HANDOFF 2
 
-/* Workspace rules.  The workspace must be zero-filled before its first use.  The
- * kernels leave their tickets zero after every launch; when the geometry (batch x kv
- * heads, q heads) differs from the previous launch that used the same workspace
- * address, the library clears the ticket area itself (one small kernel on `stream`)
- * before the launch.  Launches that share a workspace must be ordered on one stream. */
+/* Workspace rules.  The workspace must be zero-filled before its first use.  Its
+ * ticket area sits at fixed offsets for up to 1024 split (sequence, kv head) pairs,
+ * whatever the launch geometry, and the kernels leave every ticket zero after a
+ * launch, so one workspace serves launches of any geometry in any order (graph replays
+ * included) with no clearing in between.  A launch that splits more than 1024 pairs
+ * (possible only with splits_hint) fails with HKV_ERR_CAPACITY.  Launches that share a
+ * workspace must be ordered on one stream. */
 
 size_t hkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                                   int32_t head_dim, int32_t int4_max_len,

@@ -176,3 +176,37 @@ def test_decode_graph_rejects_host_work():
     runner = DecodeGraph(None, FusedHeteroCache(num_layers=2, device=DEV))
     with pytest.raises(HeteroKVError):
         runner.step(None, None)      # nothing prefilled yet
+
+
+def test_decode_graph_reports_replay_errors():
+    """A device error raised by a replayed step (here a block-table entry outside the pool,
+    which the decode kernel replaces by a valid record and reports as
+    HKV_ERR_BIT_BLOCK_ID) reaches the caller at the next step, and the graph is dropped so
+    that a later step captures again."""
+    print("case: DecodeGraph error word after a replay", flush=True)
+    from heterokv._lib import HeteroKVError
+    from heterokv.engine_wrapper import ChunkedPrefillEngine, DecodeGraph, FusedHeteroCache
+    model = _tiny_qwen2()
+    ids = torch.randint(0, 512, (1, 300), generator=torch.Generator().manual_seed(2)).to(DEV)
+    cache = FusedHeteroCache(num_layers=2, sink_tokens=16, keep_tail=80, chunk_size=64, device=DEV)
+    runner = DecodeGraph(model, cache)
+    with torch.inference_mode():
+        ChunkedPrefillEngine(model, cache, chunk_size=64).prefill(ids)
+        tok = ids[:, -1:]
+        for step in range(3):                   # eager, captured, replayed
+            runner.step(tok, torch.tensor([[300 + step]], device=DEV))
+        torch.cuda.synchronize()
+        assert runner.graph is not None
+        st = cache._manager._layers[0]
+        assert st.bt is not None and st.int4_len > 0
+        good = st.bt[0, 0].item()
+        st.bt[0, 0] = 1 << 30                   # outside the pool: reported, not read
+        runner.step(tok, torch.tensor([[303]], device=DEV))   # this replay sets the bit
+        torch.cuda.synchronize()
+        st.bt[0, 0] = good
+        with pytest.raises(HeteroKVError, match="block table"):
+            runner.step(tok, torch.tensor([[304]], device=DEV))
+        assert runner.graph is None
+        out = runner.step(tok, torch.tensor([[304]], device=DEV))   # captures again
+        assert torch.isfinite(out).all() and runner.graph is not None
+    runner.close()

@@ -1,6 +1,8 @@
 """hkv_decode_attn_noalloc (the decode entry point that allocates nothing; its scratch is a
 static device array) against hkv_decode_attn with a caller workspace: bitwise equal
-outputs under the fixed block schedule, on two calls in a row, the second smaller, and a
+outputs under the fixed block schedule, on two calls in a row, the second smaller; across
+launches whose (sequence, kv head) pair count changes (32, 8, 32 pairs), eagerly and with a
+graph captured at one pair count and replayed after eager launches at another; and a
 capacity error for a geometry beyond the scratch size."""
 import math
 
@@ -49,6 +51,60 @@ def test_noalloc_matches_workspace_entry(handoff):
         got2 = ops.decode_attention(noalloc=True, agent_handoff=handoff, deterministic=True, err=err, **c)
         torch.cuda.synchronize()
         assert torch.equal(got2, want)
+    err.check()
+
+
+def _fresh(c):
+    from heterokv import ops
+    return ops.decode_attention(workspace=ops.DecodeWorkspace(DEV), deterministic=True, **c)
+
+
+@pytest.mark.parametrize("entry", ["noalloc", "shared_workspace"])
+def test_pair_count_changes(entry):
+    """One scratch (or one shared workspace) used by launches of 32, 8 and again 32 pairs:
+    every output equals a fresh workspace's, bit for bit."""
+    from heterokv import ops
+    big = _inputs(4, 4, 32, 8, 64, 3000, 512)     # 4 x 8 = 32 pairs
+    small = _inputs(5, 1, 32, 8, 64, 9000, 1024)  # 8 pairs, more ranges each
+    ws = ops.DecodeWorkspace(DEV)
+    err = ops.ErrorWord(DEV)
+    want = {"big": _fresh(big), "small": _fresh(small)}
+    for step, (name, c) in enumerate([("big", big), ("small", small), ("big", big), ("small", small)]):
+        print("case: %s, launch %d, %s geometry" % (entry, step, name), flush=True)
+        if entry == "noalloc":
+            got = ops.decode_attention(noalloc=True, deterministic=True, err=err, **c)
+        else:
+            got = ops.decode_attention(workspace=ws, deterministic=True, err=err, **c)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want[name])
+    err.check()
+
+
+def test_noalloc_graph_replay_across_pair_counts():
+    """A graph that captured the allocation-free decode at 32 pairs, replayed after eager
+    launches at 8 pairs (whose partial states land where nothing of the 32-pair launch's
+    tickets lives), gives the eager 32-pair output on every replay."""
+    from heterokv import ops
+    big = _inputs(6, 4, 32, 8, 64, 3000, 512)
+    small = _inputs(7, 1, 32, 8, 64, 9000, 1024)
+    err = ops.ErrorWord(DEV)
+    want_big, want_small = _fresh(big), _fresh(small)
+    out = torch.empty_like(want_big)
+    ops.decode_attention(noalloc=True, deterministic=True, err=err, out=out, **big)   # eager, 32 pairs
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=DEV)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        ops.decode_attention(noalloc=True, deterministic=True, err=err, out=out, **big)
+    for rep in range(4):
+        print("case: graph replay %d after an eager 8-pair launch" % rep, flush=True)
+        got_small = ops.decode_attention(noalloc=True, deterministic=True, err=err, **small)
+        torch.cuda.synchronize()
+        assert torch.equal(got_small, want_small)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want_big)
     err.check()
 
 
