@@ -588,6 +588,119 @@ def bench_probe(torch, args):
     return line
 
 
+TIMELINE_LIB = os.path.join(ROOT, "hetero-kvcache-optimizer_amd", "heterokv", "libheterokv_timeline.so")
+
+
+def bench_timeline(torch, args):
+    """Phase timeline of the 32K decode kernel, from the library's timeline build
+    (HKV_DECODE_TIMELINE: every wave stamps the 100 MHz constant clock at its phase
+    boundaries).  The stamps of each sampled launch are read back and reduced to: first data
+    consumed (INT4 and fp16 ranges), block ids of the INT4 ranges in LDS, streaming end
+    per workgroup (INT4 ranges and fp16 ranges), partial states stored, the last ticket,
+    the final merge's loads and the output write of each pair's last workgroup.  A graph of
+    the 8 launches is replayed and the stamps of its last launch are read (launches back to
+    back, as in the headline bench).  Times are microseconds from that launch's first wave
+    start; figures are medians over the samples."""
+    import ctypes
+    import numpy as np
+    from heterokv import _lib
+    _lib.LIB_PATH = TIMELINE_LIB
+    from heterokv import ops
+    lib = _lib.load()
+    lib.hkv_decode_timeline_read.restype = ctypes.c_int64
+    lib.hkv_decode_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    dev = torch.device("cuda:0")
+    q, K, V = make_inputs(torch)
+    R = args.copies
+    bt = torch.arange((MID + 15) // 16, dtype=torch.int32, device=dev)[None]
+    copies = [build_copy(torch, ops, q, K, V, dev, bt) for _ in range(R)]
+    q_dev = q.to(dev)
+    out = torch.empty((B, HQ, D), dtype=torch.float16, device=dev)
+    ws = ops.DecodeWorkspace(dev)
+    err = ops.ErrorWord(dev)
+
+    def launch(i):
+        c = copies[i % R]
+        ops.decode_attention(q_dev, zones=c["zones"], pool=c["pool"], block_table=c["bt"], int4_max_len=MID,
+                             workspace=ws, out=out, deterministic=args.deterministic, err=err)
+
+    for i in range(max(args.warmup, R)):
+        launch(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(R):
+            launch(i)
+    g.replay()
+    torch.cuda.synchronize()
+    buf = np.zeros((16384, 16), dtype=np.uint64)
+    keys = ("first_data_int4_p50", "first_data_f16_p50", "ids_in_lds_int4_p50", "ids_in_lds_int4_max",
+            "stream_end_int4_p50", "stream_end_int4_max", "stream_end_f16_p50", "stream_end_f16_max",
+            "stream_end_all_min", "partials_stored_max", "last_ticket_max", "final_loads_done_max",
+            "output_written_max")
+    samples = {k: [] for k in keys}
+    per_xcd = []
+    n_s = max(min(args.steps, 256), 8)
+    for i in range(n_s):
+        g.replay()   # the stamps of the graph's last launch (steady state, launches back to back)
+        n = lib.hkv_decode_timeline_read(buf.ctypes.data_as(ctypes.c_void_p), buf.shape[0])
+        if n <= 0:
+            raise RuntimeError("timeline read failed (%d)" % n)
+        t = buf[:n].astype(np.int64)
+        t0 = t[:, 0].min()
+        us = lambda col: (t[:, col] - t0) / 100.0   # noqa: E731  (100 MHz clock)
+        info = t[:, 7]
+        n4 = (info >> 24) & 0xFFFFFF
+        nfw = info & 0xFFFFFF
+        xcd = (info >> 56) & 0xF
+        last = ((info >> 48) & 1) == 1
+        wg = np.arange(n) // 8
+        int4_rng = (n4 > 0) & (nfw == 0)
+        f16_rng = (nfw > 0) & (n4 == 0)
+        end_wg = np.array([us(2)[wg == w].max() for w in range(n // 8)])
+        kind4 = np.array([int4_rng[w * 8] for w in range(n // 8)])
+        kindf = np.array([f16_rng[w * 8] for w in range(n // 8)])
+        ids = us(1)[int4_rng]
+        first = us(8)
+        samples["first_data_int4_p50"].append(float(np.median(first[int4_rng])) if int4_rng.any() else None)
+        samples["first_data_f16_p50"].append(float(np.median(first[f16_rng])) if f16_rng.any() else None)
+        samples["ids_in_lds_int4_p50"].append(float(np.median(ids)) if ids.size else None)
+        if os.environ.get("HKV_TIMELINE_WAITS") == "1":
+            for key, col, sel in (("prologue_in_f16_p50", 9, f16_rng), ("prologue_in_int4_p50", 10, int4_rng)):
+                samples.setdefault(key, []).append(float(np.median(us(col)[sel])) if sel.any() else None)
+        samples["ids_in_lds_int4_max"].append(float(ids.max()) if ids.size else None)
+        for name, sel in (("int4", kind4), ("f16", kindf)):
+            e = end_wg[sel]
+            samples["stream_end_%s_p50" % name].append(float(np.median(e)) if e.size else None)
+            samples["stream_end_%s_max" % name].append(float(e.max()) if e.size else None)
+        samples["stream_end_all_min"].append(float(end_wg.min()))
+        samples["partials_stored_max"].append(float(us(3).max()))
+        samples["last_ticket_max"].append(float(us(4)[last].max()) if last.any() else None)
+        samples["final_loads_done_max"].append(float(us(5)[last].max()) if last.any() else None)
+        samples["output_written_max"].append(float(us(6)[last].max()) if last.any() else None)
+        per_xcd.append([float(end_wg[np.array([xcd[w * 8] for w in range(n // 8)]) == x].max())
+                        for x in range(8) if (xcd == x).any()])
+    err.check()
+    med = {k: (round(float(np.median([v for v in vals if v is not None])), 3)
+               if any(v is not None for v in vals) else None) for k, vals in samples.items()}
+    line = {
+        "metric": "INT4-KV decode kernel phase timeline at 32K ctx (us from the first wave's start)",
+        "value": med["output_written_max"], "unit": "us", "n_gpus": 1, "steps": n_s, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (the 32K decode workload's seeded K/V)",
+        "config": {"workload": "single-layer INT4-KV decode attention, batch 1, 32 q / 8 kv heads, ctx 32768 = "
+                               "64 fp16 sink + 28608 INT4 + 4096 fp16 recent; timeline build of the library, "
+                               "last launch of a replayed 8-launch graph",
+                   "phases_us_median": med,
+                   "stream_end_max_per_xcd_us_median": [round(float(x), 3) for x in np.median(np.array(per_xcd), 0)],
+                   "waves_per_launch": int(n)},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    return line
+
+
 T_LAYERS, T_HQ, T_HKV, T_HIDDEN, T_INTER, T_VOCAB = 28, 28, 4, 3584, 18944, 152064
 T_CTX, T_CHUNK, T_SINK, T_KEEP, T_HOST_FRAC = 131072, 2048, 64, 4160, 0.75
 
@@ -928,11 +1041,13 @@ def main():
                     help="nested configuration blocks of the default line: any of c1 (quantize+pack), c3 (batched "
                          "paged decode), c4 (chunked prefill), c5 (128K tiered decode with 75%% host offload); "
                          "'none' for the 32K decode alone")
-    ap.add_argument("--workload", choices=["decode", "prefill", "tiered", "paged", "scoring", "quant", "probe"],
+    ap.add_argument("--workload",
+                    choices=["decode", "prefill", "tiered", "paged", "scoring", "quant", "probe", "timeline"],
                     default=None,
                     help="run one configuration alone and print its block as the line (for profiling): decode "
                          "(32K), prefill (C4), tiered (C5), paged (C3), quant (C1), scoring (heavy hitters), probe "
-                         "(streaming-read probes at the decode's byte count)")
+                         "(streaming-read probes at the decode's byte count), timeline (the 32K decode kernel's "
+                         "phase timeline from the library's timeline build)")
     ap.add_argument("--probe-shapes", default=None,
                     help="probe shapes pattern:workgroups:waves:depth, comma-separated (pattern contig or parts)")
     ap.add_argument("--copy-calibration", type=float, default=0.0,
@@ -963,7 +1078,8 @@ def main():
 
     single = {"prefill": lambda: leg_c4(torch, ops, args), "paged": lambda: leg_c3(torch, ops, args),
               "quant": lambda: leg_c1(torch, ops, args), "tiered": lambda: leg_c5(torch, args),
-              "scoring": lambda: bench_scoring(torch, ops, args), "probe": lambda: bench_probe(torch, args)}
+              "scoring": lambda: bench_scoring(torch, ops, args), "probe": lambda: bench_probe(torch, args),
+              "timeline": lambda: bench_timeline(torch, args)}
     if args.workload in single:
         blk = single[args.workload]()
         if blk is not None:

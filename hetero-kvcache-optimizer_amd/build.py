@@ -2,20 +2,26 @@
 
     python hetero-kvcache-optimizer_amd/build.py
 
-Compiles every csrc/*.hip file with hipcc for gfx950 into
-heterokv/libheterokv.so.  Correctly rounded fp32 division/sqrt stay on (the
-quantizer is bit-exact with an IEEE reference) and packed-fp32 instructions are
-disabled for device code.  The streaming-read probes (csrc/probe/*.hip, used by
-bench.py's probe workload only) go into heterokv/libhkvprobe.so.
+Compiles every csrc/*.hip file with hipcc for gfx950 (one object per file, in
+parallel, under _build/) and links heterokv/libheterokv.so.  Correctly rounded fp32
+division/sqrt stay on (the quantizer is bit-exact with an IEEE reference) and
+packed-fp32 instructions are disabled for device code.  Two measurement libraries are
+linked beside it, for bench.py only: heterokv/libheterokv_timeline.so (the same
+library with the decode kernel built with HKV_DECODE_TIMELINE, which records per-wave
+phase timestamps) and heterokv/libhkvprobe.so (the streaming-read probes of
+csrc/probe/).
 """
 import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
+BUILD_DIR = os.path.join(PKG_DIR, "_build")
 OUT = os.path.join(PKG_DIR, "heterokv", "libheterokv.so")
+TIMELINE_OUT = os.path.join(PKG_DIR, "heterokv", "libheterokv_timeline.so")
 PROBE_OUT = os.path.join(PKG_DIR, "heterokv", "libhkvprobe.so")
 
 HIPCC_FLAGS = [
@@ -23,7 +29,6 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "--offload-arch=gfx950",
     "-fPIC",
-    "-shared",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-fno-fast-math",
     "-ffp-contract=on",
@@ -35,6 +40,7 @@ HIPCC_FLAGS = [
     "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wno-unused-command-line-argument",
 ]
+LINK_FLAGS = ["--offload-arch=gfx950", "-fPIC", "-shared"]
 
 
 def hipcc_path():
@@ -50,28 +56,45 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(srcs, out_path, verbose):
-    tmp = out_path + ".tmp"
-    cmd = [hipcc_path()] + HIPCC_FLAGS + ["-o", tmp] + srcs
+def _run(cmd, verbose):
     if verbose:
         print("[heterokv] " + " ".join(cmd), flush=True)
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    out = res.stdout
     # the host pass does not know the device-only feature name; that warning is expected
-    lines = [ln for ln in out.splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
+    lines = [ln for ln in res.stdout.splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
     if res.returncode != 0:
-        sys.stderr.write(out)
-        raise RuntimeError("hipcc failed with exit code %d" % res.returncode)
+        sys.stderr.write(res.stdout)
+        raise RuntimeError("hipcc failed with exit code %d: %s" % (res.returncode, " ".join(cmd[-3:])))
     if verbose and lines:
         print("\n".join(lines), flush=True)
+
+
+def _link(objs, out_path, verbose):
+    tmp = out_path + ".tmp"
+    _run([hipcc_path()] + LINK_FLAGS + ["-o", tmp] + objs, verbose)
     os.replace(tmp, out_path)
 
 
 def build(verbose=True):
-    _compile(sources(), OUT, verbose)
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    hipcc = hipcc_path()
+    jobs = []   # (source, object, extra flags)
+    for src in sources():
+        jobs.append((src, os.path.join(BUILD_DIR, os.path.basename(src) + ".o"), []))
+    timeline_obj = os.path.join(BUILD_DIR, "decode_attn_timeline.o")
+    jobs.append((os.path.join(CSRC, "decode_attn.hip"), timeline_obj, ["-DHKV_DECODE_TIMELINE"]))
     probe_dir = os.path.join(CSRC, "probe")
-    _compile(sorted(os.path.join(probe_dir, f) for f in os.listdir(probe_dir) if f.endswith(".hip")), PROBE_OUT,
-             verbose)
+    probe_srcs = sorted(os.path.join(probe_dir, f) for f in os.listdir(probe_dir) if f.endswith(".hip"))
+    for src in probe_srcs:
+        jobs.append((src, os.path.join(BUILD_DIR, "probe_" + os.path.basename(src) + ".o"), []))
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", "0")) or os.cpu_count() or 4, 16))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        list(ex.map(lambda j: _run([hipcc] + HIPCC_FLAGS + j[2] + ["-c", "-o", j[1], j[0]], verbose), jobs))
+    lib_objs = [o for s, o, f in jobs[:len(sources())]]
+    _link(lib_objs, OUT, verbose)
+    _link([timeline_obj if os.path.basename(o) == "decode_attn.hip.o" else o for o in lib_objs], TIMELINE_OUT,
+          verbose)
+    _link([o for s, o, f in jobs if os.path.basename(o).startswith("probe_")], PROBE_OUT, verbose)
     return OUT
 
 

@@ -40,6 +40,7 @@
 #include "nibble_decode.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -62,6 +63,10 @@ static_assert((kHeadDim * 4) % 8 == 0 && (kPartStride * 4) % 16 == 0, "m, l load
 #define HKV_DECODE_PREFETCH 2
 #endif
 constexpr int kPrefetch = HKV_DECODE_PREFETCH;  // INT4 block pairs in flight per wave
+#ifndef HKV_DECODE_F16_DEPTH
+#define HKV_DECODE_F16_DEPTH 2
+#endif
+constexpr int kF16Depth = HKV_DECODE_F16_DEPTH;  // fp16 zone tiles in flight per wave
 constexpr int kMaxSplits = 64;
 // INT4 tokens, and fp16 tokens over all zones, per sequence: 2^22 items of 16 tokens
 // keep the range arithmetic in 32 bits.
@@ -70,6 +75,35 @@ constexpr int kIdWindow = 1024;           // INT4 block ids staged in LDS at a t
 constexpr int kIdPerThread = kIdWindow / kThreads;
 static_assert(kIdWindow % kThreads == 0, "whole id entries per thread");
 constexpr float kLog2e = 1.4426950408889634f;
+
+// Timeline build (HKV_DECODE_TIMELINE, libheterokv_timeline.so, for measurement only):
+// every wave records the 100 MHz constant clock at the phase boundaries below and lane 0
+// writes them, with the wave's XCD and range, as eight words at exit.
+//   [0] start  [1] first id window in LDS  [2] streaming done  [3] partial state stored
+//   [4] ticket known  [5] final merge loads done  [6] output written  [7] info
+//   [8] first unit's data consumed (end of the first step)
+//   [9] fp16 prologue loads arrived, [10] INT4 prologue loads arrived (only with
+//       HKV_TIMELINE_WAITS=1 in the environment: the wave then waits for both slots before
+//       its first step, which the measured kernel does not)
+#ifdef HKV_DECODE_TIMELINE
+constexpr int kTlMaxWaves = 16384;
+constexpr int kTlWords = 16;
+#define TL_MARK(i) (tl_t[i] = __builtin_amdgcn_s_memrealtime())
+#define TL_FLUSH(info)                                                                              \
+    do {                                                                                            \
+        if (lane == 0 && p.tl && blockIdx.x * kWaves + wave < kTlMaxWaves) {                        \
+            unsigned long long* _d = p.tl + ((size_t)blockIdx.x * kWaves + wave) * kTlWords;         \
+            for (int _i = 0; _i < 7; ++_i) _d[_i] = tl_t[_i];                                       \
+            _d[7] = (info);                                                                         \
+            _d[8] = tl_t[7];                                                                        \
+            _d[9] = tl_w[0];                                                                        \
+            _d[10] = tl_w[1];                                                                       \
+        }                                                                                           \
+    } while (0)
+#else
+#define TL_MARK(i) ((void)0)
+#define TL_FLUSH(info) ((void)0)
+#endif
 // Bytes one kv head reads per item (the weights that balance the ranges).
 constexpr int64_t kInt4ItemBytes = kBlockTokens * (kHeadDim / 2 + 5) * 2;   // 2208
 constexpr int64_t kF16ItemBytes = kBlockTokens * kHeadDim * 2 * 2;           // 8192
@@ -120,6 +154,10 @@ struct DecodeParams {
     int64_t sc_sb, sc_sh;
     int sc_zone[HKV_MAX_F16_ZONES];
     float* stats;              // [B][Hq][2]: the softmax max and sum of each row
+#ifdef HKV_DECODE_TIMELINE
+    unsigned long long* tl;    // per-wave phase timestamps (timeline build only)
+    int tl_waits;              // 1: also wait for the prologue loads and stamp their arrival
+#endif
 };
 
 // Partial states cross workgroups (and XCDs) through agent-scope relaxed atomic
@@ -525,6 +563,11 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     const int kzsh = 8 * (c & 3);
     const int nrep = p.nrep;
     unsigned owner_old = 0u, owner_bit = 0u;   // placement check (below, after the streaming)
+#ifdef HKV_DECODE_TIMELINE
+    unsigned long long tl_t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    unsigned long long tl_w[2] = {0, 0};
+    TL_MARK(0);
+#endif
 
     const int len4 = p.int4_lens ? min(max(p.int4_lens[b], 0), p.int4_max_len) : p.int4_max_len;
     int lenz[HKV_MAX_F16_ZONES];
@@ -602,7 +645,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     __shared__ int sm_ctr[2];   // next INT4 pair, next fp16 tile (kDynamic)
     if (kDynamic && threadIdx.x == 0) {
         sm_ctr[0] = kPrefetch * kWaves;   // the first round of each window is static
-        sm_ctr[1] = 2 * kWaves;
+        sm_ctr[1] = kF16Depth * kWaves;
     }
 
     // ---- fp16 zone tiles f0 .. f0 + nf, depth 2.  Every slot of a round is
@@ -612,13 +655,13 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     // on which the later slots were not refilled, and the waits at the loop head
     // would then drain every slot.
     if (nf > 0) {
-        F16Tile buf[2];
-        int tq[2];
-        ZoneP zq[2];
-        int lq[2];
-        int seq = wave + 2 * kWaves;
+        F16Tile buf[kF16Depth];
+        int tq[kF16Depth];
+        ZoneP zq[kF16Depth];
+        int lq[kF16Depth];
+        int seq = wave + kF16Depth * kWaves;
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
+        for (int k = 0; k < kF16Depth; ++k) {
             tq[k] = wave + k * kWaves;
             int t;
             locate_tile(p, zt, lenz, f0 + min(tq[k], nf - 1), zq[k], lq[k], t);
@@ -627,14 +670,21 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             __builtin_amdgcn_sched_barrier(0);
             lq[k] -= t * kBlockTokens;
         }
+#ifdef HKV_DECODE_TIMELINE
+        if (p.tl_waits) {
+            __builtin_amdgcn_s_waitcnt(0);
+            tl_w[0] = __builtin_amdgcn_s_memrealtime();
+        }
+#endif
         // the first INT4 window's ids arrive with these tiles (they were requested
         // first); they and the counters are published before the loop starts
         if (a1 > a0) commit_block_ids(p, min(kIdWindow, a1 - a0), idr, sm_ids);
         __syncthreads();
+        TL_MARK(1);
         if (tq[0] < nf) {
             do {
 #pragma unroll
-                for (int k = 0; k < 2; ++k) {
+                for (int k = 0; k < kF16Depth; ++k) {
                     if constexpr (kScores) {
                         int zi, t;
                         locate_zone(zt, f0 + min(tq[k], nf - 1), zi, t);
@@ -645,6 +695,9 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                     } else {
                         step_f16(buf[k], tq[k] < nf ? min(kBlockTokens, lq[k]) : 0, g, qf, p.scale_log2, acc, m, l);
                     }
+#ifdef HKV_DECODE_TIMELINE
+                    if (tl_t[7] == 0) TL_MARK(7);
+#endif
                     tq[k] = next_unit<kDynamic>(&sm_ctr[1], seq);
                     int t;
                     locate_tile(p, zt, lenz, f0 + min(tq[k], nf - 1), zq[k], lq[k], t);
@@ -663,6 +716,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     if (nf <= 0 && a1 > a0) {
         commit_block_ids(p, min(kIdWindow, a1 - a0), idr, sm_ids);
         __syncthreads();
+        TL_MARK(1);
     }
     for (int wb = a0; wb < a1; wb += kIdWindow) {
         const int wn = min(kIdWindow, a1 - wb);
@@ -687,6 +741,12 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             load_int4(p, h, __builtin_amdgcn_readfirstlane((int)id.y), 2 * pk[k] + 1 < wn, c, g, bufB[k]);
             __builtin_amdgcn_sched_barrier(0);
         }
+#ifdef HKV_DECODE_TIMELINE
+        if (p.tl_waits && wb == a0) {
+            __builtin_amdgcn_s_waitcnt(0);
+            tl_w[1] = __builtin_amdgcn_s_memrealtime();
+        }
+#endif
         int nxt = next_unit<kDynamic>(&sm_ctr[0], seq);
         u2 nid = read_pair_ids(sm_ids, min(nxt, npairs - 1));
         if (pk[0] < npairs) {
@@ -702,6 +762,9 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                                              srow + (lb + 1) * kBlockTokens + 4 * g);
                     else
                         step_int4_pair(bufA[k], bufB[k], nA, nB, g, kzsh, qf, p.scale_log2, acc, m, l);
+#ifdef HKV_DECODE_TIMELINE
+                    if (tl_t[7] == 0) TL_MARK(7);
+#endif
                     pk[k] = nxt;
                     __builtin_amdgcn_sched_barrier(0);
                     load_int4(p, h, __builtin_amdgcn_readfirstlane((int)nid.x), nxt < npairs, c, g, bufA[k]);
@@ -718,6 +781,11 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         }
     }
 
+    TL_MARK(2);
+#ifdef HKV_DECODE_TIMELINE
+    const unsigned long long tl_info = ((unsigned long long)(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15) << 56) |
+                                       ((unsigned long long)(unsigned)(a1 - a0) << 24) | (unsigned)max(nf, 0);
+#endif
     // XCD-local hand-off: OR this workgroup's XCD bit (HW_REG_XCC_ID) into the pair's
     // device-scope mask; the old mask is examined at the ticket.  Issued here, its round
     // trip overlaps the merge below.  (At the start of the kernel it cost ~1.7 us on the
@@ -787,7 +855,11 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             }
         }
     }
-    if (nsplit == 1) return;
+    TL_MARK(3);
+    if (nsplit == 1) {
+        TL_FLUSH(tl_info);
+        return;
+    }
     // every lane waits until its agent-coherent stores have completed, then the
     // barrier makes that true for the whole workgroup before the ticket is taken
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -817,7 +889,11 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         sm_ticket = tk;
     }
     __syncthreads();
-    if (sm_ticket != nsplit - 1) return;
+    TL_MARK(4);
+    if (sm_ticket != nsplit - 1) {
+        TL_FLUSH(tl_info);
+        return;
+    }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
     // ---- last workgroup of this pair: merge the nsplit partial states in one
@@ -871,6 +947,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         w[5] = O[3];
     }
     __syncthreads();
+    TL_MARK(5);
     if (threadIdx.x < units) {
         const int u = threadIdx.x;
         const int hd = u / (kHeadDim / 4), d4 = (u % (kHeadDim / 4)) * 4;
@@ -895,6 +972,8 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             st[1] = L;
         }
     }
+    TL_MARK(6);
+    TL_FLUSH(tl_info | (1ull << 48));
     // last in the kernel, so that no barrier waits for these stores: every workgroup of
     // the pair has taken its ticket, so its mask update is done
     if (threadIdx.x == 0) {
@@ -1001,6 +1080,25 @@ extern "C" size_t hkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads,
         return 0;
     return workspace_bytes(batch, num_q_heads, num_kv_heads, kMaxSplits);
 }
+
+#ifdef HKV_DECODE_TIMELINE
+static __device__ unsigned long long g_timeline[kTlMaxWaves * kTlWords];
+static int64_t g_timeline_waves = 0;
+
+// Copies the timestamps of the last decode launch (16 words per wave, workgroup-major)
+// into `host` (room for max_waves waves); returns the number of waves copied.  Waits for
+// the device.  Timeline build only.
+extern "C" int64_t hkv_decode_timeline_read(unsigned long long* host, int64_t max_waves) {
+    int64_t n = g_timeline_waves < max_waves ? g_timeline_waves : max_waves;
+    if (n > kTlMaxWaves) n = kTlMaxWaves;
+    if (!host || n <= 0) return 0;
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    if (hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline), (size_t)n * kTlWords * sizeof(unsigned long long), 0,
+                            hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    return n;
+}
+#endif
 
 // The launch behind both decode entry points: `wsp` / `ws_bytes` is the caller's
 // workspace (hkv_decode_attn) or this device's static scratch (hkv_decode_attn_noalloc).
@@ -1112,6 +1210,19 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
     // one range per pair needs no hand-off (and must not leave a mask bit behind)
     p.xcc_local = (BH % p.nxcc) == 0 && ms > 1 && !(a->flags & HKV_DECODE_AGENT_HANDOFF) ? 1 : 0;
     p.max_splits = ms;
+#ifdef HKV_DECODE_TIMELINE
+    {
+        static unsigned long long* tl_ptr[64] = {};
+        int dev = 0;
+        HKV_HIP_CHECK(hipGetDevice(&dev));
+        HKV_REQUIRE(dev >= 0 && dev < 64, HKV_ERR_UNSUPPORTED, "timeline: device %d", dev);
+        if (!tl_ptr[dev]) HKV_HIP_CHECK(hipGetSymbolAddress((void**)&tl_ptr[dev], HIP_SYMBOL(g_timeline)));
+        p.tl = tl_ptr[dev];
+        const char* w = getenv("HKV_TIMELINE_WAITS");
+        p.tl_waits = (w && w[0] == '1') ? 1 : 0;
+        g_timeline_waves = (int64_t)BH * ms * kWaves;
+    }
+#endif
     p.scores = a->scores;
     p.sc_sb = a->scores_stride_b;
     p.sc_sh = a->scores_stride_h;
