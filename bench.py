@@ -188,7 +188,9 @@ P_ROWS = list(range(0, 32)) + list(range(P_SQ - 32, P_SQ))   # CPU sample / pari
 
 
 def leg_c4(torch, ops, args):
-    """Chunked prefill (one hkv_prefill_attn call: the INT4 kernel, then the zone kernel): 2048 fp16
+    """Chunked prefill (one hkv_prefill_attn call: the chunk rewrite into the zone layout, the zone
+    kernel over the fp16 zones and the chunk, then the INT4 kernel, which merges the zone kernel's
+    softmax state into its own; all three inside the timed call): 2048 fp16
     queries, 32 q / 8 kv heads, over 64 fp16 sink + 131072 INT4 + 4096 fp16 recent tokens plus the
     chunk itself, causally."""
     from oracle import torch_ref as tr

@@ -7,10 +7,12 @@
 // INT4 token (dequantized as (code - zero point) x scale), every fp16 zone token and the
 // chunk's own tokens t <= q (causal), GQA q head i -> kv head i / n_rep.
 //
-// INT4 tiles are staged into LDS as fp16 K rows (code - zero point) x K scale x sm_scale
-// x log2 e and V^T rows (code - zero point) x V scale, so the scores come out of the
-// MFMAs in the log2 domain; each element takes the one fp16 rounding that dequantizing
-// to fp16 takes.
+// INT4 tiles are staged into LDS as fp16 K rows (code - zero point) x K scale and V^T
+// rows (code - zero point) x V scale; the queries carry sm_scale x log2 e (rounded to
+// fp16 once, as in the zone kernel), so the scores come out of the MFMAs in the log2
+// domain.  The staging rounds the scale to fp16 and then the product: two roundings,
+// within about 1.5 fp16 ulps of the Path C dequantization's one while the scale is at
+// least 2^-14 (store_k4 / store_v4).
 #include "nibble_decode.h"
 #include "prefill_flat.h"
 
@@ -85,17 +87,25 @@ __device__ __forceinline__ void load_v4(const PrefillParams& p, int h, int id, i
     s.vs = __builtin_bit_cast(f4, bld16(r, kPartVs + g * 16));
     s.vz = bld4(r, kPartVz + g * 4);
 }
-// Writes a staged block into LDS: K as (code - zero point) x K scale x sm_scale x log2 e
-// with the per-token biases, V as (code - zero point) x V scale; `valid` = valid tokens
-// of the block.  Tokens past it get scale 0 (their codes are finite, their scales may be
-// anything) and bias -inf.
-__device__ __forceinline__ void store_k4(const SlotK& s, uint8_t* lds, uint8_t* bias, float scale_log2, int wt,
-                                         int lane, int valid) {
+// Writes a staged block into LDS: K as (code - zero point) x K scale with the per-token
+// biases, V as (code - zero point) x V scale (the queries carry sm_scale x log2 e, so the
+// scores come out of the MFMAs in the log2 domain); `valid` = valid tokens of the block.
+// Tokens past it get scale 0 (their codes are finite, their scales may be anything) and
+// bias -inf.
+//
+// Rounding.  The products are formed in packed fp16: the scale is rounded to fp16, then
+// each product, so a staged element lies within about 1.5 fp16 ulps of the reference's
+// dequantized value ((code - zp) x scale in float32, then .to(float16),
+// kv_compressor.py:129-132) while the scale is at least 2^-14.  A smaller scale becomes
+// an fp16 subnormal with fewer significant bits (about 2% error at 1e-6).  Keeping the
+// softmax scale on the queries (not folded into K, which would make every K scale 8x
+// smaller) keeps K's scales as far from that range as the reference's own fp16 keys.
+__device__ __forceinline__ void store_k4(const SlotK& s, uint8_t* lds, uint8_t* bias, int wt, int lane, int valid) {
     const int rr = lane >> 2, pt = lane & 3;
     const int tok = wt * 16 + rr;
     const uint32_t kz = s.kz & 0xFFu;
     const h2 kz1024 = zp1024(kz, kz), kz64 = zp64(kz, kz);
-    const _Float16 f = (_Float16)(rr < valid ? s.ks * scale_log2 : 0.0f);
+    const _Float16 f = (_Float16)(rr < valid ? s.ks : 0.0f);
     const h2 f2 = {f, f};
     const uint32_t w4[4] = {s.w.x, s.w.y, s.w.z, s.w.w};
 #pragma unroll
@@ -151,7 +161,7 @@ struct Int4Stage {
         else load_v4(p, w.h, id, w.lane, sl);
     }
     __device__ void stage(int s, uint8_t* buf, uint8_t* bias, int x) const {
-        if constexpr (kTeam == 0) store_k4(ring[s], buf, bias, p.scale_log2, w.wt, w.lane, valid(x));
+        if constexpr (kTeam == 0) store_k4(ring[s], buf, bias, w.wt, w.lane, valid(x));
         else store_v4(ring[s], buf, w.wt, w.lane, valid(x));
     }
     __device__ void refill(int s, int x) {   // tile x just staged from slot s
@@ -196,7 +206,7 @@ __global__ __launch_bounds__(kFlatThreads, 1) void prefill_attn_kernel(PrefillPa
     if (tm.n4 == 0) return;
 
     ph8 qf[8];
-    flat_load_q(p, b, qh, head_ok && qrow < p.Sq, qrow, hh, 1.0f, qf);
+    flat_load_q(p, b, qh, head_ok && qrow < p.Sq, qrow, hh, p.scale_log2, qf);   // q carries sm_scale x log2 e
     pf16v acc[4];
     float m = -INFINITY, l = 0.f;
 #pragma unroll

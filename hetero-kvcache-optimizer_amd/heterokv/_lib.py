@@ -34,7 +34,7 @@ _ERR_BIT_TEXT = {
     ERR_BIT_SLOT: "a token slot lay beyond its block table row",
     ERR_BIT_PLACEMENT: "decode ranges of one (sequence, kv head) ran on more than one XCD; that launch's "
                        "output is invalid (later launches use the device-scope hand-off)",
-    ERR_BIT_RANGE: "a finite bf16 value beyond the fp16 range (|x| > 65504) was narrowed to fp16",
+    ERR_BIT_RANGE: "a finite bf16 or fp32 value beyond the fp16 range (|x| > 65504) was narrowed to fp16",
 }
 
 

@@ -334,13 +334,20 @@ def register_attention() -> str:
 
 
 class ChunkedPrefillEngine:
-    """engine_wrapper.py:411-496: feeds a long prompt through the model in chunks."""
+    """engine_wrapper.py:411-496: feeds a long prompt through the model in chunks.
 
-    def __init__(self, model, cache: FusedHeteroCache, chunk_size: int = 2048, verbose: bool = False):
+    After every chunk it schedules a prefetch of every chunk key in the DRAM table, as the
+    reference does (:484-486), so the prefetcher's side stream dequantizes the stored
+    chunks while the next chunk runs; prefetch_after_chunk=False skips that (the
+    attention outputs are the same either way)."""
+
+    def __init__(self, model, cache: FusedHeteroCache, chunk_size: int = 2048, verbose: bool = False,
+                 prefetch_after_chunk: bool = True):
         self.model = model
         self.cache = cache
         self.chunk_size = chunk_size
         self.verbose = verbose
+        self.prefetch_after_chunk = prefetch_after_chunk
 
     @torch.inference_mode()
     def prefill(self, input_ids: torch.Tensor, position_ids: Optional[torch.Tensor] = None,
@@ -366,6 +373,9 @@ class ChunkedPrefillEngine:
                               position_ids=chunk_pos, attention_mask=chunk_mask, cache_position=chunk_cache_pos)
             if self.verbose:
                 print("  chunk [%6d:%6d] dram_entries=%d" % (start, end, len(self.cache.dram_table)), flush=True)
+            if self.prefetch_after_chunk and self.cache._manager is not None:
+                for key in list(self.cache.dram_table.keys()):
+                    self.cache.schedule_prefetch(key)
             chunk_idx += 1
             if chunk_idx % 4 == 0 or end == total_len:
                 gc.collect()

@@ -56,6 +56,18 @@ def _as_4d(t):
     return t
 
 
+def _as_kernel_q(q: torch.Tensor, err) -> torch.Tensor:
+    """q in a dtype the kernels take: fp16 and bf16 as they are (the kernels range-check a
+    bf16 q themselves); any other floating dtype is rounded to fp16, and a finite value
+    beyond the fp16 range (which would become inf) sets HKV_ERR_BIT_RANGE in `err` on the
+    device, reported like the kernels' own range errors (no host synchronization)."""
+    if q.dtype in (torch.float16, torch.bfloat16):
+        return q
+    over = (q.abs() > 65504.0) & torch.isfinite(q)
+    torch.bitwise_or(err.dev, over.any().to(torch.int32) * _lib.ERR_BIT_RANGE, out=err.dev)
+    return q.to(torch.float16)
+
+
 def fused_dequant_attn_decode(q: torch.Tensor, k_data: torch.Tensor, k_scales: torch.Tensor,
                               k_zps: torch.Tensor, v_data: torch.Tensor, v_scales: torch.Tensor,
                               v_zps: torch.Tensor, sm_scale: Optional[float] = None) -> torch.Tensor:
@@ -80,7 +92,7 @@ def fused_dequant_attn_decode(q: torch.Tensor, k_data: torch.Tensor, k_scales: t
     bt = torch.arange(B * nblk, dtype=torch.int32, device=q.device).reshape(B, nblk)
     start = torch.zeros(B, dtype=torch.int32, device=q.device)
     ops.repack_codes(pool, kd, vd, ks, vs, kz, vz, start, bt, err=err)
-    qq = q if q.dtype in (torch.float16, torch.bfloat16) else q.to(torch.float16)
+    qq = _as_kernel_q(q, err)
     out = ops.decode_attention(qq, zones=(), pool=pool, block_table=bt, int4_lens=None, int4_max_len=S,
                                sm_scale=sm_scale, workspace=_WS[q.device], err=err, out_dtype=qq.dtype)
     err.post()
@@ -112,7 +124,7 @@ def fused_dequant_attn_forward(q: torch.Tensor, k_data: torch.Tensor, k_scales: 
     err = _errword(q.device)
     err.poll()
     pool, bt, S = _repack_reference(q, k_data, k_scales, k_zps, v_data, v_scales, v_zps, err)
-    qq = q if q.dtype in (torch.float16, torch.bfloat16) else q.to(torch.float16)
+    qq = _as_kernel_q(q, err)
     out = ops.prefill_attention(qq, pool=pool, block_table=bt, int4_max_len=S, sm_scale=sm_scale, err=err,
                                 out_dtype=qq.dtype)
     err.post()

@@ -679,11 +679,16 @@ class HeteroKVManager:
 
     def schedule_prefetch(self, chunk_key: str) -> None:
         """manager.py:335-350: dequantize the chunk to bf16 on the prefetcher's side stream
-        (AsyncPrefetcher) so that a later swap_in finds it ready."""
+        (AsyncPrefetcher) so that a later swap_in finds it ready.  The prefetcher holds at
+        most AsyncPrefetcher._SLOTS chunks not yet fetched; a key scheduled while it is full
+        is skipped (its swap_in dequantizes it then), where the reference's buffer grows
+        without bound."""
         if not self.enable_prefetch or chunk_key not in self._chunks:
             return
         if self._async_pf is None:
             self._async_pf = AsyncPrefetcher(self.device)
+        if chunk_key not in self._async_pf.buffer and self._async_pf.free_slots == 0:
+            return
         self._async_pf.submit_prefetch_task(chunk_key, self.chunk_codes(chunk_key), self._compressor)
 
     def swap_in(self, layer_idx: int, chunk_key: str) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:

@@ -205,8 +205,16 @@ class DRAMStorageManager:
     def num_entries(self) -> int:
         return len(self._table)
 
+    @property
     def keys(self) -> List[str]:
+        """Chunk keys in insertion order (a property, as dram_storage.py:211-213)."""
         return list(self._table.keys())
+
+    def memory_summary(self) -> Dict[str, Any]:
+        """Entry count and stored bytes (dram_storage.py:217-222); the bytes are the
+        entries' tensor bytes, not the 16-byte-rounded pinned slabs holding them."""
+        return {"num_entries": len(self._table), "total_bytes": self._total_bytes,
+                "total_mb": self._total_bytes / (1024 * 1024)}
 
     def clear(self) -> None:
         self._table.clear()
@@ -227,6 +235,11 @@ class AsyncPrefetcher:
         self.buffer: Dict[str, Tuple[torch.Tensor, torch.Tensor]] = {}
         self._slot_of: Dict[str, int] = {}
         self._free_slots = list(range(self._SLOTS))
+
+    @property
+    def free_slots(self) -> int:
+        """Chunks that can still be submitted before one is fetched or cleared."""
+        return len(self._free_slots)
 
     def submit_prefetch_task(self, chunk_key: str, dram_data: Dict[str, Any], compressor) -> None:
         """prefetcher.py:47-98.  Entries held in host memory are copied on the side stream

@@ -363,6 +363,35 @@ def test_exact_lengths_and_generate():
         assert ca.get_seq_length() == cb.get_seq_length() == 306
 
 
+def test_chunked_prefill_schedules_prefetch():
+    """ChunkedPrefillEngine schedules a prefetch of every DRAM chunk after each chunk, as
+    the reference does (engine_wrapper.py:484-486): the side stream holds every stored
+    chunk dequantized afterwards, a swap_in returns the same bf16 K/V as a direct
+    dequantization, and decode logits do not change."""
+    print("case: ChunkedPrefillEngine per-chunk prefetch", flush=True)
+    from heterokv.engine_wrapper import ChunkedPrefillEngine, FusedHeteroCache
+    model = _tiny_qwen2()
+    ids = torch.randint(0, 512, (1, 300), generator=torch.Generator().manual_seed(8)).to(DEV)
+    kw = dict(num_layers=2, sink_tokens=16, keep_tail=80, chunk_size=64, device=DEV)
+    ca, cb = FusedHeteroCache(**kw), FusedHeteroCache(**kw)
+    with torch.inference_mode():
+        ChunkedPrefillEngine(model, ca, chunk_size=64).prefill(ids)
+        ChunkedPrefillEngine(model, cb, chunk_size=64, prefetch_after_chunk=False).prefill(ids)
+        torch.cuda.synchronize()
+        keys = list(ca.dram_table.keys())
+        assert len(keys) >= 4 and keys == list(cb.dram_table.keys())
+        pa = ca._manager._async_pf
+        assert pa is not None and sorted(pa.buffer) == sorted(keys)
+        assert cb._manager._async_pf is None or not cb._manager._async_pf.buffer
+        p = torch.tensor([[300]], device=DEV)
+        la = model(input_ids=ids[:, -1:], position_ids=p, past_key_values=ca, use_cache=True).logits
+        lb = model(input_ids=ids[:, -1:], position_ids=p, past_key_values=cb, use_cache=True).logits
+        assert torch.equal(la, lb)
+        ka, va = ca.swap_in_chunk(keys[0])
+        kb, vb = cb.swap_in_chunk(keys[0])
+        assert ka.dtype == torch.bfloat16 and torch.equal(ka, kb) and torch.equal(va, vb)
+
+
 def test_mask_sizes_match_materialized_keys():
     """get_mask_sizes, asked before each update as transformers does, equals the key length
     the materialized route returns, through prefill, the tail filling, heavy-hitter growth."""

@@ -249,6 +249,36 @@ def test_reference_api_fused_dequant_attn_decode():
     assert err <= TOL
 
 
+def test_reference_api_fp32_q():
+    """An fp32 q is rounded to fp16 for the kernel; in range it attends as its fp16
+    rounding does, and a finite value beyond the fp16 range is reported (HKV_ERR_BIT_RANGE
+    through the API's error word at the next call's check) instead of becoming inf
+    silently."""
+    print("case: fused_dequant_attn_decode with an fp32 q", flush=True)
+    from heterokv import HeteroKVError, fused_dequant_attn_decode
+    from heterokv import fused_dequant_attn as fda
+    g = torch.Generator().manual_seed(14)
+    H, S = 8, 300
+    q = torch.randn((1, H, 1, 128), generator=g)
+    K = torch.randn((1, H, S, 128), generator=g).half()
+    V = torch.randn((1, H, S, 128), generator=g).half()
+    kc, ks, kz = oc.compress(K.numpy(), 128)
+    vc, vs, vz = oc.compress(V.numpy(), 128)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    args = (t(kc), t(ks).reshape(1, H, S), t(kz).reshape(1, H, S), t(vc), t(vs).reshape(1, H, S),
+            t(vz).reshape(1, H, S))
+    out32 = fused_dequant_attn_decode(q.to(DEV), *args)
+    out16 = fused_dequant_attn_decode(q.half().to(DEV), *args)
+    assert out32.dtype == torch.float32
+    assert (out32 - out16.float()).abs().max().item() <= 1e-3   # on-demand schedule: last-bit differences
+    fda._errword(torch.device(DEV)).check()
+    big = q.clone()
+    big[0, 3, 0, 5] = 1e6
+    fused_dequant_attn_decode(big.to(DEV), *args)
+    with pytest.raises(HeteroKVError, match="fp16 range"):
+        fda._errword(torch.device(DEV)).check()
+
+
 def test_bad_block_id_sets_flag():
     print("case: decode with an out-of-range block id", flush=True)
     from heterokv import ops

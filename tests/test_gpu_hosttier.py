@@ -266,6 +266,9 @@ def test_dram_storage_manager_and_async_prefetcher():
     assert store.store("l0_e1", qk, sk, zk, qv, sv, zv)
     assert not store.store_entry("l0_e2", entry)          # entry cap
     assert store.num_entries == 2 and store.total_bytes == 2 * nbytes
+    assert store.keys == ["l0_e0", "l0_e1"]                 # a property, as the reference's
+    assert store.memory_summary() == {"num_entries": 2, "total_bytes": 2 * nbytes,
+                                      "total_mb": 2 * nbytes / (1024 * 1024)}
     got = store.retrieve("l0_e0")
     assert all(t.device.type == "cpu" and t.is_pinned() for t in got.values())
     for name in entry:

@@ -73,6 +73,60 @@ def test_manager_index_parity(sink, budget, chunks, steps):
     assert s["max_hbm_tokens"] == orc.max_hbm_tokens()
 
 
+def _oracle_attention(K, V, q, b, H, positions, dram):
+    parts_k = [K[b].index_select(1, torch.tensor(positions)).double().numpy()]
+    parts_v = [V[b].index_select(1, torch.tensor(positions)).double().numpy()]
+    if dram:
+        idx = torch.tensor(dram)
+        kc, ks, kz = oc.compress(K[b].index_select(1, idx).numpy(), 128)
+        vc, vs, vz = oc.compress(V[b].index_select(1, idx).numpy(), 128)
+        parts_k.insert(0, oa.dequant_rows(kc, ks.reshape(H, -1), kz.reshape(H, -1)))
+        parts_v.insert(0, oa.dequant_rows(vc, vs.reshape(H, -1), vz.reshape(H, -1)))
+    return oa.attend(q[b].double().numpy(), np.concatenate(parts_k, 1), np.concatenate(parts_v, 1))
+
+
+@pytest.mark.parametrize("hh_budget", [8, 24])
+def test_heavy_hitter_zone_fills_then_drops_vs_oracle(hh_budget):
+    """A small heavy-hitter budget in both the manager and the oracle (manager.py:686-750,
+    attention_competition_queue.py:73-107): decode runs past the recent window filling,
+    the heavy-hitter zone filling and the drops after it; at every step the zone contents
+    match the oracle's key cache, and fused decode attention over them (and the INT4 tier)
+    matches the float64 oracle."""
+    print("case: heavy-hitter zone fill then drop, budget %d" % hh_budget, flush=True)
+    from heterokv.manager import HeteroKVManager
+    L, B, H, HQ = 2, 1, 2, 8
+    sink, budget, chunks, steps = 16, 80, [64, 64, 64], 3 * hh_budget + 20
+    K, V = _kv(40 + hh_budget, B, H, sum(chunks) + steps)
+    mgr = HeteroKVManager(L, sink_tokens=sink, hbm_budget_tokens=budget, device=DEV)
+    orc = ManagerOracle(L, sink_tokens=sink, hbm_budget_tokens=budget)
+    mgr._heavyhitter_budget = hh_budget     # before any layer's zones are allocated
+    orc.hh_budget = hh_budget
+    g = torch.Generator().manual_seed(41)
+    pos, checked = 0, 0
+    for n in chunks + [1] * steps:
+        mode = "prefill" if n > 1 else "decode"
+        for layer in range(L):
+            k, v = K[:, :, pos:pos + n].to(DEV), V[:, :, pos:pos + n].to(DEV)
+            mgr.update(layer, k, v, mode=mode, seq_offset=pos)
+            orc.update(layer, range(pos, pos + n), mode, seq_offset=pos)
+            assert mgr.positions(layer) == orc.key_cache[layer], (layer, pos)
+            if mode == "decode" and layer == 1 and pos % 5 == 0:
+                q = (torch.randn((B, HQ, 1, 128), generator=g) / math.sqrt(128)).half()
+                for include_dram in (False, True):
+                    out = mgr.attend_decode(layer, q.to(DEV), include_dram=include_dram).float().cpu().numpy()
+                    dram = orc.dram_positions(layer) if include_dram else []
+                    ref = _oracle_attention(K, V, q, 0, H, orc.key_cache[layer], dram)
+                    assert np.abs(out[0] - ref).max() <= 2e-3, (pos, include_dram)
+                checked += 1
+        pos += n
+    for layer in range(L):
+        st = mgr._layers[layer]
+        assert st.hh_len == hh_budget                       # filled, then frozen
+        assert len(orc.hh[layer]) == hh_budget
+    assert checked >= 5
+    mgr.check_errors()
+
+
 def test_manager_decompress_dram_chunks_matches_path_c():
     print("case: decompress_dram_chunks", flush=True)
     from heterokv.manager import HeteroKVManager

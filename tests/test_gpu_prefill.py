@@ -35,14 +35,21 @@ def _poison_tails(pool, bt, mids, Hkv):
     pool.data.copy_(torch.from_numpy(data))
 
 
-def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0, poison=False, io_dtype=torch.float16):
+def _ulp16(x):
+    """fp16 unit in the last place at |x| (subnormal spacing below 2^-14)."""
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -24)))
+    return 2.0 ** np.maximum(e - 10, -24)
+
+
+def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0, poison=False, io_dtype=torch.float16,
+          k_scale=1.0, v_scale=1.0):
     from heterokv import ops
     g = torch.Generator().manual_seed(seed)
     hist = sink + max(mids) + max(recents)
     K = torch.randn((B, Hkv, hist, 128), generator=g)
     K[..., [7, 31, 64, 100]] *= 8
-    K = K.half()
-    V = torch.randn((B, Hkv, hist, 128), generator=g).half()
+    K = (K * k_scale).half()
+    V = (torch.randn((B, Hkv, hist, 128), generator=g) * v_scale).half()
     # q, the chunk and the output in io_dtype (bf16 q/chunk values are exact in fp16 here)
     CK = torch.randn((B, Hkv, Sq, 128), generator=g).to(io_dtype)
     CV = torch.randn((B, Hkv, Sq, 128), generator=g).to(io_dtype)
@@ -101,8 +108,11 @@ def _case(seed, B, Hq, Hkv, Sq, sink, mids, recents, causal=True, q_scale=1.0, p
             vs.append(CV[b].double().numpy())
             mask = np.concatenate([mask, np.tril(np.ones((Sq, Sq), dtype=bool))], axis=1)
         ref = oa.attend(q[b].double().numpy(), np.concatenate(ks, 1), np.concatenate(vs, 1), mask=mask)
-        # a bf16 output adds its own rounding: half an ulp, 2^-9 of the value
-        tol = TOL + (np.abs(ref) * 2.0 ** -9 if io_dtype == torch.bfloat16 else 0.0)
+        # a bf16 output adds its own rounding: half an ulp, 2^-9 of the value; with V scaled
+        # by v_scale the bar scales with it, plus half an fp16 ulp of the output
+        tol = TOL * v_scale + (np.abs(ref) * 2.0 ** -9 if io_dtype == torch.bfloat16 else 0.0)
+        if v_scale != 1.0:
+            tol = tol + 0.5 * _ulp16(ref)
         err = np.abs(got[b] - ref)
         print("  b=%d max abs err %.3e" % (b, err.max()), flush=True)
         assert np.all(np.isfinite(got[b]))
@@ -144,6 +154,24 @@ def test_bf16_query_chunk_and_output():
     print("case: prefill with bf16 q, chunk and output, 16/4 Sq=100, sink 64 + INT4 300 + recent 50", flush=True)
     _case(11, 1, 16, 4, 100, 64, [300], [50], io_dtype=torch.bfloat16)
     _case(12, 2, 8, 8, 37, 0, [0, 70], [20, 0], io_dtype=torch.bfloat16)
+
+
+def test_small_magnitude_keys():
+    """K rows scaled by 3e-5, so nearly all INT4 K scales lie below fp16's normal range
+    (2^-14), with q scaled so that the scores vary by a few log2 units.  The staging rounds
+    each scale to fp16 (a subnormal here) and then the product; with the softmax scale on
+    the queries, not folded into the keys, a CPU emulation of this case stays at 1.0e-4 of
+    the float64 oracle (6.3e-4 with the scale folded into the keys, 7.5e-5 with every
+    product rounded once from fp32)."""
+    print("case: prefill with K scales below 2^-14 (K x 3e-5, q x 1e5), 8/2 Sq=48, 16 + 700 INT4 + 40", flush=True)
+    _case(13, 1, 8, 2, 48, 16, [700], [40], causal=False, k_scale=3e-5, q_scale=1e5)
+
+
+def test_small_magnitude_values():
+    """V rows scaled by 3e-5 (V scales ~1e-5, below 2^-14): the output matches the oracle to
+    2e-3 of the V scale plus half an fp16 ulp of the output."""
+    print("case: prefill with V scales below 2^-14 (V x 3e-5), 8/2 Sq=48, 16 + 700 INT4 + 40", flush=True)
+    _case(14, 1, 8, 2, 48, 16, [700], [40], causal=False, v_scale=3e-5)
 
 
 def test_medium_c4_like():
