@@ -21,6 +21,8 @@ namespace {
 
 // Halves offset of V[token s][dim d] inside a 16-token transposed tile:
 // [g = s/4][c = d%16][n = d/16][i = s%4].
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ int vtile_off(int s, int d) {
     return (((s >> 2) * 16 + (d & 15)) * 8 + (d >> 4)) * 4 + (s & 3);
 }
@@ -60,7 +62,6 @@ __device__ __forceinline__ void report_range(bool over, int* err) {
 // multiple of 16), the tile is transposed through LDS and written with one 16-byte
 // store per lane; otherwise each lane writes its 8 V values into their tile slots.
 __global__ __launch_bounds__(256) void zone_write_kernel(ZoneWriteParams p) {
-    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
     __shared__ __align__(16) uint16_t sv[kBlockTokens][kHeadDim + 8];   // +8 halves: rows start on different banks
     const int j = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int t = threadIdx.x, r = t >> 4, q = t & 15;
@@ -123,31 +124,55 @@ __global__ __launch_bounds__(256) void zone_write_kernel(ZoneWriteParams p) {
     }
 }
 
-__global__ __launch_bounds__(128) void zone_copy_kernel(const uint16_t* __restrict__ sk,
+// Copies and reads work on 16-slot tiles: one 256-thread workgroup per tile of the slot
+// range, thread (r, q) = (t / 16, t % 16) owns slot r of the tile and dims 8q .. 8q+7.
+// K rows move as 16-byte pieces.  V tiles are stored transposed (vtile_off), so a V
+// read stages the whole 4 KB tile in LDS with 16-byte loads and writes row-major
+// 16-byte pieces; a copy between tile-aligned ranges moves whole tiles as 16-byte
+// pieces, any other copy moves V element by element.
+__global__ __launch_bounds__(256) void zone_copy_kernel(const uint16_t* __restrict__ sk,
                                                         const uint16_t* __restrict__ sv, int scap, int s0,
                                                         uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
-                                                        int dcap, int d0, int H) {
-    const int i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int d = threadIdx.x;
+                                                        int dcap, int d0, int n, int H) {
+    const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int t = threadIdx.x, r = t >> 4, q = t & 15;
     const int64_t bh = (int64_t)b * H + h;
-    const int ss = s0 + i, ds = d0 + i;
-    dk[(bh * dcap + ds) * kHeadDim + d] = sk[(bh * scap + ss) * kHeadDim + d];
-    dv[(bh * (dcap / kBlockTokens) + ds / kBlockTokens) * (kBlockTokens * kHeadDim) + vtile_off(ds & 15, d)] =
-        sv[(bh * (scap / kBlockTokens) + ss / kBlockTokens) * (kBlockTokens * kHeadDim) + vtile_off(ss & 15, d)];
+    const int i = tile * kBlockTokens + r;   // slot of the copy range
+    if (i < n)
+        *(u4v*)(dk + (bh * dcap + d0 + i) * kHeadDim + 8 * q) = *(const u4v*)(sk + (bh * scap + s0 + i) * kHeadDim + 8 * q);
+    if (s0 % kBlockTokens == 0 && d0 % kBlockTokens == 0 && tile * kBlockTokens + kBlockTokens <= n) {
+        const int64_t st = bh * (scap / kBlockTokens) + (s0 / kBlockTokens + tile);
+        const int64_t dt = bh * (dcap / kBlockTokens) + (d0 / kBlockTokens + tile);
+        *(u4v*)(dv + dt * (kBlockTokens * kHeadDim) + 8 * t) = *(const u4v*)(sv + st * (kBlockTokens * kHeadDim) + 8 * t);
+    } else if (i < n) {
+        const int ss = s0 + i, ds = d0 + i;
+        const uint16_t* src = sv + (bh * (scap / kBlockTokens) + ss / kBlockTokens) * (kBlockTokens * kHeadDim);
+        uint16_t* dst = dv + (bh * (dcap / kBlockTokens) + ds / kBlockTokens) * (kBlockTokens * kHeadDim);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[vtile_off(ds & 15, 8 * q + e)] = src[vtile_off(ss & 15, 8 * q + e)];
+    }
 }
 
-__global__ __launch_bounds__(128) void zone_read_kernel(const uint16_t* __restrict__ zk,
+__global__ __launch_bounds__(256) void zone_read_kernel(const uint16_t* __restrict__ zk,
                                                         const uint16_t* __restrict__ zv, int H,
                                                         int cap, int n, uint16_t* __restrict__ ok,
                                                         uint16_t* __restrict__ ov) {
-    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int d = threadIdx.x;
+    const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int t = threadIdx.x, r = t >> 4, q = t & 15;
     const int64_t bh = (int64_t)b * H + h;
-    const int64_t dst = (bh * n + s) * kHeadDim + d;
-    if (ok) ok[dst] = zk[(bh * cap + s) * kHeadDim + d];
+    const int s = tile * kBlockTokens + r;
+    if (ok && s < n) *(u4v*)(ok + (bh * n + s) * kHeadDim + 8 * q) = *(const u4v*)(zk + (bh * cap + s) * kHeadDim + 8 * q);
     if (ov) {
-        const int64_t tile = bh * (cap / kBlockTokens) + s / kBlockTokens;
-        ov[dst] = zv[tile * (kBlockTokens * kHeadDim) + vtile_off(s & 15, d)];
+        __shared__ __align__(16) uint16_t sv[kBlockTokens * kHeadDim];
+        *(u4v*)&sv[8 * t] = *(const u4v*)(zv + (bh * (cap / kBlockTokens) + tile) * (kBlockTokens * kHeadDim) + 8 * t);
+        __syncthreads();
+        if (s < n) {
+            u4v w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = (uint32_t)sv[vtile_off(r, 8 * q + 2 * e)] | ((uint32_t)sv[vtile_off(r, 8 * q + 2 * e + 1)] << 16);
+            *(u4v*)(ov + (bh * n + s) * kHeadDim + 8 * q) = w;
+        }
     }
 }
 
@@ -338,8 +363,10 @@ extern "C" int hkv_zone_read(const uint16_t* zone_k, const uint16_t* zone_v, int
                 "hkv_zone_read: bad sizes");
     if (n == 0 || batch == 0) return HKV_OK;
     HKV_REQUIRE(zone_k && zone_v && (out_k || out_v), HKV_ERR_ARG, "hkv_zone_read: null pointer");
-    hipLaunchKernelGGL(zone_read_kernel, dim3(n, num_kv_heads, batch), dim3(128), 0, (hipStream_t)stream,
-                       zone_k, zone_v, num_kv_heads, capacity, n, out_k, out_v);
+    HKV_REQUIRE((((uintptr_t)zone_k | (uintptr_t)zone_v | (uintptr_t)out_k | (uintptr_t)out_v) & 15) == 0, HKV_ERR_ARG,
+                "hkv_zone_read: zone and output pointers must be 16-byte aligned");
+    hipLaunchKernelGGL(zone_read_kernel, dim3((n + kBlockTokens - 1) / kBlockTokens, num_kv_heads, batch), dim3(256), 0,
+                       (hipStream_t)stream, zone_k, zone_v, num_kv_heads, capacity, n, out_k, out_v);
     HKV_LAUNCH_CHECK("zone_read_kernel");
     return HKV_OK;
 }
@@ -360,8 +387,11 @@ extern "C" int hkv_zone_copy(const uint16_t* src_k, const uint16_t* src_v, int32
                 HKV_ERR_CAPACITY, "hkv_zone_copy: slot range outside a zone");
     if (n == 0 || batch == 0) return HKV_OK;
     HKV_REQUIRE(src_k && src_v && dst_k && dst_v, HKV_ERR_ARG, "hkv_zone_copy: null pointer");
-    hipLaunchKernelGGL(zone_copy_kernel, dim3(n, num_kv_heads, batch), dim3(128), 0, (hipStream_t)stream, src_k,
-                       src_v, src_capacity, src_slot, dst_k, dst_v, dst_capacity, dst_slot, num_kv_heads);
+    HKV_REQUIRE((((uintptr_t)src_k | (uintptr_t)src_v | (uintptr_t)dst_k | (uintptr_t)dst_v) & 15) == 0, HKV_ERR_ARG,
+                "hkv_zone_copy: zone pointers must be 16-byte aligned");
+    hipLaunchKernelGGL(zone_copy_kernel, dim3((n + kBlockTokens - 1) / kBlockTokens, num_kv_heads, batch), dim3(256), 0,
+                       (hipStream_t)stream, src_k, src_v, src_capacity, src_slot, dst_k, dst_v, dst_capacity, dst_slot,
+                       n, num_kv_heads);
     HKV_LAUNCH_CHECK("zone_copy_kernel");
     return HKV_OK;
 }

@@ -111,6 +111,31 @@ def test_zone_write_layouts(T, start, ring):
         err.check()
 
 
+@pytest.mark.parametrize("src,dst,n", [(0, 16, 32), (16, 0, 16), (3, 40, 21), (20, 7, 1), (0, 0, 48), (32, 64, 17)])
+def test_zone_copy_and_read(src, dst, n):
+    """hkv_zone_copy (whole-tile 16-byte path for tile-aligned ranges, per-element V moves
+    otherwise) and hkv_zone_read of every length (partial last tile) against the slots
+    written through hkv_zone_write; the copy leaves every other destination slot alone."""
+    print("case: zone copy %d -> %d x %d, reads" % (src, dst, n), flush=True)
+    from heterokv import ops
+    B, H, cap = 2, 3, 96
+    k, v = _kv(7 + src + n, B, H, cap)
+    k2, v2 = _kv(8 + dst + n, B, H, cap)
+    a = ops.F16Zone(B, H, cap, DEV)
+    c = ops.F16Zone(B, H, cap, DEV)
+    a.write(k.to(DEV), v.to(DEV), 0)
+    c.write(k2.to(DEV), v2.to(DEV), 0)
+    for m in (1, 15, 16, 17, 95, 96):
+        rk, rv = a.read(m)
+        assert torch.equal(rk.cpu(), k[:, :, :m]) and torch.equal(rv.cpu(), v[:, :, :m]), m
+    a.copy_to(c, src, dst, n)
+    rk, rv = c.read(cap)
+    want_k, want_v = k2.clone(), v2.clone()
+    want_k[:, :, dst:dst + n] = k[:, :, src:src + n]
+    want_v[:, :, dst:dst + n] = v[:, :, src:src + n]
+    assert torch.equal(rk.cpu(), want_k) and torch.equal(rv.cpu(), want_v)
+
+
 def test_zone_write_bf16_conversion_is_exact():
     """bf16 -> fp16 narrowing in the zone kernels equals numpy's round-to-nearest-even
     conversion for every bf16 pattern of magnitude below the fp16 range."""
