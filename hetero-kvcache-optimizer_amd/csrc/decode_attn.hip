@@ -30,7 +30,7 @@
 // workgroup 0 rotates from launch to launch, so only the id modulo the XCD count
 // is fixed).  When every range of a pair shares an XCD (pairs a multiple of the
 // XCD count), the hand-off stays in that XCD's L2: plain stores, an L2 atomic
-// ticket and L1-bypassing loads.  Otherwise (or with HKV_DECODE_AGENT_HANDOFF) it
+// ticket and group-scope loads.  Otherwise (or with HKV_DECODE_AGENT_HANDOFF) it
 // goes through memory with agent-scope (sc1) accesses.  The placement is checked
 // on every launch: each workgroup ORs its XCD bit into a device-scope mask of its
 // pair when its streaming ends and reads the old mask back at its ticket; a foreign
@@ -172,7 +172,10 @@ __device__ __forceinline__ float ld_agent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// L1-bypassing (sc0) loads through a buffer resource: coherent at the XCD's L2.
+// Group-scope (sc0) loads through a buffer resource.  They can be served from this
+// CU's L1, which every kernel starts with empty; the merging workgroup reads the pair's
+// partial states only after its ticket shows them all final and has read none of their
+// lines before, so every line it loads comes from the XCD's L2 in its final state.
 __device__ __forceinline__ float ld_l2(__amdgpu_buffer_rsrc_t r, int byte_off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 1));
 }
@@ -528,7 +531,7 @@ __device__ __forceinline__ int part_point(int n, int i, int d) {
 // Partial states s0 + j K (j < 8) of head hd for the final merge: m, l and
 // float4 d4 of o.  Splits past the end read the last split again and get
 // m = -inf, so that every load is issued unconditionally.  kL2: XCD-local
-// hand-off (L1-bypassing buffer loads), else agent-scope loads.
+// hand-off (group-scope buffer loads), else agent-scope loads.
 template <bool kL2>
 __device__ __forceinline__ void load_partials(__amdgpu_buffer_rsrc_t prs, const float* parts, int s0, int K,
                                               int nsplit, int nrep, int hd, int d4, float* ms, float* ls, f4* os) {
