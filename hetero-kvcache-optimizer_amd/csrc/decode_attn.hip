@@ -63,10 +63,12 @@ static_assert((kHeadDim * 4) % 8 == 0 && (kPartStride * 4) % 16 == 0, "m, l load
 #define HKV_DECODE_PREFETCH 2
 #endif
 constexpr int kPrefetch = HKV_DECODE_PREFETCH;  // INT4 block pairs in flight per wave
+// fp16 zone tiles in flight per wave: one (an 8 KB tile per wave is already as much in
+// flight as two INT4 block pairs; two tiles measured ~1% slower on the 32K decode)
 #ifndef HKV_DECODE_F16_DEPTH
-#define HKV_DECODE_F16_DEPTH 2
+#define HKV_DECODE_F16_DEPTH 1
 #endif
-constexpr int kF16Depth = HKV_DECODE_F16_DEPTH;  // fp16 zone tiles in flight per wave
+constexpr int kF16Depth = HKV_DECODE_F16_DEPTH;
 constexpr int kMaxSplits = 64;
 // INT4 tokens, and fp16 tokens over all zones, per sequence: 2^22 items of 16 tokens
 // keep the range arithmetic in 32 bits.
@@ -107,10 +109,14 @@ constexpr int kTlWords = 16;
 // Bytes one kv head reads per item (the weights that balance the ranges).
 constexpr int64_t kInt4ItemBytes = kBlockTokens * (kHeadDim / 2 + 5) * 2;   // 2208
 constexpr int64_t kF16ItemBytes = kBlockTokens * kHeadDim * 2 * 2;           // 8192
+// Balance weight of an INT4 block against an fp16 tile (8192): its 2208 bytes plus the
+// block-id indirection (INT4-only ranges start streaming only when their first ids are in
+// LDS, ~2.5 us into the 32K decode) and the nibble decode; fitted on the 32K decode,
+// where 3300 gives 24 INT4-only and 8 fp16-only ranges per (sequence, kv head).
 #ifndef HKV_INT4_COST
-#define HKV_INT4_COST 2560
+#define HKV_INT4_COST 3300
 #endif
-constexpr int64_t kInt4Cost = HKV_INT4_COST;   // balance weight of an INT4 block against an fp16 tile
+constexpr int64_t kInt4Cost = HKV_INT4_COST;
 
 struct ZoneP {
     const uint16_t* k;
