@@ -561,6 +561,7 @@ __device__ __forceinline__ void load_partials(__amdgpu_buffer_rsrc_t prs, const 
 
 template <bool kDynamic, bool kScores>
 __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
+    touch_kernel_args(p);   // the range plan below reads the arguments in a dependent chain
     const int BH = p.B * p.Hkv;
     const int bh = blockIdx.x % BH;
     const int split = blockIdx.x / BH;
@@ -578,14 +579,15 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     TL_MARK(0);
 #endif
 
-    const int len4 = p.int4_lens ? min(max(p.int4_lens[b], 0), p.int4_max_len) : p.int4_max_len;
+    // per-sequence lengths: wave-uniform scalar loads (the kernel does not write them)
+    const int len4 = p.int4_lens ? min(max(load_uniform_i32(p.int4_lens, b), 0), p.int4_max_len) : p.int4_max_len;
     int lenz[HKV_MAX_F16_ZONES];
     ZoneTiles zt;
 #pragma unroll
     for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
         lenz[zi] = 0;
         if (zi < p.nz)
-            lenz[zi] = p.z[zi].lens ? min(max(p.z[zi].lens[b], 0), p.z[zi].max_len) : p.z[zi].max_len;
+            lenz[zi] = p.z[zi].lens ? min(max(load_uniform_i32(p.z[zi].lens, b), 0), p.z[zi].max_len) : p.z[zi].max_len;
         zt.nt[zi] = (lenz[zi] + kBlockTokens - 1) / kBlockTokens;
     }
     // Range `split` of this (sequence, kv head): INT4 blocks [a0, a1) and fp16

@@ -80,6 +80,36 @@ struct RecordLayout {
     __host__ __device__ static int64_t vz(int h) { return part(h) + kPartVz; }
 };
 
+// ---------------------------------------------------------------- kernel arguments
+// A kernel's argument block is read with scalar loads, and a prologue whose loads depend
+// on each other (a pointer tested, then a field on another 64-byte line read) misses
+// the scalar cache one line at a time, a memory round trip each.  Touching every line of
+// the block once, all loads issued together, at kernel entry makes the later argument
+// loads hit the scalar cache: one round trip instead of a chain of them.
+template <class P>
+__device__ __forceinline__ void touch_kernel_args(const P& p) {
+    constexpr int kWords = (int)(sizeof(P) / 4), kLines = (kWords + 15) / 16;
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(&p);
+    uint32_t v[kLines];
+#pragma unroll
+    for (int i = 0; i < kLines; ++i) v[i] = w[16 * i < kWords ? 16 * i : kWords - 1];
+    static_assert(kLines <= 8, "argument block of at most 8 lines");
+    // one statement, so that every load is issued before the single wait
+    asm volatile("" ::"s"(v[0]), "s"(v[1 < kLines ? 1 : 0]), "s"(v[2 < kLines ? 2 : 0]), "s"(v[3 < kLines ? 3 : 0]),
+                 "s"(v[4 < kLines ? 4 : 0]), "s"(v[5 < kLines ? 5 : 0]), "s"(v[6 < kLines ? 6 : 0]),
+                 "s"(v[7 < kLines ? 7 : 0]));
+    __builtin_amdgcn_sched_barrier(0);   // nothing that reads an argument moves above the wait
+}
+
+// A wave-uniform read of a word the kernel does not write, through the scalar cache
+// (a constant-address-space load): it completes on the scalar counter, so it does not
+// queue behind the wave's vector loads, and no vector-to-scalar move waits for it.
+// The scalar cache starts every kernel empty.
+__device__ __forceinline__ int32_t load_uniform_i32(const int32_t* base, int64_t i) {
+    typedef const __attribute__((address_space(4))) int32_t* const_i32_p;
+    return *((const_i32_p)base + i);
+}
+
 // ---------------------------------------------------------------- numeric helpers
 __device__ __forceinline__ float h2f(uint16_t b) {
     return __half2float(__ushort_as_half(b));

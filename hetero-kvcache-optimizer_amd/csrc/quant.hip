@@ -93,31 +93,34 @@ struct PackParams {
     int vec_ok;  // 16-byte aligned rows: use 128-bit loads
 };
 
-// Values p[0..7] and p[64..71] of a token row (vals[0..7], vals[8..15]).  The 8 lanes
-// of a row read dims 8 part .. +7 and 64 + 8 part .. +7, so each of the two 16-byte
-// loads of a wave fills whole 128-byte lines (the first or second half of 8 rows):
-// 8.17-8.24 vs 8.37-8.41 us on the 8x4096-token K+V pack.  The rows are read once:
-// non-temporal loads (8.8 vs 9.0 us).
-__device__ __forceinline__ void load_row_halves(const void* src, int dtype, int64_t off, int vec_ok,
-                                                float (&vals)[16]) {
+// Values p[0..7] and p[64..71] of a token row, as 16-bit words (w[i] = values 2i, 2i + 1
+// of the 16).  The 8 lanes of a row read dims 8 part .. +7 and 64 + 8 part .. +7, so each
+// of the two 16-byte loads of a wave fills whole 128-byte lines (the first or second half
+// of 8 rows): 8.17-8.24 vs 8.37-8.41 us on the 8x4096-token K+V pack.  The rows are read
+// once: non-temporal loads (8.8 vs 9.0 us).  The words are converted to float by
+// row_values, apart from the loads, so that other loads can be issued in between.
+__device__ __forceinline__ void load_row_halves(const void* src, int64_t off, int vec_ok, uint32_t (&w)[8]) {
     const uint16_t* p = (const uint16_t*)src + off;
     if (vec_ok) {
         typedef unsigned int nv4 __attribute__((ext_vector_type(4)));
         const nv4 a = __builtin_nontemporal_load((const nv4*)p);
         const nv4 b = __builtin_nontemporal_load((const nv4*)(p + 64));
-        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint16_t lo = (uint16_t)(w[i] & 0xffffu), hi = (uint16_t)(w[i] >> 16);
-            vals[2 * i] = dtype == HKV_DTYPE_F16 ? h2f(lo) : bf2f(lo);
-            vals[2 * i + 1] = dtype == HKV_DTYPE_F16 ? h2f(hi) : bf2f(hi);
-        }
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+        w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
     } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint16_t x = p[i < 8 ? i : 56 + i];
-            vals[i] = dtype == HKV_DTYPE_F16 ? h2f(x) : bf2f(x);
+        for (int i = 0; i < 8; ++i) {
+            const int e = 2 * i < 8 ? 2 * i : 56 + 2 * i;
+            w[i] = (uint32_t)p[e] | ((uint32_t)p[e + 1] << 16);
         }
+    }
+}
+__device__ __forceinline__ void row_values(const uint32_t (&w)[8], int dtype, float (&vals)[16]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint16_t lo = (uint16_t)(w[i] & 0xffffu), hi = (uint16_t)(w[i] >> 16);
+        vals[2 * i] = dtype == HKV_DTYPE_F16 ? h2f(lo) : bf2f(lo);
+        vals[2 * i + 1] = dtype == HKV_DTYPE_F16 ? h2f(hi) : bf2f(hi);
     }
 }
 
@@ -166,39 +169,47 @@ constexpr int kPartVecs = kHeadPartBytes / 16;
 static_assert(kHeadPartBytes % 16 == 0 && kPartVecs <= 256, "one 16-byte store per lane");
 
 __global__ __launch_bounds__(256) void pack_tokens_kernel(PackParams p) {
+    touch_kernel_args(p);
     const int b = blockIdx.z, h = blockIdx.y;
-    const int start = p.start_pos[b];
+    const int start = load_uniform_i32(p.start_pos, b);
     const int lb = start / kBlockTokens + (int)blockIdx.x;
     const int lo = max(start, lb * kBlockTokens) - lb * kBlockTokens;
     const int hi = min(start + p.T, lb * kBlockTokens + kBlockTokens) - lb * kBlockTokens;
     if (lo >= hi) return;
-    if (lb < 0 || lb >= p.bt_stride) {
-        if (threadIdx.x == 0 && p.err) atomicOr(p.err, 2);
-        return;
+
+    __shared__ __align__(16) uint8_t codes[kBlockTokens][kHeadDim];   // V codes, one byte each
+    __shared__ __align__(16) uint8_t part[kHeadPartBytes];            // the record part being built
+
+    // The block-table read and the block's rows (tokens lo..hi-1 of the input, in bounds
+    // whatever the block table holds) are in flight together: the table entry is requested
+    // first, so that its check waits for it alone (read unconditionally, at column 0 when lb
+    // is outside the row: bt_stride > 0 is checked on the host).
+    const bool lb_ok = lb >= 0 && lb < p.bt_stride;
+    const int bt_entry = load_uniform_i32(p.bt, (int64_t)b * p.bt_stride + (lb_ok ? lb : 0));
+    const int phys = lb_ok ? bt_entry : -1;
+    const int t = threadIdx.x;
+    const int row = t >> 3;
+    const int kv = row >> 4, slot = row & 15, pt = t & 7;
+    const bool active = slot >= lo && slot < hi;
+    uint32_t raw[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    if (active) {
+        const int tok = lb * kBlockTokens + slot - start;
+        const int64_t off = (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)tok * p.st + pt * 8;
+        load_row_halves(kv ? p.v : p.k, off, p.vec_ok, raw);
     }
-    const int phys = p.bt[(int64_t)b * p.bt_stride + lb];
-    if (phys < 0 || (int64_t)phys >= p.pool_blocks) {
-        if (threadIdx.x == 0 && p.err) atomicOr(p.err, 1);
+    if (!lb_ok || phys < 0 || (int64_t)phys >= p.pool_blocks) {
+        if (threadIdx.x == 0 && p.err) atomicOr(p.err, lb_ok ? 1 : 2);
         return;
     }
     const RecordLayout L(p.H);
     uint4* gpart = (uint4*)(p.pool + (int64_t)phys * L.bytes + RecordLayout::part(h));
 
-    __shared__ __align__(16) uint8_t codes[kBlockTokens][kHeadDim];   // V codes, one byte each
-    __shared__ __align__(16) uint8_t part[kHeadPartBytes];            // the record part being built
-
-    const int t = threadIdx.x;
     const bool whole = lo == 0 && hi == kBlockTokens;
     if (!whole && t < kPartVecs) ((uint4*)part)[t] = gpart[t];   // visible after the barrier below
-    const int row = t >> 3;
-    const int kv = row >> 4, slot = row & 15, pt = t & 7;
-    const bool active = slot >= lo && slot < hi;
     float vals[16];
+    row_values(raw, p.dtype, vals);
     float mn = INFINITY, mx = -INFINITY;
     if (active) {
-        const int tok = lb * kBlockTokens + slot - start;
-        const int64_t off = (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)tok * p.st + pt * 8;
-        load_row_halves(kv ? p.v : p.k, p.dtype, off, p.vec_ok, vals);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             mn = __builtin_elementwise_minimum(mn, vals[i]);
