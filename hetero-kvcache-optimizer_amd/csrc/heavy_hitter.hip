@@ -33,6 +33,7 @@ struct WeightsParams {
 constexpr int kMaxWeightHeads = 256;
 
 __global__ __launch_bounds__(256) void attn_weights_kernel(WeightsParams p) {
+    touch_kernel_args(p);
     // each row's max and 1 / sum, once per workgroup
     __shared__ float sm_m[kMaxWeightHeads], sm_inv[kMaxWeightHeads];
     const int b = blockIdx.y;

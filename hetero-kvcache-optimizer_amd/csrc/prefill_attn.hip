@@ -186,6 +186,7 @@ struct Int4Stage {
 // One workgroup per CU: 8 waves (two per SIMD), up to 256 registers per wave, over one
 // kv head and 64 query rows; waves 0-3 stage K, waves 4-7 stage V^T.
 __global__ __launch_bounds__(kFlatThreads, 1) void prefill_attn_kernel(PrefillParams p) {
+    touch_kernel_args(p);
     extern __shared__ __align__(16) uint8_t lds_raw[];
     const int b = blockIdx.z;
     const FlatBlock blk = flat_block();

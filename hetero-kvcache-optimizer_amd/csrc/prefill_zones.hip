@@ -147,6 +147,7 @@ struct F16Stage {
 
 // One workgroup per CU: 8 waves (two per SIMD) over one kv head and 64 query rows.
 __global__ __launch_bounds__(kFlatThreads, 1) void prefill_zones_kernel(PrefillParams p) {
+    touch_kernel_args(p);
     extern __shared__ __align__(16) uint8_t lds_raw[];
     const int b = blockIdx.z;
     const FlatBlock blk = flat_block();

@@ -307,6 +307,7 @@ struct RepackParams {
 };
 
 __global__ __launch_bounds__(256) void repack_codes_kernel(RepackParams p) {
+    touch_kernel_args(p);
     const int b = blockIdx.z, h = blockIdx.y;
     const int start = p.start_pos[b];
     const int lb = start / kBlockTokens + (int)blockIdx.x;

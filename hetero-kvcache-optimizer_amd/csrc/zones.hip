@@ -62,6 +62,7 @@ __device__ __forceinline__ void report_range(bool over, int* err) {
 // multiple of 16), the tile is transposed through LDS and written with one 16-byte
 // store per lane; otherwise each lane writes its 8 V values into their tile slots.
 __global__ __launch_bounds__(256) void zone_write_kernel(ZoneWriteParams p) {
+    touch_kernel_args(p);
     __shared__ __align__(16) uint16_t sv[kBlockTokens][kHeadDim + 8];   // +8 halves: rows start on different banks
     const int j = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int t = threadIdx.x, r = t >> 4, q = t & 15;
@@ -210,6 +211,7 @@ __device__ inline bool state_ok(const ZoneStepParams& p, int head, int len, int 
 // full its oldest token moves to the heavy-hitter zone (while it has room) before
 // the new token takes its slot.  Every lane reads and writes only its own dim.
 __global__ __launch_bounds__(128) void zone_step_kernel(ZoneStepParams p) {
+    touch_kernel_args(p);
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const int head = p.state[0], len = p.state[1], hh = p.state[2];
     if (!state_ok(p, head, len, hh)) return;   // a state no step produced: write nothing
@@ -230,6 +232,7 @@ __global__ __launch_bounds__(128) void zone_step_kernel(ZoneStepParams p) {
 
 // Advances the state after the step and publishes the zone lengths per sequence.
 __global__ __launch_bounds__(256) void zone_advance_kernel(ZoneStepParams p) {
+    touch_kernel_args(p);
     int head = p.state[0], len = p.state[1], hh = p.state[2], dropped = p.state[3];
     if (!state_ok(p, head, len, hh)) return;
     if (len < p.ring) {
