@@ -70,6 +70,9 @@ constexpr int kPrefetch = HKV_DECODE_PREFETCH;  // INT4 block pairs in flight pe
 #endif
 constexpr int kF16Depth = HKV_DECODE_F16_DEPTH;
 constexpr int kMaxSplits = 64;
+constexpr int kArrivedMask = 0xffff;     // slice merge: arrivals in the low bits of the pair's ticket
+constexpr int kGoneBit = 1 << 30;        // slice merge: a range stopped waiting
+constexpr unsigned long long kMergeWaitTicks = 200000;   // 2 ms of the 100 MHz constant clock
 // INT4 tokens, and fp16 tokens over all zones, per sequence: 2^22 items of 16 tokens
 // keep the range arithmetic in 32 bits.
 constexpr int kMaxZoneTokens = 1 << 26;
@@ -154,6 +157,8 @@ struct DecodeParams {
     int64_t part_pair_stride;  // floats between the partial blocks of consecutive pairs (256-byte multiple)
     int xcc_local;             // 1: all ranges of a pair run on one XCD (see above)
     int nxcc;                  // XCDs the dispatcher round-robins over
+    int coop;                  // 1: slice merge by every range of a pair (see the kernel's tail)
+    unsigned long long merge_wait;   // slice merge: constant-clock ticks a range waits for the others
     // optional score output (kScores): row (b, q head) holds the log2-domain score of
     // every item [INT4 tokens | zone 0 | zone 1 | zone 2]; zone z starts at sc_zone[z]
     float* scores;
@@ -878,6 +883,133 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
+    if (p.coop) {
+        // ---- slice merge (XCD-local hand-off, every range of the pair resident).  Each
+        // range adds itself to the pair's arrival count, waits until the count is complete
+        // (bounded), then merges one slice of the pair's output from all nsplit partial
+        // states, so that the end of the kernel is one small load round trip after the
+        // last arrival instead of one workgroup loading every state.  A range whose wait
+        // runs out sets kGoneBit and leaves; the last arrival, seeing it, merges every
+        // slice (the same code, so a slice written twice gets the same bits).  A second
+        // count (done) tells the last workgroup to leave the pair's words that it may
+        // reset them: every range has made its last access to the arrival count by then.
+        __shared__ int sm_slices;   // 0: none, 1: this range's slice, 2: every slice
+        if (threadIdx.x == 0) {
+            int* const arrived = &p.counters_l2[bh * 64];
+            int* const done = &p.counters_l2[bh * 64 + 1];
+            const int old = __hip_atomic_fetch_add(arrived, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            bool bad = (owner_old & ~owner_bit) != 0u || (old & kArrivedMask) >= nsplit;
+            int slices;
+            if ((old & kArrivedMask) == nsplit - 1) {
+                slices = (old & kGoneBit) ? 2 : 1;
+            } else {
+                slices = 0;
+                const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+                for (;;) {
+                    // an OR of zero, performed at the L2 like the others' arrivals (a load
+                    // could be served from this CU's L1); the zero is opaque so that the
+                    // compiler keeps the atomic
+                    int zero;
+                    asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+                    int v = __hip_atomic_fetch_or(arrived, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    if ((v & kArrivedMask) >= nsplit) {
+                        slices = 1;
+                        break;
+                    }
+                    if (__builtin_amdgcn_s_memrealtime() - t0 > p.merge_wait) {
+                        v = __hip_atomic_fetch_or(arrived, kGoneBit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        slices = (v & kArrivedMask) >= nsplit ? 1 : 0;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            }
+            if (bad && p.err)
+                __hip_atomic_fetch_or(p.err, HKV_ERR_BIT_PLACEMENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // this workgroup's last access to the arrival count is done
+            if (__hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == nsplit - 1) {
+                __hip_atomic_store(arrived, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_store(&p.owners[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            sm_slices = slices;
+        }
+        __syncthreads();
+        TL_MARK(4);
+        const int slices = sm_slices;
+        if (slices == 0) {
+            TL_FLUSH(tl_info);
+            return;
+        }
+        // slice sl = outputs [sl S, sl S + S) of the pair's nout (head-major: head, dim);
+        // 4 threads per output, thread q of an output taking splits q, q + 4, ...
+        const float* parts = p.partials + (int64_t)bh * p.part_pair_stride;
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)parts, 0, (int)(nsplit * nrep * kPartStride * sizeof(float)), 0x00020000);
+        const int S = (nout + nsplit - 1) / nsplit;
+        const int sl0 = slices == 2 ? 0 : split, sl1 = slices == 2 ? nsplit : split + 1;
+        for (int sl = sl0; sl < sl1; ++sl) {
+            for (int t = threadIdx.x; t < 4 * S; t += kThreads) {
+                const int o = sl * S + (t >> 2), q = t & 3;
+                const bool live = o < nout;
+                const int hd = min(o, nout - 1) >> 7, d = min(o, nout - 1) & (kHeadDim - 1);
+                float M = -INFINITY, L = 0.f, O = 0.f;
+                for (int base = 0; q + base < nsplit; base += 32) {
+                    float ms[8], ls[8], os[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int sj = q + base + 4 * j;
+                        const int off = min(sj, nsplit - 1) * (nrep * kPartStride) + hd * kPartStride;
+                        const f2 ml = ld_l2_f2(prs, (off + kHeadDim) * 4);
+                        ms[j] = sj < nsplit ? ml.x : -INFINITY;
+                        ls[j] = ml.y;
+                        os[j] = ld_l2(prs, (off + d) * 4);
+                    }
+                    float Mc = ms[0];
+#pragma unroll
+                    for (int j = 1; j < 8; ++j) Mc = fmaxf(Mc, ms[j]);
+                    if (Mc > -INFINITY) {
+                        const float Mn = fmaxf(M, Mc);
+                        const float a = (M == -INFINITY) ? 0.f : fast_exp2(M - Mn);
+                        float Oc = 0.f, Lc = 0.f;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const float e = (ms[j] == -INFINITY) ? 0.f : fast_exp2(ms[j] - Mn);
+                            Oc += os[j] * e;
+                            Lc += ls[j] * e;
+                        }
+                        O = O * a + Oc;
+                        L = L * a + Lc;
+                        M = Mn;
+                    }
+                }
+                // the output's four threads are adjacent lanes
+#pragma unroll
+                for (int x = 1; x < 4; x <<= 1) {
+                    const float M2 = __shfl_xor(M, x), L2 = __shfl_xor(L, x), O2 = __shfl_xor(O, x);
+                    const float Mn = fmaxf(M, M2);
+                    const float a = (M == -INFINITY) ? 0.f : fast_exp2(M - Mn);
+                    const float c = (M2 == -INFINITY) ? 0.f : fast_exp2(M2 - Mn);
+                    O = O * a + O2 * c;
+                    L = L * a + L2 * c;
+                    M = Mn;
+                }
+                if (live && q == 0) {
+                    const float r = L > 0.f ? O / L : 0.f;
+                    p.out[(int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d] = p.out_bf16 ? f2bf_rn(r) : f2h_rn(r);
+                    if (kScores && d == 0) {
+                        float* st = p.stats + ((int64_t)b * p.Hkv * nrep + h * nrep + hd) * 2;
+                        st[0] = M;
+                        st[1] = L;
+                    }
+                }
+            }
+        }
+        TL_MARK(5);
+        TL_MARK(6);
+        TL_FLUSH(tl_info | (1ull << 48));
+        return;
+    }
     if (threadIdx.x == 0) {
         // the stores above have completed (in L2, or in memory for sc1 stores)
         int tk;
@@ -1221,6 +1353,19 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
     // one range per pair needs no hand-off (and must not leave a mask bit behind)
     p.xcc_local = (BH % p.nxcc) == 0 && ms > 1 && !(a->flags & HKV_DECODE_AGENT_HANDOFF) ? 1 : 0;
     p.max_splits = ms;
+    {
+        // slice merge: every range of a pair must be resident while it waits for the
+        // others (one 8-wave workgroup per CU: the grid fits the CUs), with the XCD-local
+        // hand-off and the on-demand schedule; a slice has at most 128 outputs (4 threads
+        // each).  HKV_DECODE_MERGE_WAIT_TICKS shortens the bounded wait (tests force the
+        // path where ranges stop waiting and the last arrival merges every slice).
+        const int nout = nrep * kHeadDim;
+        const int S = (nout + ms - 1) / ms;
+        p.coop = (p.xcc_local && !(a->flags & HKV_DECODE_DETERMINISTIC) && (int64_t)BH * ms <= num_cus() &&
+                  S <= 128 && ms < kArrivedMask) ? 1 : 0;
+        const char* mw = getenv("HKV_DECODE_MERGE_WAIT_TICKS");
+        p.merge_wait = (mw && mw[0]) ? strtoull(mw, nullptr, 10) : kMergeWaitTicks;
+    }
 #ifdef HKV_DECODE_TIMELINE
     {
         static unsigned long long* tl_ptr[64] = {};

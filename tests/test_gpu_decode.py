@@ -175,6 +175,31 @@ def test_deterministic_bitwise():
     assert ws.error_flag() == 0
 
 
+@pytest.mark.parametrize("splits", [0, 8, 31])
+def test_slice_merge_and_its_fallback(monkeypatch, splits):
+    """Eight kv heads of one sequence, every range of a pair resident (the grid fits the
+    CUs): each range merges one slice of the output once all have arrived.  With
+    HKV_DECODE_MERGE_WAIT_TICKS=0 a range stops waiting at its first poll that does not
+    find every range arrived, and the last arrival merges every slice instead.  Both paths
+    against the oracle on one workspace, alternating, so that each launch starts from the
+    counters the previous one left; the error word stays clear."""
+    from heterokv import ops
+    print("case: slice merge, B=1 32/8, 64 + 8000 + 1000, splits=%d" % splits, flush=True)
+    c = Case(16, 1, 32, 8, 64, [8000], [1000])
+    ref = c.oracle()
+    ws = ops.DecodeWorkspace(DEV)
+    for wait in ("0", None, "0", None, "0", "0", None):
+        if wait is None:
+            monkeypatch.delenv("HKV_DECODE_MERGE_WAIT_TICKS", raising=False)
+        else:
+            monkeypatch.setenv("HKV_DECODE_MERGE_WAIT_TICKS", wait)
+        got = c.run(workspace=ws, splits=splits)
+        err = np.abs(got - ref).max()
+        print("  wait=%s max abs err %.3e" % (wait, err), flush=True)
+        assert np.all(np.isfinite(got)) and err <= TOL
+        assert ws.error_flag() == 0
+
+
 def test_schedules_agree_on_long_windows():
     """Ranges longer than one block-id window (1024 INT4 blocks) restage the ids
     between windows: one range per pair (splits=1) over 40000 INT4 tokens = 2500
