@@ -24,7 +24,10 @@
 // 8 waves of the workgroup takes a contiguous piece of it.  Waves merge through
 // LDS, workgroups through a workspace: the last workgroup of a pair to finish
 // (atomic ticket after a release fence) merges the S partial states with
-// independent loads and writes the output, so the whole op is one launch.
+// independent loads and writes the output, so the whole op is one launch.  When every
+// range of a pair is resident (the grid fits the CUs) with the XCD-local hand-off, each
+// range instead waits (bounded) for the pair's arrival count and merges one slice of
+// the output (the kernel's tail describes both).
 // Workgroup ids interleave the pairs so that all ranges of a pair land on one
 // XCD: dispatch is round-robin over XCDs by workgroup id (the XCD that takes
 // workgroup 0 rotates from launch to launch, so only the id modulo the XCD count
