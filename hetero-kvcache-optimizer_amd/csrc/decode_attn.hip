@@ -202,6 +202,14 @@ __device__ __forceinline__ f2 ld_l2_f2(__amdgpu_buffer_rsrc_t r, int byte_off) {
 
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 
+// The value of lane (lane ^ x) of the same quad, x = 1 or 2 (DPP quad_perm [1,0,3,2] or
+// [2,3,0,1]); every lane of the quad must be active.
+__device__ __forceinline__ float quad_xor(float v, int x) {
+    const int i = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(float, x == 1 ? __builtin_amdgcn_mov_dpp(i, 0xB1, 0xF, 0xF, false)
+                                            : __builtin_amdgcn_mov_dpp(i, 0x4E, 0xF, 0xF, false));
+}
+
 struct Int4Blk {
     u4 k;         // K codes of token (lane%16), dims 32g..32g+31
     u4 v;         // V codes: tokens 4g..4g+3, dims c+16n (n=0..7)
@@ -986,10 +994,11 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                         M = Mn;
                     }
                 }
-                // the output's four threads are adjacent lanes
+                // the output's four threads are one quad of lanes: exchanged with DPP quad
+                // permutes (lane ^ 1, then lane ^ 2), no LDS round trip
 #pragma unroll
                 for (int x = 1; x < 4; x <<= 1) {
-                    const float M2 = __shfl_xor(M, x), L2 = __shfl_xor(L, x), O2 = __shfl_xor(O, x);
+                    const float M2 = quad_xor(M, x), L2 = quad_xor(L, x), O2 = quad_xor(O, x);
                     const float Mn = fmaxf(M, M2);
                     const float a = (M == -INFINITY) ? 0.f : fast_exp2(M - Mn);
                     const float c = (M2 == -INFINITY) ? 0.f : fast_exp2(M2 - Mn);
