@@ -1368,12 +1368,13 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
     {
         // slice merge: every range of a pair must be resident while it waits for the
         // others (one 8-wave workgroup per CU: the grid fits the CUs), with the XCD-local
-        // hand-off and the on-demand schedule; a slice has at most 128 outputs (4 threads
-        // each).  HKV_DECODE_MERGE_WAIT_TICKS shortens the bounded wait (tests force the
+        // hand-off; a slice has at most 128 outputs (4 threads each).  Each output is
+        // merged by one quad in a fixed split order, so the deterministic schedule keeps
+        // bitwise reproducible outputs with it.  HKV_DECODE_MERGE_WAIT_TICKS shortens the bounded wait (tests force the
         // path where ranges stop waiting and the last arrival merges every slice).
         const int nout = nrep * kHeadDim;
         const int S = (nout + ms - 1) / ms;
-        p.coop = (p.xcc_local && !(a->flags & HKV_DECODE_DETERMINISTIC) && (int64_t)BH * ms <= num_cus() &&
+        p.coop = (p.xcc_local && (int64_t)BH * ms <= num_cus() &&
                   S <= 128 && ms < kArrivedMask) ? 1 : 0;
         const char* mw = getenv("HKV_DECODE_MERGE_WAIT_TICKS");
         p.merge_wait = (mw && mw[0]) ? strtoull(mw, nullptr, 10) : kMergeWaitTicks;
