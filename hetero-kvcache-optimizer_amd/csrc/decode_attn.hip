@@ -75,7 +75,11 @@ constexpr int kF16Depth = HKV_DECODE_F16_DEPTH;
 constexpr int kMaxSplits = 64;
 constexpr int kArrivedMask = 0xffff;     // slice merge: arrivals in the low bits of the pair's ticket
 constexpr int kGoneBit = 1 << 30;        // slice merge: a range stopped waiting
-constexpr unsigned long long kMergeWaitTicks = 200000;   // 2 ms of the 100 MHz constant clock
+// Bound of a range's wait in the slice merge: 25 us of the 100 MHz constant clock.  Waits
+// on the 32K decode are under ~4 us; a wait that runs out only hands the whole merge to
+// the last arrival (~3 us), and a short bound limits what two decodes running at once on
+// one GPU (neither kernel's ranges all resident) cost each other.
+constexpr unsigned long long kMergeWaitTicks = 2500;
 // INT4 tokens, and fp16 tokens over all zones, per sequence: 2^22 items of 16 tokens
 // keep the range arithmetic in 32 bits.
 constexpr int kMaxZoneTokens = 1 << 26;
