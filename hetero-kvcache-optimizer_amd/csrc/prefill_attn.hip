@@ -375,10 +375,14 @@ extern "C" int hkv_prefill_attn(const HkvPrefillArgs* a, void* stream) {
     p.czk = nullptr;
     p.czv = nullptr;
     p.ccap = ccap;
+    for (int i = 0; i < HKV_MAX_F16_ZONES; ++i)
+        p.src[i] = PfSrc{p.z[i].k, p.z[i].v, p.z[i].k ? p.z[i].cap : 16, 0};
+    p.src[HKV_MAX_F16_ZONES] = PfSrc{nullptr, nullptr, 16, 0};
     if (a->chunk_k != nullptr) {
         uint8_t* ws = (uint8_t*)a->workspace + state_bytes;
         p.czk = (const uint16_t*)ws;
         p.czv = (const uint16_t*)(ws + chunk_bytes);
+        p.src[HKV_MAX_F16_ZONES] = PfSrc{p.czk, p.czv, ccap, 0};
         HkvZoneWriteArgs zw = {};
         zw.k = a->chunk_k;
         zw.v = a->chunk_v;

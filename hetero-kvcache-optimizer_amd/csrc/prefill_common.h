@@ -31,6 +31,15 @@ struct PfZone {
     const int32_t* lens;
 };
 
+// Where the zone kernel reads the fp16 tiles of one source (a zone, or the causal chunk
+// in the zone layout): K rows [B*Hkv][cap][128], V tiles [B*Hkv][cap/16][16 x 128].
+struct PfSrc {
+    const uint16_t* k;
+    const uint16_t* v;
+    int cap;
+    int pad;
+};
+
 struct PrefillParams {
     int B, Hkv, nrep, Sq;
     float scale_log2;
@@ -58,6 +67,9 @@ struct PrefillParams {
     const uint16_t* czk;         // the causal chunk in the zone layout: K rows [B*Hkv][ccap][128]
     const uint16_t* czv;         // and V tiles [B*Hkv][ccap/16][16 x 128] (null without a chunk)
     int ccap;
+    // the zone kernel's sources in tile order: zones 0..2 (unused ones empty), then the
+    // chunk; indexed at run time, so that no source's pointers stay in registers
+    PfSrc src[HKV_MAX_F16_ZONES + 1];
 };
 
 // Tile counts of one sequence: INT4 tiles, each zone's tiles, and the causal chunk's

@@ -38,31 +38,28 @@ struct F16Stage {
         zone_tiles = tm.nz_t[0] + tm.nz_t[1] + tm.nz_t[2];
         diag = tm.nc > 0 ? zone_tiles + w.qb : -1;
     }
-    // Source of tile x: K rows, V tiles, capacity, valid length, tile index in the source
+    // Source of tile x: K rows, V tiles, capacity, valid length, tile index in the source.
+    // The source index is found from the tile counts and the source read from the
+    // argument block at that (wave-uniform) index: holding every source's pointers in
+    // registers across the tile loop spilled ~100 scalar registers into vector lanes
+    // (~55 lane moves per tile).
     __device__ void source(int x, const uint16_t*& k, const uint16_t*& v, int& cap, int& len, int& xl) const {
-        k = nullptr;
-        v = nullptr;
-        cap = 16;
-        len = 0;
+        int si = 0;
         xl = x;
 #pragma unroll
         for (int zi = 0; zi < HKV_MAX_F16_ZONES; ++zi) {
-            if (zi < p.nz && k == nullptr && xl >= 0 && xl < tm.nz_t[zi]) {
-                k = p.z[zi].k;
-                v = p.z[zi].v;
-                cap = p.z[zi].cap;
-                len = tm.lenz[zi];
-            } else if (zi < p.nz && k == nullptr) {
+            if (si == zi && xl >= tm.nz_t[zi]) {   // zones beyond p.nz have no tiles
                 xl -= tm.nz_t[zi];
+                si = zi + 1;
             }
         }
-        if (k == nullptr && xl >= 0 && xl < tm.nc) {
-            k = p.czk;
-            v = p.czv;
-            cap = p.ccap;
-            len = p.Sq;
-        }
-        if (k == nullptr) xl = 0;
+        const bool ok = si < HKV_MAX_F16_ZONES || xl < tm.nc;
+        const PfSrc& s = p.src[si];
+        k = s.k;
+        v = s.v;
+        cap = s.cap;
+        len = !ok ? 0 : si == 0 ? tm.lenz[0] : si == 1 ? tm.lenz[1] : si == 2 ? tm.lenz[2] : p.Sq;
+        if (!ok) xl = 0;
     }
     __device__ int tvalid(int x) const {
         const uint16_t *k, *v;
