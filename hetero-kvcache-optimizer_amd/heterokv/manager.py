@@ -78,6 +78,7 @@ class _LayerState:
         self.host_lbs: Optional[np.ndarray] = None
         self.version = 0                           # bumped whenever bt or pool change
         self.resident_cache = None
+        self.runs_cache = None                     # (version, selection, host runs)
         # deferred write of a prefill chunk into the tail ring: (k, v, first chunk token
         # written, its ring slot, tail length before the chunk); see _incremental_prefill
         self.pending = None
@@ -175,6 +176,9 @@ class HeteroKVManager:
         # chunk key -> (layer, first INT4 slot, token count), in eviction order
         self._chunks: "OrderedDict[str, Tuple[int, int, int]]" = OrderedDict()
         self._chunk_eviction_order: List[str] = []
+        # the same keys per layer, in eviction order (decode looks a layer's chunks up every
+        # step; scanning every layer's keys cost ~4 ms per token at 128K over 28 layers)
+        self._layer_keys: Dict[int, List[str]] = {}
         self._chunk_attention_scores: Dict[str, float] = {}
         self._eviction_counter = 0
         self._queued_tokens = 0      # tokens the reference would leave in its competition queue
@@ -460,6 +464,7 @@ class HeteroKVManager:
         ops.pack_tokens(st.pool, k, v, torch.full((st.B,), st.int4_len, dtype=torch.int32), st.bt, err=st.err)
         key = "l%d_e%d" % (layer, self._eviction_counter)
         self._chunks[key] = (layer, st.int4_len, n)
+        self._layer_keys.setdefault(layer, []).append(key)
         if isinstance(first_pos, int):
             st.int4_pos.extend(range(first_pos, first_pos + n))
         else:
@@ -546,8 +551,7 @@ class HeteroKVManager:
 
     def count_dram_tokens(self, layer_idx: int = 0) -> int:
         """manager.py:1218-1229: #chunks of the layer times the first chunk's token count."""
-        pre = "l%d_" % layer_idx
-        keys = [k for k in self._chunks if k.startswith(pre)]
+        keys = self._layer_keys.get(layer_idx)
         if not keys:
             return 0
         return len(keys) * self._chunks[keys[0]][2]
@@ -605,7 +609,7 @@ class HeteroKVManager:
             window_size = max(1, min(w_t, len(keys)))
         ranked = sorted(keys, key=lambda k: self._chunk_attention_scores.get(k, 0.0), reverse=True)
         chosen = set(ranked[:max(0, int(window_size))])
-        return [k for k in self._chunk_eviction_order if k in chosen]
+        return [k for k in keys if k in chosen]   # the layer's keys are in eviction order
 
     def get_dram_chunks_quantized_adaptive(self, layer_idx: int, window_size: Optional[int] = None
                                            ) -> Optional[Dict[str, torch.Tensor]]:
@@ -714,6 +718,7 @@ class HeteroKVManager:
         otherwise the later tokens move down by unpack + repack (per-token groups, so the
         codes are unchanged)."""
         layer, start, n = self._chunks.pop(key)
+        self._layer_keys[layer].remove(key)
         # as the reference's _dram.remove: the chunk's eviction-order entry and score stay
         st = self._layers[layer]
         for k2, (l2, s2, n2) in list(self._chunks.items()):
@@ -839,8 +844,7 @@ class HeteroKVManager:
         return full, bt
 
     def _layer_chunks(self, layer_idx: int) -> List[str]:
-        pre = "l%d_" % layer_idx
-        return [k for k in self._chunks if k.startswith(pre)]
+        return list(self._layer_keys.get(layer_idx, ()))
 
     def _selection(self, layer_idx: int):
         """Chunk keys attended at this decode step (None = all), computed once per layer
@@ -860,7 +864,7 @@ class HeteroKVManager:
                 w = max(1, min(w, len(keys)))
                 ranked = sorted(keys, key=lambda k: self._chunk_attention_scores.get(k, 0.0), reverse=True)
                 chosen = set(ranked[:w])
-                sel = tuple(k for k in self._chunk_eviction_order if k in chosen)
+                sel = tuple(k for k in keys if k in chosen)   # the layer's keys are in eviction order
         self._selection_of[layer_idx] = sel
         return sel
 
@@ -890,6 +894,9 @@ class HeteroKVManager:
         """Ranges [k0, k1) of the layer's host records needed for selection `sel`."""
         if sel is None:
             return [(0, st.n_host)]
+        c = st.runs_cache
+        if c is not None and c[0] == st.version and c[1] == sel:
+            return c[2]
         runs = []
         for k in sel:
             _, start, n = self._chunks[k]
@@ -901,6 +908,7 @@ class HeteroKVManager:
                     runs[-1] = (runs[-1][0], k1)
                 else:
                     runs.append((k0, k1))
+        st.runs_cache = (st.version, sel, runs)
         return runs
 
     def _submit(self, layer_idx: int, sel, avoid_buf: Optional[int] = None) -> Tuple[int, Any, int]:

@@ -69,9 +69,10 @@ def test_host_runs_match_brute_force(seed):
     nb = (3520 + 900 + 15) // 16
     full = (3520 + 900) // 16
     chosen = np.sort(rng.choice(B * full, size=int(0.75 * B * full), replace=False))
-    st = SimpleNamespace(n_host=len(chosen), host_lbs=(chosen // B).astype(np.int64))
+    st = SimpleNamespace(n_host=len(chosen), host_lbs=(chosen // B).astype(np.int64), version=0, runs_cache=None)
     assert m._host_runs(st, None) == [(0, len(chosen))]
-    for sel in [("l0_e0",), ("l0_e1", "l0_e3"), ("l0_e0", "l0_e1", "l0_e2", "l0_e3"), ("l0_e2",)]:
+
+    def check(sel):
         want = set()
         for k in sel:
             _, start, n = m._chunks[k]
@@ -84,4 +85,13 @@ def test_host_runs_match_brute_force(seed):
             got |= set(range(k0, k1))
         assert got == want, sel
         assert all(runs[i][1] < runs[i + 1][0] for i in range(len(runs) - 1))  # disjoint, merged
+
+    for sel in [("l0_e0",), ("l0_e1", "l0_e3"), ("l0_e0", "l0_e1", "l0_e2", "l0_e3"), ("l0_e2",), ("l0_e2",)]:
+        check(sel)
+    # the runs are cached per (layer version, selection): a new host placement with a new
+    # version is not answered from the cache
+    keep = np.sort(rng.choice(len(chosen), size=len(chosen) // 2, replace=False))
+    st.host_lbs, st.n_host = st.host_lbs[keep], len(keep)
+    st.version += 1
+    check(("l0_e2",))
     assert nb >= full
