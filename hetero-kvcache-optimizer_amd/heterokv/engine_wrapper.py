@@ -377,8 +377,14 @@ class ChunkedPrefillEngine:
                 for key in list(self.cache.dram_table.keys()):
                     self.cache.schedule_prefetch(key)
             chunk_idx += 1
-            if chunk_idx % 4 == 0 or end == total_len:
+            # The reference collects every 4 chunks (:491-494).  A full collection walks
+            # every tracked object of the process (~430K with transformers loaded, ~140 ms),
+            # so the chunks in between collect the young generations only, where a chunk's
+            # transient objects live; the last chunk still runs a full collection.
+            if end == total_len:
                 gc.collect()
+            elif chunk_idx % 4 == 0:
+                gc.collect(1)
         return last
 
 

@@ -108,7 +108,7 @@ class _LayerState:
         self.bt_host[:, self.nb:need] = (self.pool_used + np.arange(B, dtype=np.int32)[:, None] * add +
                                          np.arange(add, dtype=np.int32)[None, :])
         self.pool_used, self.nb = used, need
-        self.bt = torch.from_numpy(self.bt_host).to(self.device)
+        self.bt = ops.h2d(torch.from_numpy(self.bt_host), self.device)
         self.version += 1
 
     # -------------------------------------------------------------- tail ring
@@ -691,7 +691,9 @@ class HeteroKVManager:
             return
         if self._async_pf is None:
             self._async_pf = AsyncPrefetcher(self.device)
-        if chunk_key not in self._async_pf.buffer and self._async_pf.free_slots == 0:
+        # a chunk already dequantized is skipped by the prefetcher: skip it before its
+        # codes are gathered (that gather is a kernel launch and a host round trip)
+        if chunk_key in self._async_pf.buffer or self._async_pf.free_slots == 0:
             return
         self._async_pf.submit_prefetch_task(chunk_key, self.chunk_codes(chunk_key), self._compressor)
 
@@ -754,7 +756,7 @@ class HeteroKVManager:
                                  st.bt, err=st.err)
             st.nb = (st.int4_len - n + BLOCK_TOKENS - 1) // BLOCK_TOKENS
         st.int4_len -= n
-        st.bt = torch.from_numpy(np.ascontiguousarray(st.bt_host)).to(self.device)
+        st.bt = ops.h2d(torch.from_numpy(np.ascontiguousarray(st.bt_host)), self.device)
         st.version += 1
         st.resident_cache = None
         self._window_tables = {k2: v for k2, v in self._window_tables.items() if k2[0] != layer}
@@ -811,7 +813,7 @@ class HeteroKVManager:
             for pl in (tmp, pool):
                 pl.check_errors()
             st.pool, st.pool_used, st.bt_host = pool, len(res_ids), bh
-            st.bt = torch.from_numpy(bh).to(self.device)
+            st.bt = ops.h2d(torch.from_numpy(bh), self.device)
             st.n_host, st.host_off, st.host_lbs = len(chosen), off, lb.astype(np.int64)
             st.version += 1
             st.resident_cache = None
@@ -885,7 +887,7 @@ class HeteroKVManager:
                 raise HeteroKVError(-4, "windowed retrieval: only the last selected chunk may be partial")
             lbs.extend(range(start // BLOCK_TOKENS, (start + n + BLOCK_TOKENS - 1) // BLOCK_TOKENS))
             n4 += n
-        bt = torch.from_numpy(np.ascontiguousarray(st.bt_host[:, lbs])).to(self.device)
+        bt = ops.h2d(torch.from_numpy(np.ascontiguousarray(st.bt_host[:, lbs])), self.device)
         self._window_tables = {k2: v for k2, v in self._window_tables.items() if k2[0] != layer_idx}
         self._window_tables[key] = (bt, n4)
         return bt, n4

@@ -158,9 +158,21 @@ class Int4Pool:
             raise HeteroKVError(-1, "; ".join(why))
 
 
+def h2d(t, device):
+    """Host tensor t on `device`.  A copy from pageable memory waits for every kernel
+    already queued on the stream; this one goes through pinned memory (held by torch's
+    caching host allocator until the copy has run) and does not wait."""
+    device = torch.device(device)
+    if t.device.type != "cpu" or device.type != "cuda" or torch.cuda.is_current_stream_capturing():
+        return t.to(device)
+    return t.pin_memory().to(device, non_blocking=True)
+
+
 def _i32(t, device):
     if not isinstance(t, torch.Tensor):
         t = torch.tensor(t, dtype=torch.int32)
+    if t.device.type == "cpu":
+        return h2d(t.to(torch.int32).contiguous(), device)
     return t.to(device=device, dtype=torch.int32).contiguous()
 
 
