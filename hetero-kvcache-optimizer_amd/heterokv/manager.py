@@ -40,6 +40,40 @@ from .kv_compressor import KVCompressor
 from .prefetcher import AdaptivePrefetchController, AsyncPrefetcher, Prefetcher
 
 
+class _Scores(dict):
+    """Chunk scores that count their writes, so that a layer's cached ranking is rebuilt
+    after any change."""
+    epoch = 0
+
+    def __setitem__(self, k, v):
+        self.epoch += 1
+        super().__setitem__(k, v)
+
+    def __delitem__(self, k):
+        self.epoch += 1
+        super().__delitem__(k)
+
+    def update(self, *a, **kw):
+        self.epoch += 1
+        super().update(*a, **kw)
+
+    def pop(self, *a):
+        self.epoch += 1
+        return super().pop(*a)
+
+    def popitem(self):
+        self.epoch += 1
+        return super().popitem()
+
+    def setdefault(self, k, d=None):
+        self.epoch += 1
+        return super().setdefault(k, d)
+
+    def clear(self):
+        self.epoch += 1
+        super().clear()
+
+
 class _LayerState:
     def __init__(self, B, H, device, dtype, sink_tokens, tail_budget, hh_budget, err):
         self.B, self.H, self.device, self.dtype = B, H, device, dtype
@@ -179,7 +213,11 @@ class HeteroKVManager:
         # the same keys per layer, in eviction order (decode looks a layer's chunks up every
         # step; scanning every layer's keys cost ~4 ms per token at 128K over 28 layers)
         self._layer_keys: Dict[int, List[str]] = {}
-        self._chunk_attention_scores: Dict[str, float] = {}
+        # a layer's chunk keys by descending score (scores are set at eviction), and the
+        # selection per window size, until the layer's chunks change
+        self._ranked: Dict[int, Tuple[int, List[str]]] = {}
+        self._sel_cache: Dict[Tuple[int, int], Tuple[int, Tuple[str, ...]]] = {}
+        self._chunk_attention_scores: Dict[str, float] = _Scores()
         self._eviction_counter = 0
         self._queued_tokens = 0      # tokens the reference would leave in its competition queue
         self._workspace = None
@@ -465,6 +503,7 @@ class HeteroKVManager:
         key = "l%d_e%d" % (layer, self._eviction_counter)
         self._chunks[key] = (layer, st.int4_len, n)
         self._layer_keys.setdefault(layer, []).append(key)
+        self._forget_ranking(layer)
         if isinstance(first_pos, int):
             st.int4_pos.extend(range(first_pos, first_pos + n))
         else:
@@ -607,9 +646,7 @@ class HeteroKVManager:
             w_t = int(self._adaptive_controller.compute_window(attention_weights=self._last_attention_weights,
                                                                cache_miss=False))
             window_size = max(1, min(w_t, len(keys)))
-        ranked = sorted(keys, key=lambda k: self._chunk_attention_scores.get(k, 0.0), reverse=True)
-        chosen = set(ranked[:max(0, int(window_size))])
-        return [k for k in keys if k in chosen]   # the layer's keys are in eviction order
+        return list(self._top_chunks(layer_idx, keys, int(window_size)))
 
     def get_dram_chunks_quantized_adaptive(self, layer_idx: int, window_size: Optional[int] = None
                                            ) -> Optional[Dict[str, torch.Tensor]]:
@@ -721,6 +758,7 @@ class HeteroKVManager:
         codes are unchanged)."""
         layer, start, n = self._chunks.pop(key)
         self._layer_keys[layer].remove(key)
+        self._forget_ranking(layer)
         # as the reference's _dram.remove: the chunk's eviction-order entry and score stay
         st = self._layers[layer]
         for k2, (l2, s2, n2) in list(self._chunks.items()):
@@ -848,6 +886,26 @@ class HeteroKVManager:
     def _layer_chunks(self, layer_idx: int) -> List[str]:
         return list(self._layer_keys.get(layer_idx, ()))
 
+    def _forget_ranking(self, layer_idx: int) -> None:
+        self._ranked.pop(layer_idx, None)
+        self._sel_cache = {k: v for k, v in self._sel_cache.items() if k[0] != layer_idx}
+
+    def _top_chunks(self, layer_idx: int, keys: List[str], w: int) -> Tuple[str, ...]:
+        """The top w of the layer's chunks by score (stable descending sort), in eviction
+        order."""
+        epoch = self._chunk_attention_scores.epoch
+        hit = self._sel_cache.get((layer_idx, w))
+        if hit is not None and hit[0] == epoch:
+            return hit[1]
+        ranked = self._ranked.get(layer_idx)
+        if ranked is None or ranked[0] != epoch:
+            ranked = (epoch, sorted(keys, key=lambda k: self._chunk_attention_scores.get(k, 0.0), reverse=True))
+            self._ranked[layer_idx] = ranked
+        chosen = set(ranked[1][:max(0, w)])
+        sel = tuple(k for k in keys if k in chosen)   # the layer's keys are in eviction order
+        self._sel_cache[(layer_idx, w)] = (epoch, sel)
+        return sel
+
     def _selection(self, layer_idx: int):
         """Chunk keys attended at this decode step (None = all), computed once per layer
         and step: the window size comes from retrieval_window or, for "adaptive", from the
@@ -864,9 +922,7 @@ class HeteroKVManager:
                 else:
                     w = int(self.retrieval_window)
                 w = max(1, min(w, len(keys)))
-                ranked = sorted(keys, key=lambda k: self._chunk_attention_scores.get(k, 0.0), reverse=True)
-                chosen = set(ranked[:w])
-                sel = tuple(k for k in keys if k in chosen)   # the layer's keys are in eviction order
+                sel = self._top_chunks(layer_idx, keys, w)
         self._selection_of[layer_idx] = sel
         return sel
 
