@@ -826,14 +826,11 @@ def cpu_baseline_c5(torch, model, budget_s):
                       % (reps, t_layer)}
 
 
-def leg_c5(torch, args, timed=8, warm=2):
-    """End-to-end tiered decode at 131072 tokens: chunked prefill (2048-token chunks, fused
-    prefill kernel), then 75% of every layer's INT4 block records moved to pinned host memory;
-    decode with each layer's host records copied on the side stream one layer ahead.  Greedy
-    tokens; every variant decodes `timed` tokens after `warm` untimed ones."""
-    from heterokv.engine_wrapper import ChunkedPrefillEngine, DecodeGraph, FusedHeteroCache
-    from oracle import torch_ref as tr
-    dev = torch.device("cuda:0")
+def _tiered_prefill(torch, dev):
+    """The C5 model and its 131072-token prompt, prefilled in 2048-token chunks (fused prefill
+    kernel) through ChunkedPrefillEngine, four calls of 32768 tokens.  Returns the model, the
+    token ids, the cache and the prefill wall seconds."""
+    from heterokv.engine_wrapper import ChunkedPrefillEngine, FusedHeteroCache
     t0 = time.perf_counter()
     model = _tiered_model(torch, dev)
     torch.cuda.synchronize()
@@ -850,7 +847,27 @@ def leg_c5(torch, args, timed=8, warm=2):
             torch.cuda.synchronize()
             print("[c5] prefill %d / %d tokens, %.1f s" % (part.shape[1], T_CTX, time.perf_counter() - t0),
                   file=sys.stderr, flush=True)
-    prefill_s = time.perf_counter() - t0
+    return model, ids, cache, time.perf_counter() - t0
+
+
+def bench_tiered_prefill(torch, args):
+    """The C5 model's 128K chunked prefill alone (for a kernel trace of it)."""
+    _, _, cache, prefill_s = _tiered_prefill(torch, torch.device("cuda:0"))
+    return {"workload": "128K chunked prefill of the C5 model (28 layers, 28 q / 4 kv heads, hidden 3584, random-init "
+                        "bf16 weights, 2048-token chunks, sink 64 + recent 4096 fp16, the rest packed to INT4)",
+            "prefill_seconds": round(prefill_s, 2), "tokens": T_CTX, "tok_per_s": round(T_CTX / prefill_s, 1),
+            "int4_tokens_per_layer": cache._manager.dram_tokens(0)}
+
+
+def leg_c5(torch, args, timed=8, warm=2):
+    """End-to-end tiered decode at 131072 tokens: chunked prefill (2048-token chunks, fused
+    prefill kernel), then 75% of every layer's INT4 block records moved to pinned host memory;
+    decode with each layer's host records copied on the side stream one layer ahead.  Greedy
+    tokens; every variant decodes `timed` tokens after `warm` untimed ones."""
+    from heterokv.engine_wrapper import DecodeGraph
+    from oracle import torch_ref as tr
+    dev = torch.device("cuda:0")
+    model, ids, cache, prefill_s = _tiered_prefill(torch, dev)
     mgr = cache._manager
     int4_tokens = mgr.dram_tokens(0)
     out = {}
@@ -1071,10 +1088,12 @@ def main():
                          "paged decode), c4 (chunked prefill), c5 (128K tiered decode with 75%% host offload); "
                          "'none' for the 32K decode alone")
     ap.add_argument("--workload",
-                    choices=["decode", "prefill", "tiered", "paged", "scoring", "quant", "probe", "timeline"],
+                    choices=["decode", "prefill", "tiered", "tiered-prefill", "paged", "scoring", "quant", "probe",
+                             "timeline"],
                     default=None,
                     help="run one configuration alone and print its block as the line (for profiling): decode "
-                         "(32K), prefill (C4), tiered (C5), paged (C3), quant (C1), scoring (heavy hitters), probe "
+                         "(32K), prefill (C4), tiered (C5), tiered-prefill (the C5 model's 128K chunked prefill alone), paged "
+                         "(C3), quant (C1), scoring (heavy hitters), probe "
                          "(streaming-read probes at the decode's byte count), timeline (the 32K decode kernel's "
                          "phase timeline from the library's timeline build)")
     ap.add_argument("--probe-shapes", default=None,
@@ -1108,7 +1127,8 @@ def main():
     single = {"prefill": lambda: leg_c4(torch, ops, args), "paged": lambda: leg_c3(torch, ops, args),
               "quant": lambda: leg_c1(torch, ops, args), "tiered": lambda: leg_c5(torch, args),
               "scoring": lambda: bench_scoring(torch, ops, args), "probe": lambda: bench_probe(torch, args),
-              "timeline": lambda: bench_timeline(torch, args)}
+              "timeline": lambda: bench_timeline(torch, args),
+              "tiered-prefill": lambda: bench_tiered_prefill(torch, args)}
     if args.workload in single:
         blk = single[args.workload]()
         if blk is not None:
