@@ -893,11 +893,12 @@ class HeteroKVManager:
     def _top_chunks(self, layer_idx: int, keys: List[str], w: int) -> Tuple[str, ...]:
         """The top w of the layer's chunks by score (stable descending sort), in eviction
         order."""
-        epoch = self._chunk_attention_scores.epoch
-        hit = self._sel_cache.get((layer_idx, w))
+        # scores replaced by a plain dict count no writes: nothing is cached then
+        epoch = getattr(self._chunk_attention_scores, "epoch", None)
+        hit = self._sel_cache.get((layer_idx, w)) if epoch is not None else None
         if hit is not None and hit[0] == epoch:
             return hit[1]
-        ranked = self._ranked.get(layer_idx)
+        ranked = self._ranked.get(layer_idx) if epoch is not None else None
         if ranked is None or ranked[0] != epoch:
             ranked = (epoch, sorted(keys, key=lambda k: self._chunk_attention_scores.get(k, 0.0), reverse=True))
             self._ranked[layer_idx] = ranked

@@ -95,3 +95,25 @@ def test_host_runs_match_brute_force(seed):
     st.version += 1
     check(("l0_e2",))
     assert nb >= full
+
+
+def test_window_selection_follows_score_changes():
+    """The cached ranking of a layer's chunks is rebuilt after any score write, and the
+    selection stays in eviction order."""
+    from heterokv.manager import _Scores
+    chunks = [("l0_e%d" % i, (0, 64 * i, 64)) for i in range(6)]
+    m = _manager_stub(chunks)
+    m._chunk_attention_scores = _Scores({k: 1.0 / (i + 1) for i, k in enumerate(m._chunks)})
+    m._ranked, m._sel_cache = {}, {}
+    keys = list(m._chunks)
+    assert m._top_chunks(0, keys, 2) == ("l0_e0", "l0_e1")
+    assert m._top_chunks(0, keys, 2) == ("l0_e0", "l0_e1")          # from the cache
+    m._chunk_attention_scores["l0_e4"] = 5.0
+    assert m._top_chunks(0, keys, 2) == ("l0_e0", "l0_e4")
+    m._chunk_attention_scores.update({"l0_e5": 9.0, "l0_e2": 7.0})
+    assert m._top_chunks(0, keys, 3) == ("l0_e2", "l0_e4", "l0_e5")
+    # a plain dict put in its place is not cached at all
+    m._chunk_attention_scores = {k: float(i) for i, k in enumerate(keys)}
+    assert m._top_chunks(0, keys, 2) == ("l0_e4", "l0_e5")
+    m._chunk_attention_scores["l0_e0"] = 99.0
+    assert m._top_chunks(0, keys, 2) == ("l0_e0", "l0_e5")
