@@ -67,7 +67,8 @@ struct F16Stage {
         source(x, k, v, cap, len, xl);
         return min(kPfT, max(0, len - xl * kPfT));
     }
-    __device__ void load(int x) {
+    __device__ void load(int x) { load_into(x, slot); }
+    __device__ void load_into(int x, u4 (&dst)[4]) const {
         const uint16_t *k, *v;
         int cap, len, xl;
         source(x, k, v, cap, len, xl);
@@ -78,10 +79,10 @@ struct F16Stage {
             if (tok < len) {
                 const uint16_t* kp = k + (bh * cap + tok) * kHeadDim + (w.lane & 3) * 32;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) slot[j] = *(const u4*)(kp + 8 * j);
+                for (int j = 0; j < 4; ++j) dst[j] = *(const u4*)(kp + 8 * j);
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) slot[j] = u4{0u, 0u, 0u, 0u};
+                for (int j = 0; j < 4; ++j) dst[j] = u4{0u, 0u, 0u, 0u};
             }
         } else {
             // 64 bytes of the 16-token V tile 4 xl + wt: halves [n][i] = V[4g + i][c + 16n]
@@ -89,10 +90,10 @@ struct F16Stage {
             if (ztl * kBlockTokens < len) {
                 const uint16_t* vp = v + (bh * (cap / kBlockTokens) + ztl) * (kBlockTokens * kHeadDim) + w.lane * 32;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) slot[j] = *(const u4*)(vp + 8 * j);
+                for (int j = 0; j < 4; ++j) dst[j] = *(const u4*)(vp + 8 * j);
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) slot[j] = u4{0u, 0u, 0u, 0u};
+                for (int j = 0; j < 4; ++j) dst[j] = u4{0u, 0u, 0u, 0u};
             }
         }
     }
@@ -122,9 +123,13 @@ struct F16Stage {
     }
     __device__ void refill(int, int x) { load(x + kRing); }
     __device__ void start(uint8_t* lds) {
+        // tiles 0 and 1 requested together: one load round trip before the loop, not two
+        u4 next[4];
         load(0);
+        load_into(1, next);
         stage(0, flat_buf(lds, 0), flat_bias(lds, 0), 0);
-        load(1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) slot[j] = next[j];
         stage(0, flat_buf(lds, 1), flat_bias(lds, 1), 1);
         load(2);
     }
