@@ -208,6 +208,21 @@ def check(rc, what=""):
         raise HeteroKVError(rc, (what + ": " if what else "") + msg)
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device=None):
-    """Raw hipStream_t of torch's current stream on `device`."""
+    """Raw hipStream_t of torch's current stream on `device` (a torch.device, an index or
+    None for the current device)."""
+    if _raw_stream is not None:
+        if isinstance(device, torch.device):
+            idx = device.index if device.index is not None else torch.cuda.current_device()
+        elif isinstance(device, int):
+            idx = device
+        elif device is None:
+            idx = torch.cuda.current_device()
+        else:
+            d = torch.device(device)
+            idx = d.index if d.index is not None else torch.cuda.current_device()
+        return ctypes.c_void_p(_raw_stream(idx))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

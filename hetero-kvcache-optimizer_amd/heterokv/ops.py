@@ -5,6 +5,7 @@ pointers and torch's current stream to the library, and raises HeteroKVError on
 any failure.  Nothing falls back to the CPU.
 """
 import ctypes
+import functools
 import math
 
 import torch
@@ -341,6 +342,12 @@ class F16Zone:
 
 # ----------------------------------------------------------------------- decode attention
 def decode_workspace_bytes(batch, num_q_heads, num_kv_heads, int4_max_len, f16_max_lens):
+    return _decode_workspace_bytes(int(batch), int(num_q_heads), int(num_kv_heads), int(int4_max_len),
+                                   tuple(int(x) for x in f16_max_lens))
+
+
+@functools.lru_cache(maxsize=256)
+def _decode_workspace_bytes(batch, num_q_heads, num_kv_heads, int4_max_len, f16_max_lens):
     arr = (ctypes.c_int32 * max(len(f16_max_lens), 1))(*f16_max_lens)
     n = load().hkv_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, HEAD_DIM, int4_max_len,
                                           ctypes.cast(arr, ctypes.c_void_p), len(f16_max_lens))
