@@ -418,7 +418,9 @@ def leg_c1(torch, ops, args):
     vs = [V16.to(dev) for _ in range(R)]
     pools = [ops.Int4Pool(256, 8, dev) for _ in range(R)]
     bt = torch.arange(256, dtype=torch.int32, device=dev)[None]
-    start = torch.zeros(1, dtype=torch.int32, device=dev)
+    # the start slot as the manager's append passes it: a host value, which goes to the
+    # kernel by value (HkvPackArgs.start_base)
+    start = [0]
 
     def quant(i):
         ops.pack_tokens(pools[i % R], ks[i % R], vs[i % R], start, bt)

@@ -84,13 +84,14 @@ struct PackParams {
     int dtype;
     int64_t sb, sh, st;
     int H, T;
-    const int32_t* start_pos;
+    const int32_t* start_pos;    // null: every sequence starts at start_base
     const int32_t* bt;
     int bt_stride;
     uint8_t* pool;
     int64_t pool_blocks;
     int32_t* err;
     int vec_ok;  // 16-byte aligned rows: use 128-bit loads
+    int start_base;
 };
 
 // Values p[0..7] and p[64..71] of a token row, as 16-bit words (w[i] = values 2i, 2i + 1
@@ -171,7 +172,8 @@ static_assert(kHeadPartBytes % 16 == 0 && kPartVecs <= 256, "one 16-byte store p
 __global__ __launch_bounds__(256) void pack_tokens_kernel(PackParams p) {
     touch_kernel_args(p);
     const int b = blockIdx.z, h = blockIdx.y;
-    const int start = load_uniform_i32(p.start_pos, b);
+    // a start passed by value saves the kernel its first memory round trip
+    const int start = p.start_pos ? load_uniform_i32(p.start_pos, b) : p.start_base;
     const int lb = start / kBlockTokens + (int)blockIdx.x;
     const int lo = max(start, lb * kBlockTokens) - lb * kBlockTokens;
     const int hi = min(start + p.T, lb * kBlockTokens + kBlockTokens) - lb * kBlockTokens;
@@ -488,8 +490,7 @@ extern "C" int hkv_pack_tokens(const HkvPackArgs* a, void* stream) {
     HKV_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->num_tokens >= 0, HKV_ERR_ARG,
                 "hkv_pack_tokens: bad batch/heads/tokens");
     if (a->batch == 0 || a->num_tokens == 0) return HKV_OK;
-    HKV_REQUIRE(a->k && a->v && a->start_pos && a->block_table && a->pool, HKV_ERR_ARG,
-                "hkv_pack_tokens: null pointer");
+    HKV_REQUIRE(a->k && a->v && a->block_table && a->pool, HKV_ERR_ARG, "hkv_pack_tokens: null pointer");
     HKV_REQUIRE(a->pool_blocks > 0 && a->bt_stride > 0, HKV_ERR_ARG, "hkv_pack_tokens: empty pool/table");
     HKV_REQUIRE(a->batch <= 65535 && a->num_kv_heads <= 65535, HKV_ERR_ARG, "hkv_pack_tokens: grid too large");
     PackParams p;
@@ -502,6 +503,7 @@ extern "C" int hkv_pack_tokens(const HkvPackArgs* a, void* stream) {
     p.H = a->num_kv_heads;
     p.T = a->num_tokens;
     p.start_pos = a->start_pos;
+    p.start_base = a->start_base;
     p.bt = a->block_table;
     p.bt_stride = a->bt_stride;
     p.pool = a->pool;

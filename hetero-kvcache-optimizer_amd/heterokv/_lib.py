@@ -13,7 +13,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libheterokv.so")
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_U8 = 0, 1, 2, 3
 MAX_F16_ZONES = 3
 DECODE_DETERMINISTIC = 1   # HKV_DECODE_DETERMINISTIC
@@ -65,7 +65,7 @@ class PackArgs(ctypes.Structure):
                 ("src_stride_b", i64), ("src_stride_h", i64), ("src_stride_t", i64),
                 ("batch", i32), ("num_kv_heads", i32), ("head_dim", i32), ("num_tokens", i32),
                 ("start_pos", vp), ("block_table", vp), ("bt_stride", i32),
-                ("pool", vp), ("pool_blocks", i64), ("err_flag", vp)]
+                ("pool", vp), ("pool_blocks", i64), ("err_flag", vp), ("start_base", i32)]
 
 
 class RepackArgs(ctypes.Structure):

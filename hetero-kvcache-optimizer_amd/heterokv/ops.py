@@ -178,9 +178,28 @@ def _i32(t, device):
 
 
 def _check_table(bt, sp, B, T, what):
-    if bt.shape[0] < B or sp.numel() < B:
+    nsp = sp.numel() if sp is not None else B
+    if bt.shape[0] < B or nsp < B:
         raise HeteroKVError(-1, "%s: block table / start positions cover %d / %d sequences, need %d" %
-                            (what, bt.shape[0], sp.numel(), B))
+                            (what, bt.shape[0], nsp, B))
+
+
+def _uniform_start(start_pos, B):
+    """The common start of every sequence when start_pos is host data (an int, a list, or
+    a CPU tensor) with one value for all B sequences, else None."""
+    if isinstance(start_pos, int):
+        return start_pos
+    if isinstance(start_pos, torch.Tensor):
+        if start_pos.device.type != "cpu" or start_pos.numel() < B:
+            return None
+        start_pos = start_pos.reshape(-1)[:B].tolist()
+    elif isinstance(start_pos, (list, tuple)):
+        start_pos = list(start_pos)[:B]
+    else:
+        return None
+    if len(start_pos) == B and all(int(x) == int(start_pos[0]) for x in start_pos):
+        return int(start_pos[0])
+    return None
 
 
 def pack_tokens(pool, k, v, start_pos, block_table, err=None):
@@ -197,7 +216,9 @@ def pack_tokens(pool, k, v, start_pos, block_table, err=None):
     B, H, T, _ = k.shape
     if H != pool.num_kv_heads:
         raise HeteroKVError(-1, "pack_tokens: %d heads, pool has %d" % (H, pool.num_kv_heads))
-    sp = _i32(start_pos, k.device)
+    # one host start for every sequence goes by value: no copy, and no read in the kernel
+    base = _uniform_start(start_pos, B)
+    sp = _i32(start_pos, k.device) if base is None else None
     bt = _i32(block_table, k.device)
     if bt.dim() == 1:
         bt = bt.unsqueeze(0)
@@ -205,9 +226,10 @@ def pack_tokens(pool, k, v, start_pos, block_table, err=None):
     a = _lib.PackArgs(k=k.data_ptr(), v=v.data_ptr(), dtype=_DTYPES[k.dtype],
                       src_stride_b=k.stride(0), src_stride_h=k.stride(1), src_stride_t=k.stride(2),
                       batch=B, num_kv_heads=H, head_dim=HEAD_DIM, num_tokens=T,
-                      start_pos=sp.data_ptr(), block_table=bt.data_ptr(), bt_stride=bt.shape[1],
-                      pool=pool.data.data_ptr(), pool_blocks=pool.num_blocks,
-                      err_flag=err.ptr() if err is not None else pool.err.data_ptr())
+                      start_pos=sp.data_ptr() if sp is not None else None, block_table=bt.data_ptr(),
+                      bt_stride=bt.shape[1], pool=pool.data.data_ptr(), pool_blocks=pool.num_blocks,
+                      err_flag=err.ptr() if err is not None else pool.err.data_ptr(),
+                      start_base=base if base is not None else 0)
     check(load().hkv_pack_tokens(ctypes.byref(a), stream_ptr(k.device)), "hkv_pack_tokens")
 
 

@@ -78,7 +78,7 @@
 extern "C" {
 #endif
 
-#define HKV_ABI_VERSION 8
+#define HKV_ABI_VERSION 9
 
 /* dtype codes */
 #define HKV_DTYPE_F16  0
@@ -138,8 +138,9 @@ int hkv_dequantize_groups(const uint8_t* codes, const float* scales, const uint8
  * Quantize `num_tokens` consecutive tokens of every sequence and pack them into
  * INT4 block records (the quantize+pack append kernel).  Token t of sequence b
  * (source K/V at k + b*src_stride_b + h*src_stride_h + t*src_stride_t) goes to
- * INT4 slot p = start_pos[b] + t: record block_table[b*bt_stride + p/16], row p%16.
- * Rows of a block outside the written range keep their contents.
+ * INT4 slot p = start_pos[b] + t (start_base + t when start_pos is NULL): record
+ * block_table[b*bt_stride + p/16], row p%16.  Rows of a block outside the written
+ * range keep their contents.
  */
 typedef struct HkvPackArgs {
     const void* k;
@@ -147,13 +148,15 @@ typedef struct HkvPackArgs {
     int32_t dtype;                 /* F16 or BF16 */
     int64_t src_stride_b, src_stride_h, src_stride_t;   /* elements */
     int32_t batch, num_kv_heads, head_dim, num_tokens;
-    const int32_t* start_pos;      /* [batch], device */
+    const int32_t* start_pos;      /* [batch], device; NULL: every sequence starts at start_base */
     const int32_t* block_table;    /* [batch][bt_stride], device */
     int32_t bt_stride;
     uint8_t* pool;                 /* block records */
     int64_t pool_blocks;
     int32_t* err_flag;             /* optional device int: bit 0 = a block id outside the pool,
                                       bit 1 = a slot beyond the block table row (nothing written) */
+    int32_t start_base;            /* first slot of every sequence when start_pos is NULL (by
+                                      value: the kernel reads no start position from memory) */
 } HkvPackArgs;
 
 int hkv_pack_tokens(const HkvPackArgs* args, void* stream);

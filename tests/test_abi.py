@@ -32,7 +32,7 @@ def test_header_symbols_exported(lib):
 
 
 def test_version_and_record_size(lib):
-    assert lib.hkv_abi_version() == 8
+    assert lib.hkv_abi_version() == 9
     assert lib.hkv_block_bytes(8, 128) == 17664
     assert lib.hkv_block_bytes(4, 128) == 8832
     assert lib.hkv_block_bytes(8, 64) == -1

@@ -191,6 +191,27 @@ def test_batched_pack_two_sequences():
         assert np.array_equal(got[used], exp[used])
 
 
+@pytest.mark.parametrize("start", [0, 21])
+def test_start_by_value_equals_start_array(start):
+    """One host start for every sequence is passed by value (no start array); the records
+    equal those of the same start given as a device array."""
+    print("case: pack start %d by value vs device array" % start, flush=True)
+    from heterokv import ops
+    H, T = 4, 50
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn((2, H, T, 128), generator=g).half().to(DEV)
+    v = torch.randn((2, H, T, 128), generator=g).half().to(DEV)
+    bt = torch.tensor([[0, 1, 2, 3, 4, 5], [11, 10, 9, 8, 7, 6]], dtype=torch.int32)
+    by_value = ops.Int4Pool(12, H, DEV)
+    ops.pack_tokens(by_value, k, v, [start, start], bt)
+    by_array = ops.Int4Pool(12, H, DEV)
+    ops.pack_tokens(by_array, k, v, torch.tensor([start, start], dtype=torch.int32).to(DEV), bt)
+    torch.cuda.synchronize()
+    assert torch.equal(by_value.data, by_array.data)
+    by_value.check_errors()
+    by_array.check_errors()
+
+
 def test_out_of_range_block_id_is_flagged_not_written():
     print("case: bad block id", flush=True)
     from heterokv import HeteroKVError, ops
