@@ -213,8 +213,8 @@ class HeteroKVManager:
         # the same keys per layer, in eviction order (decode looks a layer's chunks up every
         # step; scanning every layer's keys cost ~4 ms per token at 128K over 28 layers)
         self._layer_keys: Dict[int, List[str]] = {}
-        # a layer's chunk keys by descending score (scores are set at eviction), and the
-        # selection per window size, until the layer's chunks change
+        # a layer's chunk keys by descending score, and the selection per window size,
+        # kept until the layer's chunks or any chunk score change
         self._ranked: Dict[int, Tuple[int, List[str]]] = {}
         self._sel_cache: Dict[Tuple[int, int], Tuple[int, Tuple[str, ...]]] = {}
         self._chunk_attention_scores: Dict[str, float] = _Scores()
@@ -499,7 +499,7 @@ class HeteroKVManager:
         """manager.py:1231-1299: quantize + pack into the layer's INT4 blocks, record the chunk."""
         n = k.shape[2]
         st.ensure_int4(st.int4_len + n)
-        ops.pack_tokens(st.pool, k, v, torch.full((st.B,), st.int4_len, dtype=torch.int32), st.bt, err=st.err)
+        ops.pack_tokens(st.pool, k, v, st.int4_len, st.bt, err=st.err)   # one start, by value
         key = "l%d_e%d" % (layer, self._eviction_counter)
         self._chunks[key] = (layer, st.int4_len, n)
         self._layer_keys.setdefault(layer, []).append(key)

@@ -204,7 +204,9 @@ def _uniform_start(start_pos, B):
 
 def pack_tokens(pool, k, v, start_pos, block_table, err=None):
     """Quantize + pack k, v [B, H, T, 128] (fp16/bf16) into `pool` at INT4 slots start_pos[b] + t.
-    Bad block ids / slots are reported in `err` (an ErrorWord; default the pool's word)."""
+    start_pos: an int (every sequence), a host list / CPU tensor, or a device int32 tensor
+    [B]; one host value for every sequence reaches the kernel by value.  Bad block ids /
+    slots are reported in `err` (an ErrorWord; default the pool's word)."""
     _require_gpu(k, v)
     if k.shape != v.shape or k.dim() != 4 or k.shape[-1] != HEAD_DIM:
         raise HeteroKVError(-1, "pack_tokens: k/v must both be [B, H, T, 128], got %s / %s" %
