@@ -200,6 +200,45 @@ def test_slice_merge_and_its_fallback(monkeypatch, splits):
         assert ws.error_flag() == 0
 
 
+def test_decode_beside_a_concurrent_kernel():
+    """Decode launches while GEMMs on another stream hold many CUs, so the ranges of a pair
+    need not all be resident at once: the slice merge's bounded wait hands the merge to the
+    last arrival when ranges give up waiting.  Outputs stay within the bound, the
+    placement check stays clear (the error word is zero), and the other stream is still
+    busy when each decode has finished."""
+    from heterokv import ops
+    print("case: decode beside a concurrent GEMM stream, B=1 32/8, 64 + 8000 + 1000", flush=True)
+    c = Case(16, 1, 32, 8, 64, [8000], [1000])
+    ref = c.oracle()
+    ws = ops.DecodeWorkspace(DEV)
+    side = torch.cuda.Stream(device=DEV)          # default priority
+    a = torch.randn(8192, 8192, device=DEV, dtype=torch.bfloat16) / 90
+    b = torch.randn(8192, 8192, device=DEV, dtype=torch.bfloat16) / 90
+    o = torch.empty_like(a)
+    q, bt = c.q.to(DEV), c.bt.to(DEV)
+    torch.cuda.synchronize()
+    main = torch.cuda.current_stream(DEV)
+    overlapped = 0
+    for i in range(5):
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                torch.matmul(a, b, out=o)
+        side_done = torch.cuda.Event()
+        side_done.record(side)
+        out = ops.decode_attention(q, zones=c.zones, pool=c.pool, block_table=bt, int4_max_len=c.maxmid,
+                                   workspace=ws)
+        done = torch.cuda.Event()
+        done.record(main)
+        done.synchronize()
+        overlapped += int(not side_done.query())
+        err = np.abs(out.float().cpu().numpy() - ref).max()
+        print("  launch %d: max abs err %.3e" % (i, err), flush=True)
+        assert err <= TOL
+        assert ws.error_flag() == 0
+    torch.cuda.synchronize()
+    assert overlapped >= 1
+
+
 def test_schedules_agree_on_long_windows():
     """Ranges longer than one block-id window (1024 INT4 blocks) restage the ids
     between windows: one range per pair (splits=1) over 40000 INT4 tokens = 2500
