@@ -73,8 +73,13 @@ constexpr int kPrefetch = HKV_DECODE_PREFETCH;  // INT4 block pairs in flight pe
 #endif
 constexpr int kF16Depth = HKV_DECODE_F16_DEPTH;
 constexpr int kMaxSplits = 64;
-constexpr int kArrivedMask = 0xffff;     // slice merge: arrivals in the low bits of the pair's ticket
-constexpr int kGoneBit = 1 << 30;        // slice merge: a range stopped waiting
+// Slice merge: the pair's arrival word holds the arrivals of the current launch in bits
+// 0-15, a generation in bits 16-29 that the last arrival advances (clearing the count),
+// and a bit set by a range that stopped waiting.
+constexpr int kArrivedMask = 0xffff;
+constexpr int kGenOne = 1 << 16;
+constexpr int kGenMask = 0x3fff << 16;
+constexpr int kGoneBit = 1 << 30;
 // Bound of a range's wait in the slice merge: 25 us of the 100 MHz constant clock.  Waits
 // on the 32K decode are under ~4 us; a wait that runs out only hands the whole merge to
 // the last arrival (~3 us), and a short bound limits what two decodes running at once on
@@ -158,7 +163,7 @@ struct DecodeParams {
     int* err;
     int* counters;            // agent-scope tickets, one int per pair
     unsigned* owners;         // agent-scope XCD masks, one per pair (placement check)
-    int* counters_l2;         // XCD-local tickets, one 256-byte line per pair
+    int* counters_l2;         // XCD-local words, one 256-byte line per pair: [0] slice-merge arrivals, [1] ticket
     float* partials;
     int max_splits;
     int64_t part_pair_stride;  // floats between the partial blocks of consecutive pairs (256-byte multiple)
@@ -905,18 +910,26 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         // states, so that the end of the kernel is one small load round trip after the
         // last arrival instead of one workgroup loading every state.  A range whose wait
         // runs out sets kGoneBit and leaves; the last arrival, seeing it, merges every
-        // slice (the same code, so a slice written twice gets the same bits).  A second
-        // count (done) tells the last workgroup to leave the pair's words that it may
-        // reset them: every range has made its last access to the arrival count by then.
+        // slice (the same code, so a slice written twice gets the same bits).  The last
+        // arrival also resets the pair's words at once: it advances the generation and
+        // clears the count in one store, so a range still waiting sees the launch
+        // complete either way (count full, or generation moved on), and no range needs
+        // another round trip to the word before its slice.
         __shared__ int sm_slices;   // 0: none, 1: this range's slice, 2: every slice
         if (threadIdx.x == 0) {
             int* const arrived = &p.counters_l2[bh * 64];
-            int* const done = &p.counters_l2[bh * 64 + 1];
             const int old = __hip_atomic_fetch_add(arrived, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            bool bad = (owner_old & ~owner_bit) != 0u || (old & kArrivedMask) >= nsplit;
+            const int gen = old & kGenMask;
+            // a count at or past the range count is what a launch whose ranges did not
+            // share one L2 leaves behind: reported, and the word starts a new generation
+            const bool overrun = (old & kArrivedMask) >= nsplit;
+            const bool bad = (owner_old & ~owner_bit) != 0u || overrun;
             int slices;
-            if ((old & kArrivedMask) == nsplit - 1) {
+            if ((old & kArrivedMask) == nsplit - 1 || overrun) {
                 slices = (old & kGoneBit) ? 2 : 1;
+                // every range has arrived, so every mask update is done
+                __hip_atomic_store(arrived, (gen + kGenOne) & kGenMask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_store(&p.owners[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 slices = 0;
                 const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
@@ -927,13 +940,23 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                     int zero;
                     asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
                     int v = __hip_atomic_fetch_or(arrived, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    if ((v & kArrivedMask) >= nsplit) {
+                    if ((v & kGenMask) != gen || (v & kArrivedMask) >= nsplit) {
                         slices = 1;
                         break;
                     }
                     if (__builtin_amdgcn_s_memrealtime() - t0 > p.merge_wait) {
-                        v = __hip_atomic_fetch_or(arrived, kGoneBit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                        slices = (v & kArrivedMask) >= nsplit ? 1 : 0;
+                        // stop waiting: set kGoneBit in this generation's word while its
+                        // count is short (then the last arrival sees it), unless the count
+                        // completed meanwhile
+                        for (;;) {
+                            if ((v & kGenMask) != gen || (v & kArrivedMask) >= nsplit) {
+                                slices = 1;
+                                break;
+                            }
+                            if (__hip_atomic_compare_exchange_strong(arrived, &v, v | kGoneBit, __ATOMIC_RELAXED,
+                                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
+                                break;
+                        }
                         break;
                     }
                     __builtin_amdgcn_s_sleep(2);
@@ -941,12 +964,6 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             }
             if (bad && p.err)
                 __hip_atomic_fetch_or(p.err, HKV_ERR_BIT_PLACEMENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            // this workgroup's last access to the arrival count is done
-            if (__hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == nsplit - 1) {
-                __hip_atomic_store(arrived, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                __hip_atomic_store(done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                __hip_atomic_store(&p.owners[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
             sm_slices = slices;
         }
         __syncthreads();
@@ -1030,7 +1047,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         // the stores above have completed (in L2, or in memory for sc1 stores)
         int tk;
         if (p.xcc_local)
-            tk = __hip_atomic_fetch_add(&p.counters_l2[bh * 64], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            tk = __hip_atomic_fetch_add(&p.counters_l2[bh * 64 + 1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         else
             tk = __hip_atomic_fetch_add(&p.counters[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // another XCD's bit in the mask: this pair's ranges did not share one L2.  A
@@ -1039,7 +1056,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         const bool foreign = (owner_old & ~owner_bit) != 0u;
         if (tk >= nsplit) {
             if (p.xcc_local)
-                __hip_atomic_store(&p.counters_l2[bh * 64], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_store(&p.counters_l2[bh * 64 + 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             else
                 __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -1137,7 +1154,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     // the pair has taken its ticket, so its mask update is done
     if (threadIdx.x == 0) {
         if (p.xcc_local) {
-            __hip_atomic_store(&p.counters_l2[bh * 64], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store(&p.counters_l2[bh * 64 + 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             __hip_atomic_store(&p.owners[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
             __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
