@@ -73,6 +73,7 @@ constexpr int kPrefetch = HKV_DECODE_PREFETCH;  // INT4 block pairs in flight pe
 #endif
 constexpr int kF16Depth = HKV_DECODE_F16_DEPTH;
 constexpr int kMaxSplits = 64;
+constexpr int kLineWords = 64;           // ints per 256-byte hand-off line
 // Slice merge: the pair's arrival word holds the arrivals of the current launch in bits
 // 0-15, a generation in bits 16-29 that the last arrival advances (clearing the count),
 // and a bit set by a range that stopped waiting.
@@ -161,9 +162,11 @@ struct DecodeParams {
     uint16_t* out;
     int64_t o_sb, o_sh;
     int* err;
-    int* counters;            // agent-scope tickets, one int per pair
-    unsigned* owners;         // agent-scope XCD masks, one per pair (placement check)
-    int* counters_l2;         // XCD-local words, one 256-byte line per pair: [0] slice-merge arrivals, [1] ticket
+    // Hand-off words, one 256-byte line (kLineWords ints) per pair and kind, so that the
+    // atomics of different pairs do not queue at one cache line:
+    int* counters;            // agent-scope ticket: word 0 of the pair's agent line
+    unsigned* owners;         // agent-scope XCD mask (placement check): word 1 of the same line
+    int* counters_l2;         // XCD-local line: [0] slice-merge arrivals, [1] ticket
     float* partials;
     int max_splits;
     int64_t part_pair_stride;  // floats between the partial blocks of consecutive pairs (256-byte multiple)
@@ -830,7 +833,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     // later OR returns the other's bit, so a split placement is always reported.
     if (p.xcc_local && threadIdx.x == 0) {
         owner_bit = 1u << (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
-        owner_old = __hip_atomic_fetch_or(&p.owners[bh], owner_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        owner_old = __hip_atomic_fetch_or(&p.owners[bh * kLineWords], owner_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // ---- merge the waves of this workgroup through LDS
@@ -917,7 +920,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         // another round trip to the word before its slice.
         __shared__ int sm_slices;   // 0: none, 1: this range's slice, 2: every slice
         if (threadIdx.x == 0) {
-            int* const arrived = &p.counters_l2[bh * 64];
+            int* const arrived = &p.counters_l2[bh * kLineWords];
             const int old = __hip_atomic_fetch_add(arrived, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             const int gen = old & kGenMask;
             // a count at or past the range count is what a launch whose ranges did not
@@ -929,7 +932,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                 slices = (old & kGoneBit) ? 2 : 1;
                 // every range has arrived, so every mask update is done
                 __hip_atomic_store(arrived, (gen + kGenOne) & kGenMask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                __hip_atomic_store(&p.owners[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&p.owners[bh * kLineWords], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 slices = 0;
                 const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
@@ -1047,18 +1050,18 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         // the stores above have completed (in L2, or in memory for sc1 stores)
         int tk;
         if (p.xcc_local)
-            tk = __hip_atomic_fetch_add(&p.counters_l2[bh * 64 + 1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            tk = __hip_atomic_fetch_add(&p.counters_l2[bh * kLineWords + 1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         else
-            tk = __hip_atomic_fetch_add(&p.counters[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            tk = __hip_atomic_fetch_add(&p.counters[bh * kLineWords], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // another XCD's bit in the mask: this pair's ranges did not share one L2.  A
         // ticket beyond the range count is what such a launch leaves behind; it is
         // reset so that later launches count from zero again.
         const bool foreign = (owner_old & ~owner_bit) != 0u;
         if (tk >= nsplit) {
             if (p.xcc_local)
-                __hip_atomic_store(&p.counters_l2[bh * 64 + 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_store(&p.counters_l2[bh * kLineWords + 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             else
-                __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&p.counters[bh * kLineWords], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         if ((foreign || tk >= nsplit) && p.err)
             __hip_atomic_fetch_or(p.err, HKV_ERR_BIT_PLACEMENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1154,10 +1157,10 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     // the pair has taken its ticket, so its mask update is done
     if (threadIdx.x == 0) {
         if (p.xcc_local) {
-            __hip_atomic_store(&p.counters_l2[bh * 64 + 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            __hip_atomic_store(&p.owners[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&p.counters_l2[bh * kLineWords + 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store(&p.owners[bh * kLineWords], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
-            __hip_atomic_store(&p.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&p.counters[bh * kLineWords], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -1198,8 +1201,10 @@ int choose_splits(int BH, int int4_max_len, const int32_t* f16_max_lens, int nz,
     return (int)s;
 }
 
-// Workspace: [header (error word) | agent tickets | XCD masks | XCD-local tickets
+// Workspace: [header (error word) | agent lines (ticket, XCD mask) | XCD-local lines
 // (256 B each) | partial states, one 256-byte aligned block per (sequence, kv head)].
+// One line per pair: packed one word per pair, the 256 atomics of a 32K decode's 8 pairs
+// went to one cache line and queued there (the placement check then cost ~0.6 us per launch).
 // The ticket area holds kHandoffPairs slots of each kind at fixed offsets, whatever the
 // launch geometry, so the partial states of one launch never overlap the tickets of
 // another launch on the same workspace: the kernels leave every ticket at zero, and a
@@ -1210,7 +1215,7 @@ constexpr int64_t kHandoffPairs = 1024;
 
 size_t pair_part_bytes(int nrep, int nsplit) { return align256((size_t)nsplit * nrep * kPartStride * sizeof(float)); }
 
-constexpr size_t kTicketAreaEnd = kWsHeader + 2 * kHandoffPairs * sizeof(int) + kHandoffPairs * 256;
+constexpr size_t kTicketAreaEnd = kWsHeader + 2 * kHandoffPairs * 256;
 static_assert(kTicketAreaEnd % 256 == 0, "partial states start 256-byte aligned");
 
 size_t workspace_bytes(int B, int Hq, int Hkv, int nsplit) {
@@ -1378,8 +1383,8 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
     char* ws = (char*)wsp;
     p.err = a->err_flag ? (int*)a->err_flag : (int*)ws;
     p.counters = (int*)(ws + kWsHeader);
-    p.owners = (unsigned*)(ws + kWsHeader + kHandoffPairs * sizeof(int));
-    p.counters_l2 = (int*)(ws + kWsHeader + 2 * kHandoffPairs * sizeof(int));
+    p.owners = (unsigned*)(ws + kWsHeader) + 1;
+    p.counters_l2 = (int*)(ws + kWsHeader + kHandoffPairs * 256);
     p.partials = (float*)(ws + kTicketAreaEnd);
     p.part_pair_stride = (int64_t)(pair_part_bytes(nrep, ms) / sizeof(float));
     p.nxcc = num_xcc();

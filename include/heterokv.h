@@ -336,8 +336,8 @@ typedef struct HkvDecodeArgs {
 
 /* Workspace rules.  The workspace must be zero-filled before its first use.  Its
  * ticket area sits at fixed offsets for up to 1024 split (sequence, kv head) pairs,
- * whatever the launch geometry, and the kernels leave every ticket zero after a
- * launch, so one workspace serves launches of any geometry in any order (graph replays
+ * whatever the launch geometry, and the kernels leave every ticket at a zero count after
+ * a launch, so one workspace serves launches of any geometry in any order (graph replays
  * included) with no clearing in between.  A launch that splits more than 1024 pairs
  * (possible only with splits_hint) fails with HKV_ERR_CAPACITY.  Launches that share a
  * workspace must be ordered on one stream. */

@@ -111,10 +111,10 @@ def test_decode_argument_errors(lib):
 def test_workspace_size(lib):
     from heterokv import ops
     n = ops.decode_workspace_bytes(1, 32, 8, 28608, [64, 4096])
-    # header + a fixed ticket area for 1024 pairs (agent tickets, XCD masks, one 256-byte
-    # XCD-local ticket each) + partial states for up to 64 ranges per (sequence, kv head):
-    # 8 pairs x 64 ranges x 4 heads x 132 floats
-    assert n == 256 + 1024 * 4 + 1024 * 4 + 1024 * 256 + 8 * 64 * 4 * 132 * 4
+    # header + a fixed ticket area for 1024 pairs (one 256-byte agent line with the ticket
+    # and the XCD mask, one 256-byte XCD-local line each) + partial states for up to 64
+    # ranges per (sequence, kv head): 8 pairs x 64 ranges x 4 heads x 132 floats
+    assert n == 256 + 1024 * 256 + 1024 * 256 + 8 * 64 * 4 * 132 * 4
     # the ticket area does not move with the geometry
     n2 = ops.decode_workspace_bytes(4, 32, 8, 28608, [64, 4096])
     assert n2 - n == 24 * 64 * 4 * 132 * 4
