@@ -173,6 +173,7 @@ struct DecodeParams {
     int xcc_local;             // 1: all ranges of a pair run on one XCD (see above)
     int nxcc;                  // XCDs the dispatcher round-robins over
     int coop;                  // 1: slice merge by every range of a pair (see the kernel's tail)
+    int slice_outputs;         // slice merge: outputs per slice, ceil(n_rep * 128 / ranges)
     unsigned long long merge_wait;   // slice merge: constant-clock ticks a range waits for the others
     // optional score output (kScores): row (b, q head) holds the log2-domain score of
     // every item [INT4 tokens | zone 0 | zone 1 | zone 2]; zone z starts at sc_zone[z]
@@ -831,14 +832,25 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     // 32K decode: the pair's 32 atomics serialize on one address, and loads issued after
     // one complete after it.)  Of any two workgroups of a pair on different XCDs, the
     // later OR returns the other's bit, so a split placement is always reported.
+    // The last refills (zero-sized past the range's end) complete first, so that the OR
+    // below is the one load in flight when the merge starts: with refills still pending on
+    // the path that skips the OR, the compiler waited for all loads, the OR included,
+    // before the first shuffle of the merge.
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     if (p.xcc_local && threadIdx.x == 0) {
         owner_bit = 1u << (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
         owner_old = __hip_atomic_fetch_or(&p.owners[bh * kLineWords], owner_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // ---- merge the waves of this workgroup through LDS
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    // the row sum over the four 16-lane rows, by lane swaps (the operands of each add are
+    // the same on both lanes of a swapped pair, so every lane gets the same bits)
+    {
+        const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+        l = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+        const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+        l = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+    }
     extern __shared__ float smem[];
     float* sm_o = smem;                                   // [kWaves][nrep][128]
     float* sm_m = sm_o + kWaves * nrep * kHeadDim;        // [kWaves][nrep]
@@ -858,7 +870,14 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     __syncthreads();
 
     const int nout = nrep * kHeadDim;
-    float* part = p.partials + (int64_t)bh * p.part_pair_stride + (int64_t)split * (nrep * kPartStride);
+    // the pair's partial states, computed once and held in registers (opaque to the
+    // compiler, which would otherwise read the arguments again after the arrival wait)
+    float* parts = p.partials + (int64_t)bh * p.part_pair_stride;
+    uint16_t* obase = p.out + (int64_t)b * p.o_sb + (int64_t)(h * nrep) * p.o_sh;   // this kv head's outputs
+    int64_t osh = p.o_sh;
+    int obf16 = p.out_bf16, slice_outputs = p.slice_outputs;
+    asm volatile("" : "+s"(parts), "+s"(obase), "+s"(osh), "+s"(obf16), "+s"(slice_outputs));
+    float* part = parts + (int64_t)split * (nrep * kPartStride);
     for (int idx = threadIdx.x; idx < nout; idx += kThreads) {
         const int hd = idx >> 7, d = idx & (kHeadDim - 1);
         float M = -INFINITY;
@@ -874,7 +893,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         }
         if (nsplit == 1) {
             const float r = L > 0.f ? O / L : 0.f;
-            p.out[(int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d] = p.out_bf16 ? f2bf_rn(r) : f2h_rn(r);
+            obase[(int64_t)hd * osh + d] = obf16 ? f2bf_rn(r) : f2h_rn(r);
             if (kScores && d == 0) {
                 float* st = p.stats + ((int64_t)b * p.Hkv * nrep + h * nrep + hd) * 2;
                 st[0] = M;
@@ -978,10 +997,9 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         }
         // slice sl = outputs [sl S, sl S + S) of the pair's nout (head-major: head, dim);
         // 4 threads per output, thread q of an output taking splits q, q + 4, ...
-        const float* parts = p.partials + (int64_t)bh * p.part_pair_stride;
         const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)parts, 0, (int)(nsplit * nrep * kPartStride * sizeof(float)), 0x00020000);
-        const int S = (nout + nsplit - 1) / nsplit;
+        const int S = slice_outputs;
         const int sl0 = slices == 2 ? 0 : split, sl1 = slices == 2 ? nsplit : split + 1;
         for (int sl = sl0; sl < sl1; ++sl) {
             for (int t = threadIdx.x; t < 4 * S; t += kThreads) {
@@ -1032,7 +1050,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                 }
                 if (live && q == 0) {
                     const float r = L > 0.f ? O / L : 0.f;
-                    p.out[(int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d] = p.out_bf16 ? f2bf_rn(r) : f2h_rn(r);
+                    obase[(int64_t)hd * osh + d] = obf16 ? f2bf_rn(r) : f2h_rn(r);
                     if (kScores && d == 0) {
                         float* st = p.stats + ((int64_t)b * p.Hkv * nrep + h * nrep + hd) * 2;
                         st[0] = M;
@@ -1079,7 +1097,6 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     // memory round trip.  Thread t owns float4 `u` of one head and the splits
     // s = k, k + K, k + 2K, ... (K = threads per unit); all its loads are
     // independent.  The K per-thread states then merge through LDS.
-    const float* parts = p.partials + (int64_t)bh * p.part_pair_stride;
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)parts, 0, (int)(nsplit * nrep * kPartStride * sizeof(float)), 0x00020000);
     const int units = nrep * (kHeadDim / 4);
@@ -1142,9 +1159,9 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
             O += f4{w[2], w[3], w[4], w[5]} * e;
         }
         const float inv = L > 0.f ? 1.0f / L : 0.f;
-        uint16_t* op = p.out + (int64_t)b * p.o_sb + (int64_t)(h * nrep + hd) * p.o_sh + d4;
+        uint16_t* op = obase + (int64_t)hd * osh + d4;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) op[v] = p.out_bf16 ? f2bf_rn(O[v] * inv) : f2h_rn(O[v] * inv);
+        for (int v = 0; v < 4; ++v) op[v] = obf16 ? f2bf_rn(O[v] * inv) : f2h_rn(O[v] * inv);
         if (kScores && d4 == 0) {
             float* st = p.stats + ((int64_t)b * p.Hkv * nrep + h * nrep + hd) * 2;
             st[0] = M;
@@ -1402,6 +1419,7 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
         const int S = (nout + ms - 1) / ms;
         p.coop = (p.xcc_local && (int64_t)BH * ms <= num_cus() &&
                   S <= 128 && ms < kArrivedMask) ? 1 : 0;
+        p.slice_outputs = S;
         const char* mw = getenv("HKV_DECODE_MERGE_WAIT_TICKS");
         p.merge_wait = (mw && mw[0]) ? strtoull(mw, nullptr, 10) : kMergeWaitTicks;
     }
