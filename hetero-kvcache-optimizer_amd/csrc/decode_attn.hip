@@ -25,9 +25,10 @@
 // LDS, workgroups through a workspace: the last workgroup of a pair to finish
 // (atomic ticket after a release fence) merges the S partial states with
 // independent loads and writes the output, so the whole op is one launch.  When every
-// range of a pair is resident (the grid fits the CUs) with the XCD-local hand-off, each
-// range instead waits (bounded) for the pair's arrival count and merges one slice of
-// the output (the kernel's tail describes both).
+// range of a pair is resident (the grid fits the CUs), each range instead waits
+// (bounded) for the pair's arrival count and merges one slice of the output, in the
+// XCD's L2 with the XCD-local hand-off and through memory otherwise (the kernel's tail
+// describes both).
 // Workgroup ids interleave the pairs so that all ranges of a pair land on one
 // XCD: dispatch is round-robin over XCDs by workgroup id (the XCD that takes
 // workgroup 0 rotates from launch to launch, so only the id modulo the XCD count
@@ -211,6 +212,66 @@ __device__ __forceinline__ f4 ld_l2_f4(__amdgpu_buffer_rsrc_t r, int byte_off) {
 }
 __device__ __forceinline__ f2 ld_l2_f2(__amdgpu_buffer_rsrc_t r, int byte_off) {
     return __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 1));
+}
+// The same loads at device scope (sc1: coherent with other XCDs' device-scope stores).
+constexpr int kAuxL2 = 1, kAuxDevice = 16;
+
+// Slice merge: the (m, l) pair and output d of eight partial states (splits q + base,
+// q + base + 4, ...), with loads of cache policy kAux.
+template <int kAux>
+__device__ __forceinline__ void load_slice8(__amdgpu_buffer_rsrc_t prs, int q, int base, int nsplit, int nrep, int hd,
+                                            int d, float (&ms)[8], float (&ls)[8], float (&os)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int sj = q + base + 4 * j;
+        const int off = min(sj, nsplit - 1) * (nrep * kPartStride) + hd * kPartStride;
+        const f2 ml = __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(prs, (off + kHeadDim) * 4, 0, kAux));
+        ms[j] = sj < nsplit ? ml.x : -INFINITY;
+        ls[j] = ml.y;
+        os[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, (off + d) * 4, 0, kAux));
+    }
+}
+
+// Slice merge: a range's arrival (one thread), with atomics of scope kScope on the pair's
+// arrival word.  Returns 0 (the wait ran out: leave), 1 (merge this range's slice) or 2
+// (merge every slice: the last arrival, after some range stopped waiting).  The last
+// arrival resets the word at once (generation advanced, count cleared, one store) and
+// clears `mask` (the placement check's, or null); *overrun reports a count at or past the
+// range count at arrival.
+template <int kScope>
+__device__ __forceinline__ int slice_arrival(int* arrived, int nsplit, unsigned long long merge_wait,
+                                             unsigned* mask, bool* overrun) {
+    const int old = __hip_atomic_fetch_add(arrived, 1, __ATOMIC_RELAXED, kScope);
+    const int gen = old & kGenMask;
+    // a count at or past the range count is what a launch whose ranges did not share one
+    // L2 leaves behind: reported, and the word starts a new generation
+    *overrun = (old & kArrivedMask) >= nsplit;
+    if ((old & kArrivedMask) == nsplit - 1 || *overrun) {
+        __hip_atomic_store(arrived, (gen + kGenOne) & kGenMask, __ATOMIC_RELAXED, kScope);
+        // every range has arrived, so every mask update is done
+        if (mask) __hip_atomic_store(mask, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return (old & kGoneBit) ? 2 : 1;
+    }
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+        // an OR of zero, performed where the others' arrivals are (a load could be served
+        // from this CU's L1); the zero is opaque so that the compiler keeps the atomic
+        int zero;
+        asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+        int v = __hip_atomic_fetch_or(arrived, zero, __ATOMIC_RELAXED, kScope);
+        if ((v & kGenMask) != gen || (v & kArrivedMask) >= nsplit) return 1;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > merge_wait) {
+            // stop waiting: set kGoneBit in this generation's word while its count is
+            // short (then the last arrival sees it), unless the count completed meanwhile
+            for (;;) {
+                if ((v & kGenMask) != gen || (v & kArrivedMask) >= nsplit) return 1;
+                if (__hip_atomic_compare_exchange_strong(arrived, &v, v | kGoneBit, __ATOMIC_RELAXED,
+                                                         __ATOMIC_RELAXED, kScope))
+                    return 0;
+            }
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
 }
 
 __device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
@@ -588,7 +649,9 @@ __device__ __forceinline__ void load_partials(__amdgpu_buffer_rsrc_t prs, const 
     }
 }
 
-template <bool kDynamic, bool kScores>
+// kL2: the XCD-local hand-off (p.xcc_local), a template parameter so that each hand-off's
+// kernel carries only its own tail code.
+template <bool kDynamic, bool kScores, bool kL2>
 __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     touch_kernel_args(p);   // the range plan below reads the arguments in a dependent chain
     const int BH = p.B * p.Hkv;
@@ -837,7 +900,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     // the path that skips the OR, the compiler waited for all loads, the OR included,
     // before the first shuffle of the merge.
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-    if (p.xcc_local && threadIdx.x == 0) {
+    if (kL2 && threadIdx.x == 0) {
         owner_bit = 1u << (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
         owner_old = __hip_atomic_fetch_or(&p.owners[bh * kLineWords], owner_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -899,7 +962,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                 st[0] = M;
                 st[1] = L;
             }
-        } else if (p.xcc_local) {
+        } else if (kL2) {
             part[hd * kPartStride + d] = O;
             if (d == 0) {
                 part[hd * kPartStride + kHeadDim] = M;
@@ -926,7 +989,8 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
     if (p.coop) {
-        // ---- slice merge (XCD-local hand-off, every range of the pair resident).  Each
+        // ---- slice merge (every range of the pair resident; atomics and loads in the
+        // XCD's L2 with the XCD-local hand-off, at device scope otherwise).  Each
         // range adds itself to the pair's arrival count, waits until the count is complete
         // (bounded), then merges one slice of the pair's output from all nsplit partial
         // states, so that the end of the kernel is one small load round trip after the
@@ -939,51 +1003,14 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         // another round trip to the word before its slice.
         __shared__ int sm_slices;   // 0: none, 1: this range's slice, 2: every slice
         if (threadIdx.x == 0) {
-            int* const arrived = &p.counters_l2[bh * kLineWords];
-            const int old = __hip_atomic_fetch_add(arrived, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            const int gen = old & kGenMask;
-            // a count at or past the range count is what a launch whose ranges did not
-            // share one L2 leaves behind: reported, and the word starts a new generation
-            const bool overrun = (old & kArrivedMask) >= nsplit;
+            bool overrun;
+            const int slices =
+                kL2
+                    ? slice_arrival<__HIP_MEMORY_SCOPE_WORKGROUP>(&p.counters_l2[bh * kLineWords], nsplit, p.merge_wait,
+                                                                  &p.owners[bh * kLineWords], &overrun)
+                    : slice_arrival<__HIP_MEMORY_SCOPE_AGENT>(&p.counters[bh * kLineWords + 2], nsplit, p.merge_wait,
+                                                              nullptr, &overrun);
             const bool bad = (owner_old & ~owner_bit) != 0u || overrun;
-            int slices;
-            if ((old & kArrivedMask) == nsplit - 1 || overrun) {
-                slices = (old & kGoneBit) ? 2 : 1;
-                // every range has arrived, so every mask update is done
-                __hip_atomic_store(arrived, (gen + kGenOne) & kGenMask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                __hip_atomic_store(&p.owners[bh * kLineWords], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else {
-                slices = 0;
-                const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-                for (;;) {
-                    // an OR of zero, performed at the L2 like the others' arrivals (a load
-                    // could be served from this CU's L1); the zero is opaque so that the
-                    // compiler keeps the atomic
-                    int zero;
-                    asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
-                    int v = __hip_atomic_fetch_or(arrived, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    if ((v & kGenMask) != gen || (v & kArrivedMask) >= nsplit) {
-                        slices = 1;
-                        break;
-                    }
-                    if (__builtin_amdgcn_s_memrealtime() - t0 > p.merge_wait) {
-                        // stop waiting: set kGoneBit in this generation's word while its
-                        // count is short (then the last arrival sees it), unless the count
-                        // completed meanwhile
-                        for (;;) {
-                            if ((v & kGenMask) != gen || (v & kArrivedMask) >= nsplit) {
-                                slices = 1;
-                                break;
-                            }
-                            if (__hip_atomic_compare_exchange_strong(arrived, &v, v | kGoneBit, __ATOMIC_RELAXED,
-                                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
-                                break;
-                        }
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(2);
-                }
-            }
             if (bad && p.err)
                 __hip_atomic_fetch_or(p.err, HKV_ERR_BIT_PLACEMENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             sm_slices = slices;
@@ -1009,15 +1036,10 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
                 float M = -INFINITY, L = 0.f, O = 0.f;
                 for (int base = 0; q + base < nsplit; base += 32) {
                     float ms[8], ls[8], os[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int sj = q + base + 4 * j;
-                        const int off = min(sj, nsplit - 1) * (nrep * kPartStride) + hd * kPartStride;
-                        const f2 ml = ld_l2_f2(prs, (off + kHeadDim) * 4);
-                        ms[j] = sj < nsplit ? ml.x : -INFINITY;
-                        ls[j] = ml.y;
-                        os[j] = ld_l2(prs, (off + d) * 4);
-                    }
+                    if (kL2)
+                        load_slice8<kAuxL2>(prs, q, base, nsplit, nrep, hd, d, ms, ls, os);
+                    else
+                        load_slice8<kAuxDevice>(prs, q, base, nsplit, nrep, hd, d, ms, ls, os);
                     float Mc = ms[0];
 #pragma unroll
                     for (int j = 1; j < 8; ++j) Mc = fmaxf(Mc, ms[j]);
@@ -1067,7 +1089,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     if (threadIdx.x == 0) {
         // the stores above have completed (in L2, or in memory for sc1 stores)
         int tk;
-        if (p.xcc_local)
+        if (kL2)
             tk = __hip_atomic_fetch_add(&p.counters_l2[bh * kLineWords + 1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         else
             tk = __hip_atomic_fetch_add(&p.counters[bh * kLineWords], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1076,7 +1098,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         // reset so that later launches count from zero again.
         const bool foreign = (owner_old & ~owner_bit) != 0u;
         if (tk >= nsplit) {
-            if (p.xcc_local)
+            if (kL2)
                 __hip_atomic_store(&p.counters_l2[bh * kLineWords + 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             else
                 __hip_atomic_store(&p.counters[bh * kLineWords], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1110,7 +1132,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
         for (int s0 = k; s0 < nsplit; s0 += 8 * K) {
             float ms[8], ls[8];
             f4 os[8];
-            if (p.xcc_local)
+            if (kL2)
                 load_partials<true>(prs, parts, s0, K, nsplit, nrep, hd, d4, ms, ls, os);
             else
                 load_partials<false>(prs, parts, s0, K, nsplit, nrep, hd, d4, ms, ls, os);
@@ -1173,7 +1195,7 @@ __global__ __launch_bounds__(kThreads) void decode_attn_kernel(DecodeParams p) {
     // last in the kernel, so that no barrier waits for these stores: every workgroup of
     // the pair has taken its ticket, so its mask update is done
     if (threadIdx.x == 0) {
-        if (p.xcc_local) {
+        if (kL2) {
             __hip_atomic_store(&p.counters_l2[bh * kLineWords + 1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             __hip_atomic_store(&p.owners[bh * kLineWords], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
@@ -1410,15 +1432,16 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
     p.max_splits = ms;
     {
         // slice merge: every range of a pair must be resident while it waits for the
-        // others (one 8-wave workgroup per CU: the grid fits the CUs), with the XCD-local
-        // hand-off; a slice has at most 128 outputs (4 threads each).  Each output is
+        // others (one 8-wave workgroup per CU: the grid fits the CUs); a slice has at most
+        // 128 outputs (4 threads each).  With the XCD-local hand-off it runs in the XCD's
+        // L2, otherwise through memory with device-scope accesses (a pair's ranges then
+        // span XCDs, as with 4 kv heads on 8 XCDs).  Each output is
         // merged by one quad in a fixed split order, so the deterministic schedule keeps
         // bitwise reproducible outputs with it.  HKV_DECODE_MERGE_WAIT_TICKS shortens the bounded wait (tests force the
         // path where ranges stop waiting and the last arrival merges every slice).
         const int nout = nrep * kHeadDim;
         const int S = (nout + ms - 1) / ms;
-        p.coop = (p.xcc_local && (int64_t)BH * ms <= num_cus() &&
-                  S <= 128 && ms < kArrivedMask) ? 1 : 0;
+        p.coop = (ms > 1 && (int64_t)BH * ms <= num_cus() && S <= 128 && ms < kArrivedMask) ? 1 : 0;
         p.slice_outputs = S;
         const char* mw = getenv("HKV_DECODE_MERGE_WAIT_TICKS");
         p.merge_wait = (mw && mw[0]) ? strtoull(mw, nullptr, 10) : kMergeWaitTicks;
@@ -1450,20 +1473,26 @@ static int decode_launch(const HkvDecodeArgs* a, void* wsp, size_t ws_bytes, voi
     const size_t lds = lds_bytes(nrep);
     const bool det = (a->flags & HKV_DECODE_DETERMINISTIC) != 0;
     const bool sc = a->scores != nullptr;
-    const int var = (det ? 0 : 1) + (sc ? 2 : 0);
-    static const void* const fns[4] = {(const void*)decode_attn_kernel<false, false>,
-                                       (const void*)decode_attn_kernel<true, false>,
-                                       (const void*)decode_attn_kernel<false, true>,
-                                       (const void*)decode_attn_kernel<true, true>};
-    static std::atomic<uint64_t> raised[4];   // the merge area plus the static id window can exceed 64 KB
+    const int var = (det ? 0 : 1) + (sc ? 2 : 0) + (p.xcc_local ? 4 : 0);
+#define HKV_DECODE_FN(v) decode_attn_kernel<((v) & 1) != 0, ((v) & 2) != 0, ((v) & 4) != 0>
+    static const void* const fns[8] = {(const void*)HKV_DECODE_FN(0), (const void*)HKV_DECODE_FN(1),
+                                       (const void*)HKV_DECODE_FN(2), (const void*)HKV_DECODE_FN(3),
+                                       (const void*)HKV_DECODE_FN(4), (const void*)HKV_DECODE_FN(5),
+                                       (const void*)HKV_DECODE_FN(6), (const void*)HKV_DECODE_FN(7)};
+    static std::atomic<uint64_t> raised[8];   // the merge area plus the static id window can exceed 64 KB
     HKV_RAISE_LDS(fns[var], 96 * 1024, raised[var]);
     const dim3 grid((unsigned)(BH * ms)), block(kThreads);
     switch (var) {
-        case 0: hipLaunchKernelGGL((decode_attn_kernel<false, false>), grid, block, lds, (hipStream_t)stream, p); break;
-        case 1: hipLaunchKernelGGL((decode_attn_kernel<true, false>), grid, block, lds, (hipStream_t)stream, p); break;
-        case 2: hipLaunchKernelGGL((decode_attn_kernel<false, true>), grid, block, lds, (hipStream_t)stream, p); break;
-        default: hipLaunchKernelGGL((decode_attn_kernel<true, true>), grid, block, lds, (hipStream_t)stream, p); break;
+        case 0: hipLaunchKernelGGL((HKV_DECODE_FN(0)), grid, block, lds, (hipStream_t)stream, p); break;
+        case 1: hipLaunchKernelGGL((HKV_DECODE_FN(1)), grid, block, lds, (hipStream_t)stream, p); break;
+        case 2: hipLaunchKernelGGL((HKV_DECODE_FN(2)), grid, block, lds, (hipStream_t)stream, p); break;
+        case 3: hipLaunchKernelGGL((HKV_DECODE_FN(3)), grid, block, lds, (hipStream_t)stream, p); break;
+        case 4: hipLaunchKernelGGL((HKV_DECODE_FN(4)), grid, block, lds, (hipStream_t)stream, p); break;
+        case 5: hipLaunchKernelGGL((HKV_DECODE_FN(5)), grid, block, lds, (hipStream_t)stream, p); break;
+        case 6: hipLaunchKernelGGL((HKV_DECODE_FN(6)), grid, block, lds, (hipStream_t)stream, p); break;
+        default: hipLaunchKernelGGL((HKV_DECODE_FN(7)), grid, block, lds, (hipStream_t)stream, p); break;
     }
+#undef HKV_DECODE_FN
     HKV_LAUNCH_CHECK("decode_attn_kernel");
     return HKV_OK;
 }

@@ -175,19 +175,24 @@ def test_deterministic_bitwise():
     assert ws.error_flag() == 0
 
 
+@pytest.mark.parametrize("hq,hkv,handoff", [(32, 8, False), (32, 8, True), (28, 4, False)])
 @pytest.mark.parametrize("splits", [0, 8, 31])
-def test_slice_merge_and_its_fallback(monkeypatch, splits):
-    """Eight kv heads of one sequence, every range of a pair resident (the grid fits the
-    CUs): each range merges one slice of the output once all have arrived.  With
-    HKV_DECODE_MERGE_WAIT_TICKS=0 a range stops waiting at its first poll that does not
-    find every range arrived, and the last arrival merges every slice instead.  Both paths
-    against the oracle on one workspace, alternating, so that each launch starts from the
-    counters the previous one left; the error word stays clear."""
+def test_slice_merge_and_its_fallback(monkeypatch, splits, hq, hkv, handoff):
+    """One sequence, every range of a pair resident (the grid fits the CUs): each range
+    merges one slice of the output once all have arrived.  Eight kv heads take the
+    XCD-local hand-off (atomics and loads in the XCD's L2) unless the workspace asks for
+    the device-scope one; four kv heads (a pair's ranges on two XCDs) always take the
+    device-scope one.  With HKV_DECODE_MERGE_WAIT_TICKS=0 a range stops waiting at its
+    first poll that does not find every range arrived, and the last arrival merges every
+    slice instead.  Both paths against the oracle on one workspace, alternating, so that
+    each launch starts from the counters the previous one left; the error word stays
+    clear."""
     from heterokv import ops
-    print("case: slice merge, B=1 32/8, 64 + 8000 + 1000, splits=%d" % splits, flush=True)
-    c = Case(16, 1, 32, 8, 64, [8000], [1000])
+    print("case: slice merge, B=1 %d/%d, 64 + 8000 + 1000, splits=%d, agent_handoff=%s" % (hq, hkv, splits, handoff),
+          flush=True)
+    c = Case(16, 1, hq, hkv, 64, [8000], [1000])
     ref = c.oracle()
-    ws = ops.DecodeWorkspace(DEV)
+    ws = ops.DecodeWorkspace(DEV, agent_handoff=handoff)
     for wait in ("0", None, "0", None, "0", "0", None):
         if wait is None:
             monkeypatch.delenv("HKV_DECODE_MERGE_WAIT_TICKS", raising=False)
