@@ -205,15 +205,17 @@ def test_slice_merge_and_its_fallback(monkeypatch, splits, hq, hkv, handoff):
         assert ws.error_flag() == 0
 
 
-def test_decode_beside_a_concurrent_kernel():
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (28, 4)])
+def test_decode_beside_a_concurrent_kernel(hq, hkv):
     """Decode launches while GEMMs on another stream hold many CUs, so the ranges of a pair
     need not all be resident at once: the slice merge's bounded wait hands the merge to the
-    last arrival when ranges give up waiting.  Outputs stay within the bound, the
+    last arrival when ranges give up waiting.  Eight kv heads merge in the XCD's L2, four
+    (a pair's ranges on two XCDs) at device scope.  Outputs stay within the bound, the
     placement check stays clear (the error word is zero), and the other stream is still
     busy when each decode has finished."""
     from heterokv import ops
-    print("case: decode beside a concurrent GEMM stream, B=1 32/8, 64 + 8000 + 1000", flush=True)
-    c = Case(16, 1, 32, 8, 64, [8000], [1000])
+    print("case: decode beside a concurrent GEMM stream, B=1 %d/%d, 64 + 8000 + 1000" % (hq, hkv), flush=True)
+    c = Case(16, 1, hq, hkv, 64, [8000], [1000])
     ref = c.oracle()
     ws = ops.DecodeWorkspace(DEV)
     side = torch.cuda.Stream(device=DEV)          # default priority
