@@ -925,6 +925,18 @@ def leg_c5(torch, args, timed=8, warm=2):
         win["h2d_bytes_per_token"] = (st[-1]["bytes_h2d"] - b0) // max(timed, 1)
         win["window_chunks"] = int(mgr._adaptive_controller.stats["current_w"])
         out["windowed"] = win
+        # the same two retrievals with each step replayed from a HIP graph (DecodeGraph: each
+        # layer's host runs gathered from the pinned arena by a kernel captured before its
+        # decode kernel)
+        for name, window in (("windowed_graph", "adaptive"), ("full_graph", None)):
+            cache.retrieval_window = window
+            runner = DecodeGraph(model, cache)
+            tok, pos, _, _ = _decode_tokens_graph(torch, runner, tok, pos, max(warm, 3), dev)
+            tok, pos, tm, _ = _decode_tokens_graph(torch, runner, tok, pos, timed, dev)
+            out[name] = _summ(tm, [])
+            runner.close()
+            del runner
+        cache.retrieval_window = "adaptive"
         # host -> HBM copy rate of one layer's records on the side stream
         pf, st0 = mgr._pf, mgr._layers[0]
         rb = st0.n_host * mgr._staging[0].record_bytes
@@ -945,6 +957,8 @@ def leg_c5(torch, args, timed=8, warm=2):
                        "chunks, sink 64 + recent 4096 fp16, INT4 middle with 75% of its 16-token blocks in pinned "
                        "host memory, batch 1, greedy",
            "full_tok_per_s": full["tok_per_s"], "windowed_tok_per_s": win["tok_per_s"],
+           "full_graph_tok_per_s": out["full_graph"]["tok_per_s"],
+           "windowed_graph_tok_per_s": out["windowed_graph"]["tok_per_s"],
            "full_stall_ms_per_token": full["prefetch_stall_ms_per_token"],
            "windowed_stall_ms_per_token": win["prefetch_stall_ms_per_token"],
            "h2d_gbs_one_layer_copy": round(h2d_gbs, 2), "pcie_gen5_x16_gbs": PCIE_GEN5_X16_GBS,
@@ -958,7 +972,7 @@ def leg_c5(torch, args, timed=8, warm=2):
            # on its hardware) counts the 128K prefill plus 64 decode tokens in its wall time
            "wall_tok_per_s_prefill_plus_64_tokens": {
                k: round(64.0 / (prefill_s + 64 * out[k]["ms_per_token"] * 1e-3), 3)
-               for k in ("full", "windowed", "resident_graph")},
+               for k in ("full", "windowed", "full_graph", "windowed_graph", "resident_graph")},
            "variants": out,
            # full retrieval moves every host record over PCIe per token: its bound is the link,
            # priced at the PCIe Gen5 x16 rate (and at this box's measured one-layer copy rate)

@@ -402,9 +402,16 @@ class DecodeGraph:
     replays.  The returned logits live in the graph's memory pool and are overwritten
     by the next step.
 
-    Not for caches whose decode step does host work that has no graph form: a host
-    tier (records copied in on a side stream), a retrieval window, attention tracking.
-    The INT4 tier may not change while the graph lives (decode never adds to it)."""
+    A host tier's copies join the graph (HeteroKVManager.begin_graph_staging): each
+    staged layer's host runs are gathered from the pinned arena by a kernel captured
+    before the layer's decode kernel, in stream order, with nothing overlapping them; it
+    suits a retrieval window (a few chunks per layer), while full retrieval runs faster
+    eagerly, where the native side stream overlaps the copies with compute.  With a retrieval window the chunk selection is made on the
+    host before every step, as an eager step makes it; a step whose selection differs
+    from the captured one drops the graph and captures again.  Not for caches whose
+    decode step does host work that has no graph form: attention tracking, adaptive
+    self-healing.  The INT4 tier may not change while the graph lives (decode never adds
+    to it)."""
 
     def __init__(self, model, cache: FusedHeteroCache):
         if not cache.fused_decode:
@@ -417,20 +424,37 @@ class DecodeGraph:
         self.steps = 0
         self._ids = self._pos = self._logits = None
         self._int4 = None
+        self._sels = None
+        self._staging = False
 
     def _check(self):
         mgr = self.cache._manager
         if mgr is None:
             raise HeteroKVError(-1, "DecodeGraph: prefill the cache before decoding")
-        if mgr.retrieval_window is not None:
-            raise HeteroKVError(-4, "DecodeGraph: a retrieval window selects chunks on the host per step")
-        if any(st is not None and st.n_host > 0 for st in mgr._layers):
-            raise HeteroKVError(-4, "DecodeGraph: a host tier copies records in on a side stream per step")
         int4 = [0 if st is None else st.int4_len for st in mgr._layers]
         if self._int4 is not None and int4 != self._int4:
             raise HeteroKVError(-1, "DecodeGraph: the INT4 tier changed since the graph was captured")
         self._int4 = int4
         return mgr
+
+    def _select(self, mgr):
+        """This step's chunk selection of every layer (None without a retrieval window),
+        made on the host once per layer as an eager step makes it and left for
+        attend_decode; the window block tables are built here, outside any capture."""
+        if mgr.retrieval_window is None:
+            return None
+        sels = []
+        for li, st in enumerate(mgr._layers):
+            sel = mgr._selection(li) if st is not None and st.int4_len else None
+            if sel is not None:
+                mgr._window_table(li, st, sel)
+            sels.append(sel)
+        return tuple(sels)
+
+    def _drop(self):
+        torch.cuda.synchronize()
+        self.graph = None
+        self._logits = None
 
     def _forward(self, ids, pos):
         return self.model(input_ids=ids, position_ids=pos, past_key_values=self.cache, use_cache=True).logits
@@ -450,12 +474,19 @@ class DecodeGraph:
     def step(self, input_ids: torch.Tensor, position_ids: torch.Tensor) -> torch.Tensor:
         """input_ids, position_ids: [B, 1] on the cache's device; returns logits [B, 1, vocab]."""
         mgr = self._check()
+        sels = self._select(mgr)
+        if self.graph is not None and sels != self._sels:
+            self._drop()              # another chunk selection: capture again
         if self.steps == 0:
             mgr.enable_device_decode(True)
             out = self._forward(input_ids, position_ids)
         elif self.graph is None:
             self._ids = input_ids.clone()
             self._pos = position_ids.clone()
+            self._sels = sels
+            if any(st is not None and st.n_host > 0 for st in mgr._layers):
+                mgr.begin_graph_staging()
+                self._staging = True
             g = torch.cuda.CUDAGraph()
             # capturing runs the step's host logic once (the host state advances here);
             # its kernels run at the first replay
@@ -481,6 +512,7 @@ class DecodeGraph:
             self._ids.copy_(input_ids)
             self._pos.copy_(position_ids)
             self._advance_host(mgr)
+            mgr._selection_of.clear()     # read by the captured step, not again by a replay
             self.graph.replay()
             err.post()
             out = self._logits
@@ -488,10 +520,13 @@ class DecodeGraph:
         return out
 
     def close(self) -> None:
-        """Drop the graph and return the manager to host-stepped decode."""
-        self.graph = None
-        self._logits = None
+        """Drop the graph and return the manager to host-stepped decode (and a host tier
+        to the native prefetch schedule)."""
+        self._drop()
         if self.cache._manager is not None:
+            if self._staging:
+                self.cache._manager.end_graph_staging()
+                self._staging = False
             self.cache._manager.enable_device_decode(False)
 
 

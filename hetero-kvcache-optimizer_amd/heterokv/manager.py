@@ -238,6 +238,10 @@ class HeteroKVManager:
         self._pending: Dict[int, Tuple[int, Any, int]] = {}
         self._slot_parity: Dict[int, int] = {}
         self._waited: List[int] = []
+        # host-tier copies of a decode step under graph capture (begin_graph_staging):
+        # gather kernels on the capturing stream instead of the native side stream
+        self._graph_staging = False
+        self._graph_ids: Optional[torch.Tensor] = None
         self._selection_of: Dict[int, Any] = {}
         self._window_tables: Dict[Any, Tuple[torch.Tensor, int]] = {}
         self._selection_b: Dict[int, List[str]] = {}
@@ -1009,6 +1013,48 @@ class HeteroKVManager:
                 self._submit(j, sel, avoid_buf)
             return
 
+    # ------------------------------------------------- host tier under graph capture
+    def begin_graph_staging(self) -> None:
+        """Make the host-tier copies of the next captured decode step part of the graph.
+
+        The native prefetcher's side stream and events cannot join a capture, so while
+        this is on, attend_decode under capture gathers each staged layer's host runs from
+        the pinned arena (hipHostMalloc memory is device-accessible) into staging buffer 0
+        with the block-gather kernel, on the capturing stream right before the layer's
+        decode kernel.  Stream order keeps the next layer's gather behind this layer's
+        kernel.  A forked stream gains nothing here: the replayed graph ran its branches one
+        after the other, and its host-side launch took 3.3 ms instead of well under one.
+        Captured host-to-device memcpy nodes were slower than the kernel.  The eager
+        schedule's pending copies are dropped first (the graph rewrites its buffer)."""
+        if self._pf is not None:
+            self._pf.synchronize()
+        torch.cuda.current_stream(self.device).synchronize()
+        self._pending.clear()
+        self._buf_owner = [-1] * len(self._staging)
+        n = max([st.n_host for st in self._layers if st is not None] + [1])
+        if self._graph_ids is None or self._graph_ids.numel() < n:
+            self._graph_ids = torch.arange(n, dtype=torch.int32, device=self.device)
+        self._graph_staging = True
+
+    def end_graph_staging(self) -> None:
+        """Back to the native prefetch schedule (after every replay has finished)."""
+        torch.cuda.synchronize(self.device)
+        self._graph_staging = False
+
+    def _graph_stage(self, layer_idx: int, sel) -> int:
+        """Under capture: gather layer_idx's host runs into staging buffer 0 on the current
+        stream; returns the buffer."""
+        st = self._layers[layer_idx]
+        rb = ops.record_bytes(st.H)
+        dst = self._staging[0]
+        sp = _lib.stream_ptr(self.device)
+        for k0, k1 in self._host_runs(st, sel):
+            _lib.check(_lib.load().hkv_gather_blocks(self._pf.host_ptr(st.host_off + k0 * rb), k1 - k0, None, 0,
+                                                     self._graph_ids.data_ptr(), k1 - k0, rb,
+                                                     dst.data[k0].data_ptr(), dst.err.data_ptr(), sp),
+                       "hkv_gather_blocks")
+        return 0
+
     def prefetch_stats(self, reset: bool = True) -> Dict[str, Any]:
         """Stall of every layer that waited for host records since the last call: per layer
         max(0, t(copies done) - t(kernel needs them)) in ms (synchronizes on those events,
@@ -1068,14 +1114,18 @@ class HeteroKVManager:
                 bt, n4 = self._window_table(layer_idx, st, sel)
         staged = n4 > 0 and st.n_host > 0 and bool(self._host_runs(st, sel))
         buf = slot = None
-        if staged:
+        graph_staged = capturing and self._graph_staging
+        if graph_staged:
+            if staged:
+                buf = self._graph_stage(layer_idx, sel)
+        elif staged:
             p = self._pending.get(layer_idx)
             if p is None or p[1] != sel:
                 p = self._submit(layer_idx, sel)
             buf, _, slot = p
-        if self._pf is not None and self.enable_prefetch:
+        if self._pf is not None and self.enable_prefetch and not graph_staged:
             self._prefetch_after(layer_idx, buf)
-        if staged:
+        if staged and not graph_staged:
             self._pf.wait(slot)
         q = query_states
         scores = stats = None
@@ -1093,7 +1143,7 @@ class HeteroKVManager:
         if feed_oracle:
             w = ops.attn_weights(scores[:1], stats[:1], order=self._score_order(st, n4))
             self.update_attention_scores(w[0])
-        if staged:
+        if staged and not graph_staged:
             self._pf.mark(slot)
             self._pending.pop(layer_idx, None)
             self._waited.append(slot)

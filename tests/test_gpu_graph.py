@@ -210,3 +210,55 @@ def test_decode_graph_reports_replay_errors():
         out = runner.step(tok, torch.tensor([[304]], device=DEV))   # captures again
         assert torch.isfinite(out).all() and runner.graph is not None
     runner.close()
+
+
+@pytest.mark.parametrize("window", [None, 2, "switch"])
+def test_decode_graph_with_host_tier(window):
+    """75% of the INT4 blocks in pinned host memory: graph replays (the host runs' copies
+    captured on a forked stream) give the eager steps' logits, with full retrieval, with a
+    two-chunk window, and across a window change (the graph is captured again); after
+    close() the native prefetch schedule serves an eager step again."""
+    print("case: DecodeGraph with a host tier, window=%s" % window, flush=True)
+    from heterokv.engine_wrapper import ChunkedPrefillEngine, DecodeGraph, FusedHeteroCache
+    model = _tiny_qwen2()
+    prompt, steps = 700, 12
+    ids = torch.randint(0, 512, (1, prompt), generator=torch.Generator().manual_seed(3)).to(DEV)
+    caches = []
+    for _ in range(2):
+        c = FusedHeteroCache(num_layers=2, sink_tokens=16, keep_tail=80, chunk_size=64, device=DEV)
+        c._ensure_manager(0)._heavyhitter_budget = 8
+        c._manager.deterministic_decode = True
+        caches.append(c)
+    cache_e, cache_g = caches
+    runner = DecodeGraph(model, cache_g)
+    graphs = set()
+    with torch.inference_mode():
+        for c in caches:
+            ChunkedPrefillEngine(model, c, chunk_size=64).prefill(ids)
+            assert c.offload_to_host(0.75, seed=0) > 0
+            c.retrieval_window = 2 if window == "switch" else window
+        tok = ids[:, -1:]
+        worst = 0.0
+        for step in range(steps):
+            if window == "switch" and step == steps // 2:
+                for c in caches:
+                    c.retrieval_window = 3
+            p = torch.tensor([[prompt + step]], device=DEV)
+            le = model(input_ids=tok, past_key_values=cache_e, position_ids=p, use_cache=True).logits
+            lg = runner.step(tok, p)
+            assert torch.isfinite(lg).all()
+            err = (le.float() - lg.float()).abs().max().item()
+            worst = max(worst, err)
+            assert err < 5e-2, (step, err)
+            if runner.graph is not None:
+                graphs.add(id(runner.graph))
+            tok = le[:, -1:].argmax(-1)
+        print("  max |logit diff| %.3e over %d steps, %d graph(s)" % (worst, steps, len(graphs)), flush=True)
+        assert len(graphs) == (2 if window == "switch" else 1)
+        runner.close()
+        p = torch.tensor([[prompt + steps]], device=DEV)
+        le = model(input_ids=tok, past_key_values=cache_e, position_ids=p, use_cache=True).logits
+        lg = model(input_ids=tok, past_key_values=cache_g, position_ids=p, use_cache=True).logits
+        assert (le.float() - lg.float()).abs().max().item() < 5e-2
+    cache_e.check_errors()
+    cache_g.check_errors()
